@@ -1,0 +1,55 @@
+/* Internal definitions shared by the nmx HIP translation units (not part of the ABI). */
+#ifndef NMX_INTERNAL_H
+#define NMX_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "nmx.h"
+
+struct nmx_ctx {
+    int device;
+    hipStream_t stream;
+    char name[256];
+    char err[1024];
+    int capturing;
+};
+
+struct nmx_event {
+    hipEvent_t ev;
+};
+
+struct nmx_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+/* Record an error message on ctx; always returns -1. */
+int nmx_fail(nmx_ctx *ctx, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+/* Map a HIP status to -1 + message. */
+#define NMX_HIP(ctx, call)                                                                  \
+    do {                                                                                    \
+        hipError_t e_ = (call);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return nmx_fail((ctx), "%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, \
+                            __LINE__);                                                      \
+    } while (0)
+
+/* Launch-error check after a kernel launch (hipGetLastError). */
+#define NMX_LAUNCHED(ctx, what)                                                             \
+    do {                                                                                    \
+        hipError_t e_ = hipGetLastError();                                                  \
+        if (e_ != hipSuccess) return nmx_fail((ctx), "%s launch: %s", what, hipGetErrorString(e_)); \
+    } while (0)
+
+/* [a, a + na) and [b, b + nb) overlap (byte ranges). */
+static inline bool nmx_overlap(const void *a, size_t na, const void *b, size_t nb) {
+    const char *pa = (const char *)a, *pb = (const char *)b;
+    return na && nb && pa < pb + nb && pb < pa + na;
+}
+
+#endif

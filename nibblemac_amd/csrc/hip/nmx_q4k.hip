@@ -1,0 +1,290 @@
+/* Q4K_G32 x A8 matvec / small-batch matmul and A8 activation quantization for gfx950.
+ *
+ * Exactness contract (the reference's kern_q4k, engine/src/kern_quant.c:148-245): for every
+ * output row r and vector v the fp32 accumulator runs over the 32-column blocks in column
+ * order, acc = fma((float)dot, (D*s)*d_v, acc); acc = fma(-(M*m), fsum_v, acc), with dot the
+ * exact int32 sum of 32 nibble x int8 products. The integer part may be computed in any order;
+ * the float chain may not, so one lane owns one (row, vector) chain.
+ *
+ * Mapping (one wave64 = 64 consecutive rows = 16 four-row tiles of the native .pq layout):
+ *   - lane l reads its row's 16-byte code chunk of block k (bytes 64 + 64k + 16i of the
+ *     superblock, i = row % 4): the 4 lanes of a tile read one contiguous 64-byte run, a wave
+ *     16 runs per instruction, and over the 8 blocks of a superblock every byte of the tile's
+ *     576-byte superblock is consumed once (128-bit loads, no repack);
+ *   - every lane of a wave works on the same column block at the same time, so the A8
+ *     activations (32 int8 + d + fsum per vector) are wave-uniform and are read with scalar
+ *     loads into SGPRs, shared by all 64 rows; the integer dot is 8 v_dot4_i32_i8 per vector;
+ *   - the 6-bit sub-scales / sub-mins of the lane's row are decoded from the 64-byte scale line
+ *     once per superblock.
+ * Several matrices that share one input run in one launch (segment table). */
+#include "nmx_internal.h"
+
+namespace {
+
+constexpr int SB_BYTES = 576;
+constexpr int MAX_NV = 8; /* vectors per register pass */
+
+struct Seg {
+    const uint8_t *W;
+    float *Y;
+    int rows;
+    int ystride;
+    int wave0; /* first global wave of this matrix */
+    int pad;
+};
+
+struct SegTable {
+    Seg s[NMX_MAX_SEGS];
+    int count;
+    int total_waves;
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    const unsigned short b = (unsigned short)h;
+    _Float16 f;
+    __builtin_memcpy(&f, &b, 2);
+    return (float)f;
+}
+
+/* 6-bit values s[4k + i], k = 0..7, of one row i from a packed array (engine/FORMAT.md: 16 B
+ * of low nibbles, then 8 B of high bit pairs): L0..L3 the low-nibble dwords, H0/H1 the
+ * high-pair dwords, sh8 = 8 * i. */
+__device__ __forceinline__ void decode6(uint32_t L0, uint32_t L1, uint32_t L2, uint32_t L3,
+                                        uint32_t H0, uint32_t H1, int sh8, int out[8]) {
+    const uint32_t b0 = (L0 >> sh8) & 0xffu, b1 = (L1 >> sh8) & 0xffu;
+    const uint32_t b2 = (L2 >> sh8) & 0xffu, b3 = (L3 >> sh8) & 0xffu;
+    const uint32_t h0 = (H0 >> sh8) & 0xffu, h1 = (H1 >> sh8) & 0xffu;
+    const uint32_t lo[8] = {b0 & 15u, b1 & 15u, b2 & 15u, b3 & 15u,
+                            b0 >> 4, b1 >> 4, b2 >> 4, b3 >> 4};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t h = (k & 1) ? h1 : h0;
+        out[k] = (int)(lo[k] | (((h >> (2 * (k >> 1))) & 3u) << 4));
+    }
+}
+
+template <int NV, bool DOTS>
+__global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, int v0,
+                                                const int8_t *__restrict__ q,
+                                                const float *__restrict__ d,
+                                                const float *__restrict__ fs,
+                                                int32_t *__restrict__ dots) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wave >= tab.total_waves) return;
+    const int lane = threadIdx.x & 63;
+
+    /* segment of this wave (uniform) */
+    const uint8_t *W = tab.s[0].W;
+    float *Y = tab.s[0].Y;
+    int rows = tab.s[0].rows, ystride = tab.s[0].ystride, wave0 = tab.s[0].wave0;
+#pragma unroll
+    for (int t = 1; t < NMX_MAX_SEGS; t++)
+        if (t < tab.count && wave >= tab.s[t].wave0) {
+            W = tab.s[t].W;
+            Y = tab.s[t].Y;
+            rows = tab.s[t].rows;
+            ystride = tab.s[t].ystride;
+            wave0 = tab.s[t].wave0;
+        }
+
+    const int row_raw = (wave - wave0) * 64 + lane;
+    const bool valid = row_raw < rows;
+    const int row = valid ? row_raw : rows - 1; /* clamped: the wave stays convergent */
+    const int i = row & 3, sh8 = 8 * i;
+    const int nsb = cols >> 8, nb = cols >> 5;
+    const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * nsb * SB_BYTES);
+
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) acc[v] = 0.0f;
+
+    for (int sb = 0; sb < nsb; sb++) {
+        const uint4 *p = tp + sb * (SB_BYTES / 16);
+        const uint4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+        uint4 c[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = p[4 + 4 * k + i];
+
+        const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
+        const float D = half_bits_to_float(dw >> (16 * (i & 1)));
+        const float M = half_bits_to_float(mw >> (16 * (i & 1)));
+        int s6[8], m6[8];
+        decode6(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, s6);
+        decode6(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, m6);
+
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
+            const float of = M * (float)m6[k];
+            const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
+            const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
+            const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
+            const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
+            const int blk = sb * 8 + k;
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const size_t ai = (size_t)blk * n + v0 + v;
+                const int *xa = (const int *)(q + ai * 32);
+                int dot = __builtin_amdgcn_sdot4(lo0, xa[0], 0, false);
+                dot = __builtin_amdgcn_sdot4(lo1, xa[1], dot, false);
+                dot = __builtin_amdgcn_sdot4(lo2, xa[2], dot, false);
+                dot = __builtin_amdgcn_sdot4(lo3, xa[3], dot, false);
+                dot = __builtin_amdgcn_sdot4(hi0, xa[4], dot, false);
+                dot = __builtin_amdgcn_sdot4(hi1, xa[5], dot, false);
+                dot = __builtin_amdgcn_sdot4(hi2, xa[6], dot, false);
+                dot = __builtin_amdgcn_sdot4(hi3, xa[7], dot, false);
+                acc[v] = __builtin_fmaf((float)dot, sc * d[ai], acc[v]);
+                acc[v] = __builtin_fmaf(-of, fs[ai], acc[v]);
+                if (DOTS && valid) dots[((size_t)(v0 + v) * rows + row) * nb + blk] = dot;
+            }
+        }
+    }
+    if (valid) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) Y[(size_t)(v0 + v) * ystride + row] = acc[v];
+    }
+}
+
+/* A8 quantization, one 32-lane half-wave per (block b, vector v) unit; unit index = b * n + v,
+ * which is the block-major output index (engine/src/kern.h:19-27). Cross-lane max of |x| and
+ * the int sum are exact in any order; 127 / amax and amax / 127 are IEEE divides; the code is
+ * round-half-even (engine/src/kern_act.c:14-42, engine/metal/kernels.metal:9-27). */
+__global__ __launch_bounds__(256) void quant_a8_k(const float *__restrict__ X, int n, int cols,
+                                                  int8_t *__restrict__ q, float *__restrict__ d,
+                                                  float *__restrict__ fs) {
+    const int unit = (blockIdx.x * 256 + threadIdx.x) >> 5, j = threadIdx.x & 31;
+    const int nb = cols >> 5;
+    const bool live = unit < nb * n;
+    const int u = live ? unit : 0;
+    const int b = u / n, v = u - b * n;
+    const float x = X[(size_t)v * cols + b * 32 + j];
+    float amax = fabsf(x);
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const int c = (int)rintf(x * id);
+    int sum = c;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
+    if (!live) return;
+    q[(size_t)u * 32 + j] = (int8_t)(c > 127 ? 127 : c < -128 ? -128 : c);
+    if (j == 0) {
+        const float dd = amax / 127.0f;
+        d[u] = dd;
+        fs[u] = dd * (float)sum;
+    }
+}
+
+template <int NV>
+void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
+               const float *d, const float *fs, int32_t *dots) {
+    const unsigned blocks = (unsigned)((tab.total_waves + 3) / 4);
+    if (dots) q4k_mv_k<NV, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots);
+    else q4k_mv_k<NV, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots);
+}
+
+int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *q,
+                  const float *d, const float *fs, int32_t *dots) {
+    /* n vectors in ceil(n / MAX_NV) passes of equal size (+-1), larger first, like the
+     * reference's VECTOR_PASSES (engine/src/kern_quant.c:258-274): every pass performs the same
+     * per-vector operations, so the result does not depend on the split. */
+    for (int v = 0; v < n;) {
+        const int left = n - v, np = (left + MAX_NV - 1) / MAX_NV, nv = (left + np - 1) / np;
+        switch (nv) {
+        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        }
+        NMX_LAUNCHED(ctx, "q4k_mv");
+        v += nv;
+    }
+    return 0;
+}
+
+size_t q4k_bytes(int rows, int cols) {
+    return (size_t)(rows / 4) * (size_t)(cols / 256) * SB_BYTES;
+}
+
+} // namespace
+
+extern "C" {
+
+int nmx_quant_a8(nmx_ctx *ctx, const float *X, int n, int cols, int8_t *q, float *d,
+                 float *fsum) {
+    if (!ctx) return -1;
+    if (!X || !q || !d || !fsum) return nmx_fail(ctx, "nmx_quant_a8: NULL pointer");
+    if (n < 1 || n > 4096 || cols < 32 || cols % 32 || cols > (1 << 20))
+        return nmx_fail(ctx, "nmx_quant_a8: bad shape n=%d cols=%d", n, cols);
+    const size_t xb = (size_t)n * cols * 4, qb = (size_t)n * cols, fb = (size_t)n * (cols / 32) * 4;
+    if (nmx_overlap(q, qb, X, xb) || nmx_overlap(d, fb, X, xb) || nmx_overlap(fsum, fb, X, xb) ||
+        nmx_overlap(q, qb, d, fb) || nmx_overlap(q, qb, fsum, fb) || nmx_overlap(d, fb, fsum, fb))
+        return nmx_fail(ctx, "nmx_quant_a8: aliased buffers");
+    const size_t units = (size_t)n * (cols / 32);
+    const unsigned blocks = (unsigned)((units + 7) / 8);
+    quant_a8_k<<<blocks, 256, 0, ctx->stream>>>(X, n, cols, q, d, fsum);
+    NMX_LAUNCHED(ctx, "quant_a8");
+    return 0;
+}
+
+int nmx_q4k_matmul_multi(nmx_ctx *ctx, int count, const void *const *W, const int *rows,
+                         float *const *Y, const int *y_stride, int cols, int n,
+                         const int8_t *q, const float *d, const float *fsum) {
+    if (!ctx) return -1;
+    if (count < 1 || count > NMX_MAX_SEGS || !W || !rows || !Y || !y_stride)
+        return nmx_fail(ctx, "nmx_q4k_matmul_multi: bad segment list (count=%d)", count);
+    if (!q || !d || !fsum) return nmx_fail(ctx, "nmx_q4k_matmul: NULL activation pointer");
+    if (cols <= 0 || cols % 256 || cols > 65536 || n < 1 || n > 64)
+        return nmx_fail(ctx, "nmx_q4k_matmul: bad shape cols=%d n=%d", cols, n);
+    const size_t qb = (size_t)n * cols, fb = (size_t)n * (cols / 32) * 4;
+    SegTable tab = {};
+    tab.count = count;
+    int waves = 0;
+    for (int s = 0; s < count; s++) {
+        if (!W[s] || !Y[s]) return nmx_fail(ctx, "nmx_q4k_matmul: NULL matrix %d", s);
+        if (rows[s] <= 0 || rows[s] % 4 || rows[s] > (1 << 22) || y_stride[s] < rows[s])
+            return nmx_fail(ctx, "nmx_q4k_matmul: bad rows=%d y_stride=%d (matrix %d)", rows[s],
+                            y_stride[s], s);
+        const size_t wb = q4k_bytes(rows[s], cols), yb = ((size_t)(n - 1) * y_stride[s] + rows[s]) * 4;
+        if (nmx_overlap(Y[s], yb, W[s], wb) || nmx_overlap(Y[s], yb, q, qb) ||
+            nmx_overlap(Y[s], yb, d, fb) || nmx_overlap(Y[s], yb, fsum, fb))
+            return nmx_fail(ctx, "nmx_q4k_matmul: output %d aliases an input", s);
+        tab.s[s] = Seg{(const uint8_t *)W[s], Y[s], rows[s], y_stride[s], waves, 0};
+        waves += (rows[s] + 63) / 64;
+    }
+    tab.total_waves = waves;
+    return launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr);
+}
+
+int nmx_q4k_matmul(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                   const float *d, const float *fsum, float *Y, int y_stride, int32_t *dots) {
+    if (!ctx) return -1;
+    if (!W || !Y || !q || !d || !fsum) return nmx_fail(ctx, "nmx_q4k_matmul: NULL pointer");
+    if (rows <= 0 || rows % 4 || rows > (1 << 22) || cols <= 0 || cols % 256 || cols > 65536 ||
+        n < 1 || n > 64 || y_stride < rows)
+        return nmx_fail(ctx, "nmx_q4k_matmul: bad shape rows=%d cols=%d n=%d y_stride=%d", rows,
+                        cols, n, y_stride);
+    const size_t wb = q4k_bytes(rows, cols), qb = (size_t)n * cols, fb = (size_t)n * (cols / 32) * 4;
+    const size_t yb = ((size_t)(n - 1) * y_stride + rows) * 4;
+    if (nmx_overlap(Y, yb, W, wb) || nmx_overlap(Y, yb, q, qb) || nmx_overlap(Y, yb, d, fb) ||
+        nmx_overlap(Y, yb, fsum, fb))
+        return nmx_fail(ctx, "nmx_q4k_matmul: output aliases an input");
+    if (dots) {
+        const size_t db = (size_t)n * rows * (cols / 32) * 4;
+        if (nmx_overlap(dots, db, Y, yb) || nmx_overlap(dots, db, W, wb) ||
+            nmx_overlap(dots, db, q, qb) || nmx_overlap(dots, db, d, fb) ||
+            nmx_overlap(dots, db, fsum, fb))
+            return nmx_fail(ctx, "nmx_q4k_matmul: dots aliases a buffer");
+    }
+    SegTable tab = {};
+    tab.count = 1;
+    tab.s[0] = Seg{(const uint8_t *)W, Y, rows, y_stride, 0, 0};
+    tab.total_waves = (rows + 63) / 64;
+    return launch_passes(ctx, tab, cols, n, q, d, fsum, dots);
+}
+
+} /* extern "C" */

@@ -1,0 +1,231 @@
+"""ctypes binding of libnmx.so (include/nmx.h): the MI355X device layer.
+
+Used by the Python tests and bench.py; the C host engine (libpinfer.so) links the same library
+directly. There is no fallback: if libnmx.so is missing or no GPU is present the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB_DIR = Path(__file__).resolve().parent / "lib"
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+_fp = ctypes.POINTER(ctypes.c_float)
+
+NMX_MAX_SEGS = 6
+
+
+class NmxError(RuntimeError):
+    pass
+
+
+_SIGS: dict[str, tuple[object, list[object]]] = {
+    "nmx_create": (_vp, [_i]),
+    "nmx_create_error": (ctypes.c_char_p, []),
+    "nmx_destroy": (None, [_vp]),
+    "nmx_error": (ctypes.c_char_p, [_vp]),
+    "nmx_device_name": (ctypes.c_char_p, [_vp]),
+    "nmx_device_count": (_i, []),
+    "nmx_alloc": (_vp, [_vp, _sz]),
+    "nmx_free": (_i, [_vp, _vp]),
+    "nmx_upload": (_i, [_vp, _vp, _vp, _sz]),
+    "nmx_download": (_i, [_vp, _vp, _vp, _sz]),
+    "nmx_copy_d2d": (_i, [_vp, _vp, _vp, _sz]),
+    "nmx_fill_zero": (_i, [_vp, _vp, _sz]),
+    "nmx_sync": (_i, [_vp]),
+    "nmx_event_create": (_vp, [_vp]),
+    "nmx_event_destroy": (None, [_vp]),
+    "nmx_event_record": (_i, [_vp, _vp]),
+    "nmx_event_elapsed_ms": (_i, [_vp, _vp, _vp, _fp]),
+    "nmx_graph_begin": (_i, [_vp]),
+    "nmx_graph_end": (_vp, [_vp]),
+    "nmx_graph_launch": (_i, [_vp, _vp]),
+    "nmx_graph_destroy": (None, [_vp]),
+    "nmx_quant_a8": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "nmx_q4k_matmul": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]),
+    "nmx_q4k_matmul_multi": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    return LIB_DIR / "libnmx.so"
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libnmx.so from the package (built by nibblemac_amd.build); raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.exists():
+        raise NmxError(f"{path} is missing: run `python -m nibblemac_amd.build` first")
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGS)
+
+
+class Buffer:
+    """A device allocation: pointer, size, and an optional numpy dtype/shape."""
+
+    def __init__(self, dev: "Device", ptr: int, nbytes: int, dtype=None, shape=None):
+        self.dev, self.ptr, self.nbytes = dev, ptr, nbytes
+        self.dtype, self.shape = dtype, shape
+
+    def offset(self, nbytes: int) -> int:
+        return self.ptr + nbytes
+
+    def numpy(self) -> np.ndarray:
+        return self.dev.download(self, self.dtype, self.shape)
+
+    def free(self) -> None:
+        if self.ptr:
+            self.dev.free(self)
+            self.ptr = 0
+
+
+class Device:
+    """One nmx context (device + stream)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        self.ctx = self.lib.nmx_create(device)
+        if not self.ctx:
+            raise NmxError(self.lib.nmx_create_error().decode())
+        self._bufs: list[Buffer] = []
+
+    # ---- errors / lifetime
+    def check(self, rc: int, what: str = "nmx call") -> None:
+        if rc != 0:
+            raise NmxError(f"{what}: {self.lib.nmx_error(self.ctx).decode()}")
+
+    @property
+    def name(self) -> str:
+        return self.lib.nmx_device_name(self.ctx).decode()
+
+    def close(self) -> None:
+        if self.ctx:
+            for b in self._bufs:
+                if b.ptr:
+                    self.lib.nmx_free(self.ctx, b.ptr)
+                    b.ptr = 0
+            self.lib.nmx_destroy(self.ctx)
+            self.ctx = None
+
+    def __enter__(self) -> "Device":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    # ---- memory
+    def alloc(self, nbytes: int, dtype=None, shape=None) -> Buffer:
+        p = self.lib.nmx_alloc(self.ctx, max(int(nbytes), 1))
+        if not p:
+            raise NmxError(f"nmx_alloc({nbytes}): {self.lib.nmx_error(self.ctx).decode()}")
+        b = Buffer(self, p, int(nbytes), dtype, shape)
+        self._bufs.append(b)
+        return b
+
+    def empty(self, shape, dtype) -> Buffer:
+        dt = np.dtype(dtype)
+        shape = tuple(int(s) for s in np.atleast_1d(shape)) if not isinstance(shape, tuple) else shape
+        return self.alloc(int(np.prod(shape)) * dt.itemsize, dt, shape)
+
+    def zeros(self, shape, dtype) -> Buffer:
+        b = self.empty(shape, dtype)
+        self.check(self.lib.nmx_fill_zero(self.ctx, b.ptr, b.nbytes), "fill_zero")
+        return b
+
+    def to_device(self, arr: np.ndarray) -> Buffer:
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(arr.nbytes, arr.dtype, arr.shape)
+        if arr.nbytes:
+            self.check(self.lib.nmx_upload(self.ctx, b.ptr, arr.ctypes.data, arr.nbytes), "upload")
+        return b
+
+    def upload(self, b: Buffer, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= b.nbytes
+        self.check(self.lib.nmx_upload(self.ctx, b.ptr, arr.ctypes.data, arr.nbytes), "upload")
+
+    def download(self, b: Buffer, dtype=None, shape=None) -> np.ndarray:
+        dtype = np.dtype(dtype if dtype is not None else b.dtype)
+        shape = shape if shape is not None else b.shape
+        out = np.empty(shape, dtype)
+        self.check(self.lib.nmx_download(self.ctx, out.ctypes.data, b.ptr, out.nbytes), "download")
+        return out
+
+    def free(self, b: Buffer) -> None:
+        self.check(self.lib.nmx_free(self.ctx, b.ptr), "free")
+
+    def sync(self) -> None:
+        self.check(self.lib.nmx_sync(self.ctx), "sync")
+
+    # ---- timing / graphs
+    def event(self) -> int:
+        e = self.lib.nmx_event_create(self.ctx)
+        if not e:
+            raise NmxError("event create failed")
+        return e
+
+    def record(self, ev: int) -> None:
+        self.check(self.lib.nmx_event_record(self.ctx, ev), "event record")
+
+    def elapsed_ms(self, e0: int, e1: int) -> float:
+        ms = ctypes.c_float()
+        self.check(self.lib.nmx_event_elapsed_ms(self.ctx, e0, e1, ctypes.byref(ms)), "elapsed")
+        return float(ms.value)
+
+    def graph_begin(self) -> None:
+        self.check(self.lib.nmx_graph_begin(self.ctx), "graph begin")
+
+    def graph_end(self) -> int:
+        g = self.lib.nmx_graph_end(self.ctx)
+        if not g:
+            raise NmxError(f"graph end: {self.lib.nmx_error(self.ctx).decode()}")
+        return g
+
+    def graph_launch(self, g: int) -> None:
+        self.check(self.lib.nmx_graph_launch(self.ctx, g), "graph launch")
+
+    # ---- kernels
+    def quant_a8(self, X: Buffer | int, n: int, cols: int, q: Buffer | int, d: Buffer | int,
+                 fs: Buffer | int) -> None:
+        self.check(self.lib.nmx_quant_a8(self.ctx, _p(X), n, cols, _p(q), _p(d), _p(fs)),
+                   "quant_a8")
+
+    def q4k_matmul(self, W, rows: int, cols: int, n: int, q, d, fs, Y, y_stride: int | None = None,
+                   dots=None) -> None:
+        self.check(self.lib.nmx_q4k_matmul(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
+                                           _p(Y), y_stride or rows, _p(dots) if dots else None),
+                   "q4k_matmul")
+
+    def q4k_matmul_multi(self, Ws, rows, Ys, y_strides, cols: int, n: int, q, d, fs) -> None:
+        c = len(Ws)
+        w = (ctypes.c_void_p * c)(*[_p(x) for x in Ws])
+        r = (ctypes.c_int * c)(*rows)
+        y = (ctypes.c_void_p * c)(*[_p(x) for x in Ys])
+        s = (ctypes.c_int * c)(*y_strides)
+        self.check(self.lib.nmx_q4k_matmul_multi(self.ctx, c, w, r, y, s, cols, n, _p(q), _p(d),
+                                                 _p(fs)), "q4k_matmul_multi")
+
+
+def _p(x) -> int | None:
+    if x is None:
+        return None
+    return x.ptr if isinstance(x, Buffer) else int(x)
