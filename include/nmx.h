@@ -85,6 +85,49 @@ int nmx_q4k_matmul_multi(nmx_ctx *ctx, int count, const void *const *W, const in
                          float *const *Y, const int *y_stride, int cols, int n,
                          const int8_t *q, const float *d, const float *fsum);
 
+/* ---- Gated DeltaNet recurrence with the speculative rollback log -------------------------
+ * Replaces pf_lin_rule / pf_lin_apply (engine/src/ops.h:54-93, matvec_ref.c:140-188,
+ * kern_lin.c:155-185) and nm_metal_lin_rule / _apply (engine/metal/metal.h:66-71).
+ * S: [heads][dv][dk] fp32 in HBM (column-major per head; the layout is private to this
+ * contract, zero = reset). qkv [n][qkv_stride] = q | k (heads/rep heads of dk) | v (heads x dv);
+ * decay, beta [n][heads]; o [n][o_stride]. log [n][heads][dk + dv + 1] = k | delta | decay.
+ * log == NULL: plain pass, S advances by all n tokens.
+ * log != NULL, log0 == 0 (the reference's logged pass): S advances by token 0 only; rows
+ *   t >= 1 are logged (row 0 untouched); commit keeps e >= 1 tokens.
+ * log != NULL, log0 == 1 (extension): S is left after the pending updates, every row 0..n-1 is
+ *   logged, so any prefix 0..n can be committed by replay.
+ * keep > 0: S first advances by the keep rows of pend ([keep][heads][dk + dv + 1]), with the
+ *   replay arithmetic (row = row * decay; row = row + k_i * delta_j).
+ * dk in {32, 64, 128, 256}; dv <= 1024; n <= 64; keep <= 64. */
+typedef struct {
+    int n, heads, rep, dk, dv;
+    int qkv_stride, o_stride;
+    const float *qkv;
+    const float *decay, *beta;
+    float *S;
+    float *o;
+    float *log;
+    const float *pend;
+    int keep;
+    int log0;
+} nmx_lin_args;
+int nmx_lin_rule(nmx_ctx *ctx, const nmx_lin_args *a);
+/* S advances by the first `keep` rows of log (the commit replay). */
+int nmx_lin_apply(nmx_ctx *ctx, float *S, const float *log, int keep, int heads, int dk, int dv);
+
+/* ---- LM head fused with greedy argmax and draft acceptance -------------------------------
+ * Replaces the verify tail of pf_spec_decode: pf_matmul(head, k+1 rows) (engine/src/forward.c:
+ * 142-143), pinfer_argmax per row (forward_ops.c:387-409) and the acceptance loop
+ * (engine/src/spec.c:340-345). W is the Q4K head [rows][cols]; A8 inputs for n = k + 1 rows.
+ * logits (may be NULL) receives [n][rows] fp32. drafts [k] int32 on the device: the draft for
+ * row t + 1. out [2 + n] int32 on the device: out[0] = a (accepted drafts), out[1] = bonus =
+ * argmax(row a), out[2 + t] = argmax(row t) (first index of the maximum). work: device scratch
+ * of nmx_head_work_bytes(rows, n) bytes. k = 0 is a plain greedy step (out[1] = argmax). */
+size_t nmx_head_work_bytes(int rows, int n);
+int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                    const float *d, const float *fsum, float *logits, const int32_t *drafts,
+                    void *work, int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,12 +63,17 @@ __device__ __forceinline__ void decode6(uint32_t L0, uint32_t L1, uint32_t L2, u
     }
 }
 
-template <int NV, bool DOTS>
+/* AMAX: also reduce the wave's 64 rows to (max value, first index) per vector and write the
+ * partial to amax_v / amax_i [n][total_waves] (the head's fused greedy argmax); Y may then be
+ * NULL (logits not materialised). */
+template <int NV, bool DOTS, bool AMAX>
 __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, int v0,
                                                 const int8_t *__restrict__ q,
                                                 const float *__restrict__ d,
                                                 const float *__restrict__ fs,
-                                                int32_t *__restrict__ dots) {
+                                                int32_t *__restrict__ dots,
+                                                float *__restrict__ amax_v,
+                                                int *__restrict__ amax_i) {
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (wave >= tab.total_waves) return;
     const int lane = threadIdx.x & 63;
@@ -139,9 +144,178 @@ __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, i
             }
         }
     }
-    if (valid) {
+    if (valid && Y) {
 #pragma unroll
         for (int v = 0; v < NV; v++) Y[(size_t)(v0 + v) * ystride + row] = acc[v];
+    }
+    if (AMAX) {
+        /* (value, index) order: larger value first, then the smaller index, so the winner is
+         * the first index whose value equals the maximum (engine/src/forward_ops.c:387-409;
+         * -0 == +0 compare equal, finite logits assumed as in the reference). */
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            float bv = valid ? acc[v] : -INFINITY;
+            int bi = valid ? row : 0x7fffffff;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off);
+                const int oi = __shfl_xor(bi, off);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (lane == 0) {
+                amax_v[(size_t)(v0 + v) * tab.total_waves + wave] = bv;
+                amax_i[(size_t)(v0 + v) * tab.total_waves + wave] = bi;
+            }
+        }
+    }
+}
+
+/* Final argmax of every row from the per-wave partials, then the acceptance loop of the
+ * reference (engine/src/spec.c:340-345): a = 0; g = argmax(row 0); while a < k and
+ * drafts[a] == g: a++, g = argmax(row a). out = [a, g, argmax(row 0..n-1)]. One workgroup. */
+__global__ __launch_bounds__(256) void head_accept_k(const float *__restrict__ amax_v,
+                                                     const int *__restrict__ amax_i, int waves,
+                                                     int n, const int32_t *__restrict__ drafts,
+                                                     int32_t *__restrict__ out) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    __shared__ int am[64];
+    const int tid = threadIdx.x;
+    for (int t = 0; t < n; t++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int w = tid; w < waves; w += 256) {
+            const float ov = amax_v[(size_t)t * waves + w];
+            const int oi = amax_i[(size_t)t * waves + w];
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        sv[tid] = bv;
+        si[tid] = bi;
+        __syncthreads();
+        for (int st = 128; st >= 1; st >>= 1) {
+            if (tid < st) {
+                const float ov = sv[tid + st];
+                const int oi = si[tid + st];
+                if (ov > sv[tid] || (ov == sv[tid] && oi < si[tid])) {
+                    sv[tid] = ov;
+                    si[tid] = oi;
+                }
+            }
+            __syncthreads();
+        }
+        if (tid == 0) am[t] = si[0];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        int a = 0, g = am[0];
+        while (a < n - 1 && drafts[a] == g) {
+            a++;
+            g = am[a];
+        }
+        out[0] = a;
+        out[1] = g;
+        for (int t = 0; t < n; t++) out[2 + t] = am[t];
+    }
+}
+
+/* K-split variant for matrices with few rows (the per-layer projections): a workgroup owns
+ * 64 rows x ONE vector and KS waves split the superblocks (SBW each). Every wave computes its
+ * blocks' int dots with the same wave-uniform activations and keeps (float)dot, (D*s)*d and
+ * -(M*m) in registers; then the fp32 chain runs wave 0 -> 1 -> ... -> KS-1 in column order, the
+ * running accumulator handed over through LDS, so the per-(row, vector) operation sequence is
+ * exactly the reference's. Grid: (64-row groups over all segments) x vectors. */
+template <int SBW, bool DOTS>
+__global__ __launch_bounds__(1024) void q4k_mv_ks_k(SegTable tab, int cols, int n, int KS,
+                                                   const int8_t *__restrict__ q,
+                                                   const float *__restrict__ d,
+                                                   const float *__restrict__ fs,
+                                                   int32_t *__restrict__ dots) {
+    __shared__ float hand[64];
+    const int grp = blockIdx.x, v = blockIdx.y;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+    const uint8_t *W = tab.s[0].W;
+    float *Y = tab.s[0].Y;
+    int rows = tab.s[0].rows, ystride = tab.s[0].ystride, grp0 = tab.s[0].wave0;
+#pragma unroll
+    for (int t = 1; t < NMX_MAX_SEGS; t++)
+        if (t < tab.count && grp >= tab.s[t].wave0) {
+            W = tab.s[t].W;
+            Y = tab.s[t].Y;
+            rows = tab.s[t].rows;
+            ystride = tab.s[t].ystride;
+            grp0 = tab.s[t].wave0;
+        }
+    const int row_raw = (grp - grp0) * 64 + lane;
+    const bool valid = row_raw < rows;
+    const int row = valid ? row_raw : rows - 1;
+    const int i = row & 3, sh8 = 8 * i;
+    const int nsb = cols >> 8, nb = cols >> 5;
+    const int sb0 = w * SBW;
+    const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * nsb * SB_BYTES);
+
+    float tf[SBW * 8], tm[SBW * 8], to[SBW * 8], tfs[SBW * 8];
+#pragma unroll
+    for (int u = 0; u < SBW; u++) {
+        const int sb = sb0 + u;
+        if (sb >= nsb) { /* uniform: a short last wave */
+#pragma unroll
+            for (int k = 0; k < 8; k++) tf[u * 8 + k] = tm[u * 8 + k] = to[u * 8 + k] = tfs[u * 8 + k] = 0.0f;
+            continue;
+        }
+        const uint4 *p = tp + sb * (SB_BYTES / 16);
+        const uint4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+        uint4 c[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = p[4 + 4 * k + i];
+        const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
+        const float D = half_bits_to_float(dw >> (16 * (i & 1)));
+        const float M = half_bits_to_float(mw >> (16 * (i & 1)));
+        int s6[8], m6[8];
+        decode6(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, s6);
+        decode6(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, m6);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int blk = sb * 8 + k;
+            const size_t ai = (size_t)blk * n + v;
+            const int *xa = (const int *)(q + ai * 32);
+            int dot = __builtin_amdgcn_sdot4((int)(c[k].x & 0x0f0f0f0fu), xa[0], 0, false);
+            dot = __builtin_amdgcn_sdot4((int)(c[k].y & 0x0f0f0f0fu), xa[1], dot, false);
+            dot = __builtin_amdgcn_sdot4((int)(c[k].z & 0x0f0f0f0fu), xa[2], dot, false);
+            dot = __builtin_amdgcn_sdot4((int)(c[k].w & 0x0f0f0f0fu), xa[3], dot, false);
+            dot = __builtin_amdgcn_sdot4((int)((c[k].x >> 4) & 0x0f0f0f0fu), xa[4], dot, false);
+            dot = __builtin_amdgcn_sdot4((int)((c[k].y >> 4) & 0x0f0f0f0fu), xa[5], dot, false);
+            dot = __builtin_amdgcn_sdot4((int)((c[k].z >> 4) & 0x0f0f0f0fu), xa[6], dot, false);
+            dot = __builtin_amdgcn_sdot4((int)((c[k].w >> 4) & 0x0f0f0f0fu), xa[7], dot, false);
+            if (DOTS && valid) dots[((size_t)v * rows + row) * nb + blk] = dot;
+            tf[u * 8 + k] = (float)dot;
+            tm[u * 8 + k] = (D * (float)s6[k]) * d[ai];
+            to[u * 8 + k] = -(M * (float)m6[k]);
+            tfs[u * 8 + k] = fs[ai];
+        }
+    }
+
+    float acc = 0.0f;
+    for (int turn = 0; turn < KS; turn++) {
+        if (turn == w) {
+            if (w > 0) acc = hand[lane];
+#pragma unroll
+            for (int j = 0; j < SBW * 8; j++) {
+                if (sb0 + j / 8 < nsb) {
+                    acc = __builtin_fmaf(tf[j], tm[j], acc);
+                    acc = __builtin_fmaf(to[j], tfs[j], acc);
+                }
+            }
+            if (w + 1 < KS) hand[lane] = acc;
+            else if (valid) Y[(size_t)v * ystride + row] = acc;
+        }
+        __syncthreads();
     }
 }
 
@@ -177,28 +351,56 @@ __global__ __launch_bounds__(256) void quant_a8_k(const float *__restrict__ X, i
 
 template <int NV>
 void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
-               const float *d, const float *fs, int32_t *dots) {
+               const float *d, const float *fs, int32_t *dots, float *amv, int *ami) {
     const unsigned blocks = (unsigned)((tab.total_waves + 3) / 4);
-    if (dots) q4k_mv_k<NV, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots);
-    else q4k_mv_k<NV, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots);
+    if (amv) q4k_mv_k<NV, false, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, amv, ami);
+    else if (dots) q4k_mv_k<NV, true, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, amv, ami);
+    else q4k_mv_k<NV, false, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, amv, ami);
+}
+
+/* Rows below which the K-split kernel is used (few waves in the row-per-lane kernel). */
+constexpr int KSPLIT_MAX_ROWS = 32768;
+
+int launch_ksplit(nmx_ctx *ctx, const SegTable &tab, int total_rows_groups, int cols, int n,
+                  const int8_t *q, const float *d, const float *fs, int32_t *dots) {
+    const int nsb = cols >> 8;
+    const int sbw = nsb <= 8 ? 1 : 2;
+    const int KS = (nsb + sbw - 1) / sbw;
+    if (KS > 16) return nmx_fail(ctx, "q4k K-split: cols=%d too large", cols);
+    dim3 grid((unsigned)total_rows_groups, (unsigned)n);
+    dim3 block((unsigned)(64 * KS));
+    if (sbw == 1) {
+        if (dots) q4k_mv_ks_k<1, true><<<grid, block, 0, ctx->stream>>>(tab, cols, n, KS, q, d, fs, dots);
+        else q4k_mv_ks_k<1, false><<<grid, block, 0, ctx->stream>>>(tab, cols, n, KS, q, d, fs, dots);
+    } else {
+        if (dots) q4k_mv_ks_k<2, true><<<grid, block, 0, ctx->stream>>>(tab, cols, n, KS, q, d, fs, dots);
+        else q4k_mv_ks_k<2, false><<<grid, block, 0, ctx->stream>>>(tab, cols, n, KS, q, d, fs, dots);
+    }
+    NMX_LAUNCHED(ctx, "q4k_mv_ks");
+    return 0;
 }
 
 int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *q,
-                  const float *d, const float *fs, int32_t *dots) {
+                  const float *d, const float *fs, int32_t *dots, float *amv = nullptr,
+                  int *ami = nullptr) {
+    int total_rows = 0;
+    for (int s = 0; s < tab.count; s++) total_rows += tab.s[s].rows;
+    if (!amv && total_rows < KSPLIT_MAX_ROWS && cols <= 16 * 2 * 256)
+        return launch_ksplit(ctx, tab, tab.total_waves, cols, n, q, d, fs, dots);
     /* n vectors in ceil(n / MAX_NV) passes of equal size (+-1), larger first, like the
      * reference's VECTOR_PASSES (engine/src/kern_quant.c:258-274): every pass performs the same
      * per-vector operations, so the result does not depend on the split. */
     for (int v = 0; v < n;) {
         const int left = n - v, np = (left + MAX_NV - 1) / MAX_NV, nv = (left + np - 1) / np;
         switch (nv) {
-        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
-        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots); break;
+        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
         }
         NMX_LAUNCHED(ctx, "q4k_mv");
         v += nv;
@@ -285,6 +487,42 @@ int nmx_q4k_matmul(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const
     tab.s[0] = Seg{(const uint8_t *)W, Y, rows, y_stride, 0, 0};
     tab.total_waves = (rows + 63) / 64;
     return launch_passes(ctx, tab, cols, n, q, d, fsum, dots);
+}
+
+size_t nmx_head_work_bytes(int rows, int n) {
+    if (rows <= 0 || n <= 0) return 0;
+    return (size_t)n * (size_t)((rows + 63) / 64) * 8;
+}
+
+int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                    const float *d, const float *fsum, float *logits, const int32_t *drafts,
+                    void *work, int32_t *out) {
+    if (!ctx) return -1;
+    if (!W || !q || !d || !fsum || !work || !out || (n > 1 && !drafts))
+        return nmx_fail(ctx, "nmx_head_accept: NULL pointer");
+    if (rows <= 0 || rows % 4 || rows > (1 << 22) || cols <= 0 || cols % 256 || cols > 65536 ||
+        n < 1 || n > 64)
+        return nmx_fail(ctx, "nmx_head_accept: bad shape rows=%d cols=%d n=%d", rows, cols, n);
+    const size_t wb = q4k_bytes(rows, cols), qb = (size_t)n * cols, fb = (size_t)n * (cols / 32) * 4;
+    const size_t lb = (size_t)n * rows * 4, kb = nmx_head_work_bytes(rows, n);
+    const size_t ob = (size_t)(2 + n) * 4;
+    if (logits && (nmx_overlap(logits, lb, W, wb) || nmx_overlap(logits, lb, q, qb) ||
+                   nmx_overlap(logits, lb, d, fb) || nmx_overlap(logits, lb, fsum, fb) ||
+                   nmx_overlap(logits, lb, work, kb) || nmx_overlap(logits, lb, out, ob)))
+        return nmx_fail(ctx, "nmx_head_accept: logits alias another buffer");
+    if (nmx_overlap(work, kb, W, wb) || nmx_overlap(work, kb, q, qb) || nmx_overlap(work, kb, out, ob) ||
+        nmx_overlap(out, ob, W, wb) || nmx_overlap(out, ob, q, qb))
+        return nmx_fail(ctx, "nmx_head_accept: work/out alias another buffer");
+    SegTable tab = {};
+    tab.count = 1;
+    tab.s[0] = Seg{(const uint8_t *)W, logits, rows, rows, 0, 0};
+    tab.total_waves = (rows + 63) / 64;
+    float *amv = (float *)work;
+    int *ami = (int *)((char *)work + (size_t)n * tab.total_waves * 4);
+    if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, amv, ami)) return -1;
+    head_accept_k<<<1, 256, 0, ctx->stream>>>(amv, ami, tab.total_waves, n, drafts, out);
+    NMX_LAUNCHED(ctx, "head_accept");
+    return 0;
 }
 
 } /* extern "C" */

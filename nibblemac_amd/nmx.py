@@ -24,6 +24,15 @@ class NmxError(RuntimeError):
     pass
 
 
+class LinArgs(ctypes.Structure):
+    """Mirror of nmx_lin_args (include/nmx.h)."""
+
+    _fields_ = [("n", _i), ("heads", _i), ("rep", _i), ("dk", _i), ("dv", _i),
+                ("qkv_stride", _i), ("o_stride", _i), ("qkv", _vp), ("decay", _vp),
+                ("beta", _vp), ("S", _vp), ("o", _vp), ("log", _vp), ("pend", _vp),
+                ("keep", _i), ("log0", _i)]
+
+
 _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_create": (_vp, [_i]),
     "nmx_create_error": (ctypes.c_char_p, []),
@@ -49,6 +58,10 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_quant_a8": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "nmx_q4k_matmul": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]),
     "nmx_q4k_matmul_multi": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "nmx_lin_rule": (_i, [_vp, ctypes.POINTER(LinArgs)]),
+    "nmx_lin_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "nmx_head_work_bytes": (_sz, [_i, _i]),
+    "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -223,6 +236,26 @@ class Device:
         s = (ctypes.c_int * c)(*y_strides)
         self.check(self.lib.nmx_q4k_matmul_multi(self.ctx, c, w, r, y, s, cols, n, _p(q), _p(d),
                                                  _p(fs)), "q4k_matmul_multi")
+
+
+    def lin_rule(self, *, n, heads, rep, dk, dv, qkv_stride, o_stride, qkv, decay, beta, S, o,
+                 log=None, pend=None, keep=0, log0=False) -> None:
+        a = LinArgs(n, heads, rep, dk, dv, qkv_stride, o_stride, _p(qkv), _p(decay), _p(beta),
+                    _p(S), _p(o), _p(log), _p(pend), keep, int(log0))
+        self.check(self.lib.nmx_lin_rule(self.ctx, ctypes.byref(a)), "lin_rule")
+
+    def lin_apply(self, S, log, keep: int, heads: int, dk: int, dv: int) -> None:
+        self.check(self.lib.nmx_lin_apply(self.ctx, _p(S), _p(log), keep, heads, dk, dv),
+                   "lin_apply")
+
+    def head_work_bytes(self, rows: int, n: int) -> int:
+        return int(self.lib.nmx_head_work_bytes(rows, n))
+
+    def head_accept(self, W, rows: int, cols: int, n: int, q, d, fs, logits, drafts, work,
+                    out) -> None:
+        self.check(self.lib.nmx_head_accept(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
+                                            _p(logits), _p(drafts), _p(work), _p(out)),
+                   "head_accept")
 
 
 def _p(x) -> int | None:

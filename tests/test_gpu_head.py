@@ -1,0 +1,120 @@
+"""GPU parity: LM head (Q4K matvec over k + 1 rows) fused with greedy argmax and draft
+acceptance (libnmx.so nmx_head_accept) against the oracle.
+
+Bar: logits bit-exact, every argmax and the accepted count / bonus token identical
+(engine/src/spec.c:340-345, engine/src/forward_ops.c:387-409).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def quantized_head(rng, rows, cols, chunk=16384):
+    out = np.empty(oracle.q4k_nbytes(rows, cols), np.uint8)
+    per = oracle.q4k_nbytes(4, cols) // 4
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        w = (rng.standard_normal((r1 - r0, cols), dtype=np.float32) * np.float32(0.02))
+        out[r0 * per:r1 * per] = oracle.q4k_quantize(w)
+    return out
+
+
+def planted_drafts(argmax_rows, a, k):
+    """Drafts d_1..d_k with exactly a accepted: d_t = argmax(row t-1) for t <= a, then a draft
+    that differs from argmax(row a)."""
+    d = np.zeros(k, np.int32)
+    for t in range(k):
+        d[t] = argmax_rows[t] if t < a else (argmax_rows[t] + 1 + t) % 1000003
+    return d
+
+
+def run_head(dev, W, rows, cols, X, drafts, logits=True):
+    n = X.shape[0]
+    q, d, fs = oracle.quant_a8(X)
+    dW, dq, dd, dfs = dev.to_device(W), dev.to_device(q), dev.to_device(d), dev.to_device(fs)
+    dl = dev.zeros((n, rows), np.float32) if logits else None
+    ddr = dev.to_device(np.asarray(drafts, np.int32)) if n > 1 else None
+    work = dev.alloc(dev.head_work_bytes(rows, n))
+    out = dev.zeros(2 + n, np.int32)
+    dev.head_accept(dW, rows, cols, n, dq, dd, dfs, dl, ddr, work, out)
+    dev.sync()
+    res = out.numpy(), (dl.numpy() if logits else None)
+    for b in (dW, dq, dd, dfs, dl, ddr, work, out):
+        if b is not None:
+            b.free()
+    return res
+
+
+_CONFIG4: dict = {}
+
+
+def config4_case():
+    """248320 x 1024 Q4K head (N(0, 0.02) quantized) and 5 rows N(0, 1), built once."""
+    if not _CONFIG4:
+        rng = np.random.default_rng(40)
+        rows, cols = 248320, 1024
+        W = quantized_head(rng, rows, cols)
+        X = rng.standard_normal((5, cols)).astype(np.float32)
+        q, d, fs = oracle.quant_a8(X)
+        _CONFIG4.update(W=W, X=X, ref=oracle.q4k_matmul(W, rows, cols, q, d, fs, 5, threads=8))
+    return _CONFIG4["W"], _CONFIG4["X"], _CONFIG4["ref"]
+
+
+@pytest.mark.parametrize("accept", [0, 2, 4])
+def test_config4_head_accept(dev, accept):
+    """The config-4 head with 4 planted drafts at 0 / 50 / 100 % acceptance."""
+    print(f"[case] config4 head accept={accept}", flush=True)
+    rows, cols = 248320, 1024
+    W, X, ref = config4_case()
+    am = np.array([oracle.argmax(ref[t]) for t in range(5)], np.int32)
+    drafts = planted_drafts(am, accept, 4)
+    a_ref, bonus_ref, rows_ref = oracle.accept(ref, drafts)
+    assert a_ref == accept
+    out, logits = run_head(dev, W, rows, cols, X, drafts)
+    assert np.array_equal(logits.view(np.uint32), ref.view(np.uint32)), "logits differ"
+    assert out[0] == a_ref and out[1] == bonus_ref, (out[:2], a_ref, bonus_ref)
+    assert np.array_equal(out[2:], rows_ref)
+
+
+def test_head_ties_pick_first_index(dev):
+    """Duplicate tiles give equal logits: the first index of the maximum wins, across waves."""
+    rng = np.random.default_rng(41)
+    rows, cols = 8192, 512
+    W = quantized_head(rng, rows, cols)
+    per = oracle.q4k_nbytes(4, cols)
+    Y0 = oracle.q4k_matmul(W, rows, cols, *oracle.quant_a8(np.ones((1, cols), np.float32)), 1)
+    best = int(np.argmax(Y0[0])) // 4
+    for dst in (best + 1, best + 700, rows // 4 - 1):  # same wave, another wave, the last tile
+        if dst < rows // 4:
+            W[dst * per:(dst + 1) * per] = W[best * per:(best + 1) * per]
+    X = np.ones((3, cols), np.float32)
+    X[1] *= -1
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, 3)
+    am = [oracle.argmax(ref[t]) for t in range(3)]
+    out, logits = run_head(dev, W, rows, cols, X, np.array([am[0], am[1]], np.int32))
+    assert np.array_equal(logits.view(np.uint32), ref.view(np.uint32))
+    assert list(out[2:]) == am
+    assert out[0] == 2 and out[1] == am[2]
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 9])
+def test_head_widths_and_no_logits(dev, n):
+    """Any verify width (k = n - 1, plain step at n = 1), logits optional."""
+    rng = np.random.default_rng(42 + n)
+    rows, cols = 32768, 1024
+    W = quantized_head(rng, rows, cols)
+    X = rng.standard_normal((n, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, n)
+    am = np.array([oracle.argmax(ref[t]) for t in range(n)], np.int32)
+    drafts = planted_drafts(am, n // 2, n - 1) if n > 1 else np.zeros(0, np.int32)
+    a_ref, bonus_ref, _ = oracle.accept(ref, drafts)
+    out, _ = run_head(dev, W, rows, cols, X, drafts, logits=False)
+    assert out[0] == a_ref and out[1] == bonus_ref
+    assert np.array_equal(out[2:], am)
