@@ -63,19 +63,29 @@ __device__ __forceinline__ void decode6(uint32_t L0, uint32_t L1, uint32_t L2, u
     }
 }
 
-/* AMAX: also reduce the wave's 64 rows to (max value, first index) per vector and write the
- * partial to amax_v / amax_i [n][total_waves] (the head's fused greedy argmax); Y may then be
- * NULL (logits not materialised). */
+/* 64-bit argmax key: high word = the value's bits made order-preserving as unsigned (-0 folded
+ * into +0 so equal values tie), low word = ~index (a smaller index wins among equal values). */
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    const float c = v == 0.0f ? 0.0f : v;
+    uint32_t u = __float_as_uint(c);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+
+/* AMAX: also reduce to one (max value, first index) key per vector and workgroup (the head's
+ * fused greedy argmax, finished by head_finish_k); Y may then be NULL (logits not
+ * materialised). */
 template <int NV, bool DOTS, bool AMAX>
 __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, int v0,
                                                 const int8_t *__restrict__ q,
                                                 const float *__restrict__ d,
                                                 const float *__restrict__ fs,
                                                 int32_t *__restrict__ dots,
-                                                float *__restrict__ amax_v,
-                                                int *__restrict__ amax_i) {
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wave >= tab.total_waves) return;
+                                                unsigned long long *__restrict__ amax_key) {
+    const int wave_raw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (!AMAX && wave_raw >= tab.total_waves) return;
+    const bool wave_live = wave_raw < tab.total_waves;
+    const int wave = wave_live ? wave_raw : tab.total_waves - 1;
     const int lane = threadIdx.x & 63;
 
     /* segment of this wave (uniform) */
@@ -93,8 +103,8 @@ __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, i
         }
 
     const int row_raw = (wave - wave0) * 64 + lane;
-    const bool valid = row_raw < rows;
-    const int row = valid ? row_raw : rows - 1; /* clamped: the wave stays convergent */
+    const bool valid = wave_live && row_raw < rows;
+    const int row = row_raw < rows ? row_raw : rows - 1; /* clamped: the wave stays convergent */
     const int i = row & 3, sh8 = 8 * i;
     const int nsb = cols >> 8, nb = cols >> 5;
     const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * nsb * SB_BYTES);
@@ -151,65 +161,69 @@ __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, i
     if (AMAX) {
         /* (value, index) order: larger value first, then the smaller index, so the winner is
          * the first index whose value equals the maximum (engine/src/forward_ops.c:387-409;
-         * -0 == +0 compare equal, finite logits assumed as in the reference). */
+         * -0 == +0 compare equal, finite logits assumed as in the reference). Keys: 64-bit
+         * (order-preserving value bits, complemented index), so the order is an unsigned max.
+         * Per wave (shuffles), then per workgroup (LDS): one partial key per (vector,
+         * workgroup), plain stores; head_finish_k reduces them after the kernel boundary. */
+        __shared__ unsigned long long wkeys[4][MAX_NV];
+        const int wv = threadIdx.x >> 6;
 #pragma unroll
         for (int v = 0; v < NV; v++) {
-            float bv = valid ? acc[v] : -INFINITY;
-            int bi = valid ? row : 0x7fffffff;
+            unsigned long long key = valid ? argmax_key(acc[v], row) : 0ull;
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const int oi = __shfl_xor(bi, off);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
+                const unsigned long long o = __shfl_xor(key, off);
+                key = o > key ? o : key;
             }
-            if (lane == 0) {
-                amax_v[(size_t)(v0 + v) * tab.total_waves + wave] = bv;
-                amax_i[(size_t)(v0 + v) * tab.total_waves + wave] = bi;
-            }
+            if (lane == 0) wkeys[wv][v] = key;
+        }
+        __syncthreads();
+        if (threadIdx.x < NV) {
+            unsigned long long key = wkeys[0][threadIdx.x];
+            for (int w = 1; w < 4; w++) key = wkeys[w][threadIdx.x] > key ? wkeys[w][threadIdx.x] : key;
+            amax_key[(size_t)(v0 + threadIdx.x) * gridDim.x + blockIdx.x] = key;
         }
     }
 }
 
-/* Final argmax of every row from the per-wave partials, then the acceptance loop of the
+/* Argmax of every row from the per-workgroup partial keys, then the acceptance loop of the
  * reference (engine/src/spec.c:340-345): a = 0; g = argmax(row 0); while a < k and
- * drafts[a] == g: a++, g = argmax(row a). out = [a, g, argmax(row 0..n-1)]. One workgroup. */
-__global__ __launch_bounds__(256) void head_accept_k(const float *__restrict__ amax_v,
-                                                     const int *__restrict__ amax_i, int waves,
-                                                     int n, const int32_t *__restrict__ drafts,
-                                                     int32_t *__restrict__ out) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
+ * drafts[a] == g: a++, g = argmax(row a). out = [a, g, argmax(row 0..n-1)]. One workgroup of
+ * 1024 threads; every partial is loaded once, all loads issued before the reduction. */
+__global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *__restrict__ keys,
+                                                      int nblk, int n,
+                                                      const int32_t *__restrict__ drafts,
+                                                      int32_t *__restrict__ out) {
+    __shared__ unsigned long long red[16][8];
     __shared__ int am[64];
-    const int tid = threadIdx.x;
-    for (int t = 0; t < n; t++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int w = tid; w < waves; w += 256) {
-            const float ov = amax_v[(size_t)t * waves + w];
-            const int oi = amax_i[(size_t)t * waves + w];
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        sv[tid] = bv;
-        si[tid] = bi;
-        __syncthreads();
-        for (int st = 128; st >= 1; st >>= 1) {
-            if (tid < st) {
-                const float ov = sv[tid + st];
-                const int oi = si[tid + st];
-                if (ov > sv[tid] || (ov == sv[tid] && oi < si[tid])) {
-                    sv[tid] = ov;
-                    si[tid] = oi;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int t0 = 0; t0 < n; t0 += 8) {
+        unsigned long long k[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) k[j] = 0ull;
+        for (int b = tid; b < nblk; b += 1024) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (t0 + j < n) {
+                    const unsigned long long o = keys[(size_t)(t0 + j) * nblk + b];
+                    k[j] = o > k[j] ? o : k[j];
                 }
-            }
-            __syncthreads();
         }
-        if (tid == 0) am[t] = si[0];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const unsigned long long o = __shfl_xor(k[j], off);
+                k[j] = o > k[j] ? o : k[j];
+            }
+            if (lane == 0) red[wv][j] = k[j];
+        }
+        __syncthreads();
+        if (tid < 8 && t0 + tid < n) {
+            unsigned long long m = red[0][tid];
+            for (int w = 1; w < 16; w++) m = red[w][tid] > m ? red[w][tid] : m;
+            am[t0 + tid] = (int)(0xffffffffu - (unsigned)(m & 0xffffffffull));
+        }
         __syncthreads();
     }
     if (tid == 0) {
@@ -351,11 +365,11 @@ __global__ __launch_bounds__(256) void quant_a8_k(const float *__restrict__ X, i
 
 template <int NV>
 void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
-               const float *d, const float *fs, int32_t *dots, float *amv, int *ami) {
+               const float *d, const float *fs, int32_t *dots, unsigned long long *am) {
     const unsigned blocks = (unsigned)((tab.total_waves + 3) / 4);
-    if (amv) q4k_mv_k<NV, false, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, amv, ami);
-    else if (dots) q4k_mv_k<NV, true, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, amv, ami);
-    else q4k_mv_k<NV, false, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, amv, ami);
+    if (am) q4k_mv_k<NV, false, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
+    else if (dots) q4k_mv_k<NV, true, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
+    else q4k_mv_k<NV, false, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
 }
 
 /* Rows below which the K-split kernel is used (few waves in the row-per-lane kernel). */
@@ -381,11 +395,10 @@ int launch_ksplit(nmx_ctx *ctx, const SegTable &tab, int total_rows_groups, int 
 }
 
 int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *q,
-                  const float *d, const float *fs, int32_t *dots, float *amv = nullptr,
-                  int *ami = nullptr) {
+                  const float *d, const float *fs, int32_t *dots, unsigned long long *am = nullptr) {
     int total_rows = 0;
     for (int s = 0; s < tab.count; s++) total_rows += tab.s[s].rows;
-    if (!amv && total_rows < KSPLIT_MAX_ROWS && cols <= 16 * 2 * 256)
+    if (!am && total_rows < KSPLIT_MAX_ROWS && cols <= 16 * 2 * 256)
         return launch_ksplit(ctx, tab, tab.total_waves, cols, n, q, d, fs, dots);
     /* n vectors in ceil(n / MAX_NV) passes of equal size (+-1), larger first, like the
      * reference's VECTOR_PASSES (engine/src/kern_quant.c:258-274): every pass performs the same
@@ -393,14 +406,14 @@ int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8
     for (int v = 0; v < n;) {
         const int left = n - v, np = (left + MAX_NV - 1) / MAX_NV, nv = (left + np - 1) / np;
         switch (nv) {
-        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
-        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, amv, ami); break;
+        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
         }
         NMX_LAUNCHED(ctx, "q4k_mv");
         v += nv;
@@ -491,7 +504,8 @@ int nmx_q4k_matmul(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const
 
 size_t nmx_head_work_bytes(int rows, int n) {
     if (rows <= 0 || n <= 0) return 0;
-    return (size_t)n * (size_t)((rows + 63) / 64) * 8;
+    const size_t blocks = (size_t)((rows + 63) / 64 + 3) / 4;
+    return (size_t)n * blocks * 8; /* [n][workgroups] partial argmax keys */
 }
 
 int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
@@ -517,11 +531,12 @@ int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, cons
     tab.count = 1;
     tab.s[0] = Seg{(const uint8_t *)W, logits, rows, rows, 0, 0};
     tab.total_waves = (rows + 63) / 64;
-    float *amv = (float *)work;
-    int *ami = (int *)((char *)work + (size_t)n * tab.total_waves * 4);
-    if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, amv, ami)) return -1;
-    head_accept_k<<<1, 256, 0, ctx->stream>>>(amv, ami, tab.total_waves, n, drafts, out);
-    NMX_LAUNCHED(ctx, "head_accept");
+    if ((uintptr_t)work % 8) return nmx_fail(ctx, "nmx_head_accept: work not 8-byte aligned");
+    const int blocks = (tab.total_waves + 3) / 4;
+    unsigned long long *keys = (unsigned long long *)work;
+    if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, keys)) return -1;
+    head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out);
+    NMX_LAUNCHED(ctx, "head_finish");
     return 0;
 }
 

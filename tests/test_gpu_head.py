@@ -39,7 +39,7 @@ def run_head(dev, W, rows, cols, X, drafts, logits=True):
     dW, dq, dd, dfs = dev.to_device(W), dev.to_device(q), dev.to_device(d), dev.to_device(fs)
     dl = dev.zeros((n, rows), np.float32) if logits else None
     ddr = dev.to_device(np.asarray(drafts, np.int32)) if n > 1 else None
-    work = dev.alloc(dev.head_work_bytes(rows, n))
+    work = dev.zeros(dev.head_work_bytes(rows, n), np.uint8)
     out = dev.zeros(2 + n, np.int32)
     dev.head_accept(dW, rows, cols, n, dq, dd, dfs, dl, ddr, work, out)
     dev.sync()
@@ -118,3 +118,36 @@ def test_head_widths_and_no_logits(dev, n):
     out, _ = run_head(dev, W, rows, cols, X, drafts, logits=False)
     assert out[0] == a_ref and out[1] == bonus_ref
     assert np.array_equal(out[2:], am)
+
+
+def test_head_accept_graph_replays_reuse_work(dev):
+    """The fused argmax keeps its device-wide state in the caller's work buffer and leaves it
+    reset: consecutive calls and several replays of one captured graph (with eager uploads of new
+    drafts between them) all give the oracle's answer."""
+    rng = np.random.default_rng(44)
+    rows, cols, n = 65536, 1024, 5
+    W = quantized_head(rng, rows, cols)
+    X = rng.standard_normal((n, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, n)
+    am = np.array([oracle.argmax(ref[t]) for t in range(n)], np.int32)
+    dW, dq, dd, dfs = dev.to_device(W), dev.to_device(q), dev.to_device(d), dev.to_device(fs)
+    ddr = dev.zeros(n - 1, np.int32)
+    work = dev.zeros(dev.head_work_bytes(rows, n), np.uint8)
+    out = dev.zeros(2 + n, np.int32)
+    dev.graph_begin()
+    dev.head_accept(dW, rows, cols, n, dq, dd, dfs, None, ddr, work, out)
+    g = dev.graph_end()
+    for rep, a in enumerate([4, 0, 2, 4, 1]):
+        drafts = planted_drafts(am, a, n - 1)
+        dev.upload(ddr, drafts)
+        if rep % 2:
+            dev.head_accept(dW, rows, cols, n, dq, dd, dfs, None, ddr, work, out)
+        else:
+            dev.graph_launch(g)
+        dev.sync()
+        got = out.numpy()
+        a_ref, bonus_ref, _ = oracle.accept(ref, drafts)
+        assert got[0] == a_ref and got[1] == bonus_ref, (rep, got, a_ref, bonus_ref)
+        assert np.array_equal(got[2:], am)
+

@@ -1,0 +1,90 @@
+"""Pins of the oracle's scalar primitives (CPU only): the reference's Cephes-style pf_expf
+bit for bit against oracle/_ref (the reference's own forward_ops.c), the gate exp / log1p
+(binary64 evaluation) against x87 extended precision and against glibc expf / log1pf, and
+argmax / acceptance against brute force and the reference's pf_argmax."""
+from __future__ import annotations
+
+import ctypes
+import ctypes.util
+
+import numpy as np
+import pytest
+
+import oracle
+
+L = oracle.lib()
+ref = oracle.ref_lib()
+libm = ctypes.CDLL(ctypes.util.find_library("m"))
+libm.expf.restype, libm.expf.argtypes = ctypes.c_float, [ctypes.c_float]
+libm.log1pf.restype, libm.log1pf.argtypes = ctypes.c_float, [ctypes.c_float]
+
+
+def sweep(lo, hi, n, seed=0):
+    rng = np.random.default_rng(seed)
+    x = np.concatenate([np.linspace(lo, hi, n // 2), rng.uniform(lo, hi, n // 2)])
+    return x.astype(np.float32)
+
+
+@pytest.mark.skipif(ref is None, reason="oracle/_ref not built (reference absent)")
+def test_expf_cephes_bit_exact_vs_reference_build():
+    xs = np.concatenate([sweep(-95, 95, 20000), np.float32([0.0, -0.0, 1e-30, -87, 88, 88.5])])
+    for x in xs:
+        a, b = L.orc_expf_cephes(float(x)), ref.pf_expf(float(x))
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32), x
+
+
+def correctly_rounded(fn, x):
+    return np.float32(fn(np.longdouble(x)))
+
+
+@pytest.mark.parametrize("lo,hi", [(-20, 20), (-103, 88), (-1e-3, 1e-3)])
+def test_gate_expf_correctly_rounded_and_near_glibc(lo, hi):
+    xs = sweep(lo, hi, 20000, seed=1)
+    got = np.array([L.orc_gate_expf(float(x)) for x in xs], np.float32)
+    exact = np.array([correctly_rounded(np.exp, x) for x in xs], np.float32)
+    assert np.array_equal(got, exact)
+    glibc = np.array([libm.expf(float(x)) for x in xs], np.float32)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - glibc.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.99
+
+
+@pytest.mark.parametrize("lo,hi", [(0, 5e8), (0, 20), (1e-9, 1e-3), (-0.9, 0.9)])
+def test_gate_log1pf_correctly_rounded_and_near_glibc(lo, hi):
+    """Correctly rounded everywhere; within 1 ulp of this host's glibc log1pf, which is not
+    correctly rounded (a few percent of inputs in [0, 20] differ by one ulp)."""
+    xs = sweep(lo, hi, 20000, seed=2)
+    got = np.array([L.orc_gate_log1pf(float(x)) for x in xs], np.float32)
+    exact = np.array([correctly_rounded(np.log1p, x) for x in xs], np.float32)
+    assert np.array_equal(got, exact)
+    glibc = np.array([libm.log1pf(float(x)) for x in xs], np.float32)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - glibc.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1
+
+
+def test_argmax_first_maximum():
+    v = np.array([1, 3, 2, 3, -1], np.float32)
+    assert oracle.argmax(v) == 1
+    assert oracle.argmax(np.array([-0.0, 0.0, -1.0], np.float32)) == 0
+    assert oracle.argmax(np.array([-2.0, 0.0, -0.0], np.float32)) == 1
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        v = rng.integers(-5, 5, rng.integers(1, 300)).astype(np.float32)
+        assert oracle.argmax(v) == int(np.argmax(v))
+        if ref is not None:
+            assert ref.pf_argmax(v.ctypes.data, v.size) == int(np.argmax(v))
+
+
+def test_accept_brute_force():
+    rng = np.random.default_rng(4)
+    for _ in range(300):
+        k = int(rng.integers(0, 6))
+        V = int(rng.integers(2, 40))
+        logits = rng.integers(-3, 3, (k + 1, V)).astype(np.float32)
+        am = [int(np.argmax(r)) for r in logits]
+        drafts = np.array([am[t] if rng.random() < 0.7 else (am[t] + 1) % V for t in range(k)],
+                          np.int32)
+        a = 0
+        while a < k and drafts[a] == am[a]:
+            a += 1
+        got_a, bonus, rows = oracle.accept(logits, drafts)
+        assert (got_a, bonus, list(rows)) == (a, am[a], am)
