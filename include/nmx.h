@@ -110,6 +110,7 @@ typedef struct {
     const float *pend;
     int keep;
     int log0;
+    const int32_t *keep_dev; /* non-NULL: keep = min(*keep_dev, keep) read on the device */
 } nmx_lin_args;
 int nmx_lin_rule(nmx_ctx *ctx, const nmx_lin_args *a);
 /* S advances by the first `keep` rows of log (the commit replay). */
@@ -127,6 +128,100 @@ size_t nmx_head_work_bytes(int rows, int n);
 int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
                     const float *d, const float *fsum, float *logits, const int32_t *drafts,
                     void *work, int32_t *out);
+
+/* ---- verify-step glue (the rest of one forward pass, engine/src/forward*.c) -------------
+ * All enqueue on the context's stream; positions come from a device control block so a
+ * captured HIP graph can be replayed at any position: ctl[0] = n_past at the start of the
+ * pass, ctl[1] = e (tokens committed by the last verify pass), ctl[2] = keep (pending
+ * replay rows, e - 1 after a commit). */
+typedef struct {
+    int8_t *q;   /* NULL: no A8 output */
+    float *d, *fs;
+} nmx_a8;
+
+/* Embedding rows of a Q4K matrix (pf_get_row / kern_get_row_q, engine/src/kern_act.c:53-88):
+ * X[t][c] = (D s) u - (M m) for the token ids tok[0..n) (device). */
+int nmx_embed_q4k(nmx_ctx *ctx, const void *W, int vocab, int cols, const int32_t *tok, int n,
+                  float *X, int x_stride);
+
+/* y = rmsnorm(x) * w per row (pf_rmsnorm, engine/src/forward_ops.c:191-200), after
+ * x += add when add != NULL (pf_add_rows, engine/src/forward.c:68-73); y may be NULL; a8.q
+ * != NULL also writes the A8 quantization of y (n vectors, block-major). */
+int nmx_rmsnorm(nmx_ctx *ctx, float *x, int x_stride, const float *add, int add_stride,
+                const float *w, int n, int cols, float eps, float *y, int y_stride, nmx_a8 a8);
+
+/* Gated DeltaNet pre (engine/src/forward_lin.c:36-67): causal conv + SiLU per channel with the
+ * conv state, q/k L2 norm (+ q scale), beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)).
+ * xin != NULL marks a logged pass: the state advances by token 0 only and the raw inputs of
+ * tokens 1..n-1 are kept in xin [n][C] for the commit. */
+typedef struct {
+    int n, C, conv_k, dk, kd;
+    const float *raw;
+    int raw_stride;
+    float *out;
+    float *state;
+    const float *conv_w;
+    float *xin;
+    float qscale, l2eps;
+    const float *b_in, *a_in;
+    int g_stride, heads;
+    const float *A_log, *A, *dt_bias;
+    float *beta, *decay;
+} nmx_lin_pre_args;
+int nmx_lin_pre(nmx_ctx *ctx, const nmx_lin_pre_args *p);
+
+/* Gated RMSNorm (engine/src/forward_lin.c:70-81): per (token, head) y = rmsnorm(o) * w *
+ * silu(z); y may be NULL; optional A8 of y. */
+int nmx_lin_post(nmx_ctx *ctx, const float *o, int o_stride, const float *z, int z_stride,
+                 const float *w, int n, int heads, int dv, float eps, float *y, int y_stride,
+                 nmx_a8 a8);
+
+/* SwiGLU (pf_silu_mul, engine/src/forward_ops.c:98-110): y = silu(gate) * up (+ A8). */
+int nmx_silu_mul(nmx_ctx *ctx, const float *gate, const float *up, int stride, int n, int cols,
+                 float *y, nmx_a8 a8);
+
+/* Gated full attention (engine/src/forward_attn.c:231-266). prep: k rows normed + RoPE and
+ * stored with the v rows at position *pos + pos_off + t; query heads normed + RoPE in place.
+ * attn: causal GQA softmax attention over rows [0, position], o *= sigmoid(gate), + A8. */
+typedef struct {
+    int n, nh, nkv, hd, rot, max_ctx;
+    float *q;                    /* [n][nh][2 hd] query | gate */
+    const float *k_in, *v_in;    /* [n][nkv hd] */
+    const float *q_norm, *k_norm;
+    float eps, scale;
+    const float *rope_cos, *rope_sin; /* [max_ctx][rot/2] */
+    float *kc, *vc;              /* [nkv][max_ctx][hd] */
+    const int32_t *pos;
+    int pos_off;
+    float *o;                    /* [n][nh hd] */
+    nmx_a8 a8;
+} nmx_attn_args;
+int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p);
+int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p);
+
+/* Rollback commit of every linear layer (pf_lin_commit, engine/src/forward_lin.c:185-204)
+ * with e = ctl[1]: conv state <- last conv_k - 1 rows of [state after token 0, raw inputs
+ * 1..e-1]; pend <- log rows 1..e-1; ctl[2] = e - 1. Arrays are [layers][...] contiguous. */
+typedef struct {
+    int layers, C, conv_k;
+    float *state;          /* [layers][conv_k-1][C] */
+    const float *xin;      /* [layers][cap][C] */
+    const float *log;      /* [layers][cap][row] */
+    float *pend;           /* [layers][cap][row] */
+    int cap, row;
+    int32_t *ctl;
+} nmx_commit_args;
+int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p);
+
+/* After nmx_head_accept: vt[a + 1] = bonus; ctl[1] = a + 1 (the reference's e without a stop,
+ * engine/src/spec.c:346-349). */
+int nmx_accept_commit(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl);
+int nmx_ctl_set(nmx_ctx *ctx, int32_t *ctl, int idx, int value);
+int nmx_ctl_advance(nmx_ctx *ctx, int32_t *ctl);   /* ctl[0] += ctl[1] */
+int nmx_copy_token(nmx_ctx *ctx, int32_t *vt, const int32_t *ctl); /* vt[0] = vt[ctl[1]] */
+/* dst[0..cols) = src[(*idx + off) * stride ..] (a device-chosen row) */
+int nmx_select_row(nmx_ctx *ctx, const float *src, int stride, const int32_t *idx, int off,
+                   int cols, float *dst);
 
 #ifdef __cplusplus
 }

@@ -46,7 +46,12 @@ __global__ __launch_bounds__(1024) void lin_rule_k(nmx_lin_args a) {
     }
 
     /* deferred commit of the previous pass (matvec_ref.c:169-188 arithmetic) */
-    for (int u = 0; u < a.keep; u++) {
+    int keep = a.keep;
+    if (a.keep_dev) {
+        const int kd_ = *a.keep_dev;
+        keep = kd_ < keep ? kd_ : keep;
+    }
+    for (int u = 0; u < keep; u++) {
         const float *pr = a.pend + ((size_t)u * heads + h) * logw;
         __syncthreads();
         for (int x = tid; x < DK; x += blockDim.x) sk[(x / DK4) * PAD + x % DK4] = pr[x];
@@ -59,7 +64,7 @@ __global__ __launch_bounds__(1024) void lin_rule_k(nmx_lin_args a) {
         }
     }
 
-    const bool store_now = (a.n == 0) || (a.log0 && a.keep > 0);
+    const bool store_now = (a.n == 0) || (a.log0 && keep > 0);
     if (store_now && live) {
 #pragma unroll
         for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);

@@ -1,0 +1,115 @@
+/* Internal definitions of the MI355X engine (libpinfer.so): the context, the device-resident
+ * model and state, and the forward / speculative-decoding entry points shared by the host
+ * source files. Not part of the public API (include/pinfer.h). */
+#ifndef NMXE_ENGINE_H
+#define NMXE_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "nmx.h"
+#include "pinfer.h"
+
+#define E_MAX_BATCH 64   /* rows per forward chunk (the reference's PF_MAX_BATCH) */
+#define E_MAX_K PINFER_SPEC_MAX_K
+
+/* .pq dtypes and layout constants (engine/src/pq_format.h, pq_quant.h) */
+enum { PQ_F32 = 0, PQ_BF16 = 1, PQ_Q4K = 4 };
+
+typedef struct {
+    const void *w;      /* device pointer to Q4K_G32 bytes */
+    int rows, cols;
+} e_mat;
+
+typedef struct {
+    int is_full;
+    const float *in_norm, *post_norm;   /* device, stored effective multipliers */
+    e_mat gate, up, down;
+    /* Gated DeltaNet */
+    int lin;                            /* index among the linear layers, -1 */
+    e_mat qkv, z, b, a, out;
+    const float *conv_w, *A_log, *A, *dt_bias, *lin_norm;
+    /* gated full attention */
+    int full;                           /* index among the full-attention layers, -1 */
+    e_mat q, k, v, o;
+    const float *q_norm, *k_norm;
+} e_layer;
+
+/* one set of per-row scratch buffers (E_MAX_BATCH rows) */
+typedef struct {
+    float *x, *xn, *out, *ta, *tb, *tc, *to, *conv, *ba, *aa, *beta, *decay, *cat, *emb;
+    nmx_a8 a_h;        /* A8 of width hidden */
+    nmx_a8 a_w;        /* A8 of the wide inputs: vd, n_heads * head_dim, 2 * hidden */
+    nmx_a8 a_f;        /* A8 of width ffn */
+    nmx_a8 a_1;        /* A8 of one hidden row (the head of a single row) */
+    float *row1;       /* [hidden] */
+} e_scratch;
+
+struct pinfer_ctx {
+    nmx_ctx *dev;
+    /* dimensions (engine/src/pinfer.c:45-63) */
+    int H, ffn, n_layers, vocab;
+    int n_heads, n_kv, hd, rot;
+    int lk_heads, lv_heads, lk_dim, lv_dim, conv_k, kd, vd, conv_dim;
+    int eos;
+    float rms_eps, rope_theta;
+    int n_lin, n_full, has_mtp;
+    int max_ctx;
+
+    /* weights: the .pq data section uploaded as one block */
+    void *blob;
+    e_layer *layers;
+    e_mat embed;              /* token embedding [vocab][H] */
+    e_mat head;               /* output head [vocab][H] (the embedding when tied) */
+    const float *norm;
+    /* MTP head (engine/src/mtp.c:8-34) */
+    e_mat mtp_fc;
+    const float *mtp_norm_emb, *mtp_norm_hid, *mtp_norm_out;
+    e_layer mtp;
+
+    /* state in HBM */
+    float *conv_state;        /* [n_lin][conv_k-1][conv_dim] */
+    float *rec;               /* [n_lin][lv_heads][lv_dim][lk_dim] */
+    float *kc, *vc;           /* [n_full][n_kv][max_ctx][hd] */
+    float *mkc, *mvc;         /* MTP cache [n_kv][max_ctx][hd] */
+    float *xin;               /* [n_lin][cap][conv_dim] raw conv inputs of a logged pass */
+    float *log, *pend;        /* [n_lin][cap][lv_heads][lk_dim + lv_dim + 1] */
+    int cap;                  /* rows per log = E_MAX_K + 1 */
+    float *rope_cos, *rope_sin;
+
+    e_scratch s;
+    float *hbuf;              /* [E_MAX_BATCH][H] final-normed rows kept for the MTP pass */
+    float *mbuf;              /* [3][H]: MTP hidden of the current draft + chain ping-pong */
+    int32_t *ctl;             /* [16] control block (see nmx.h) */
+    int32_t *vt;              /* [E_MAX_K + 2] verify tokens */
+    int32_t *tok;             /* [E_MAX_BATCH] tokens of an eager forward */
+    int32_t *hout;            /* [2 + E_MAX_BATCH] head output */
+    int32_t *hout2;           /* [2 + 1] MTP head output */
+    void *hwork;              /* head argmax scratch */
+    float *logits;            /* [vocab] logits of one row when requested */
+
+    /* host mirror of the position state */
+    int n_past, mtp_rows, keep;
+    /* captured rounds: verify graph and commit graph per draft count */
+    nmx_graph *g_verify[E_MAX_K + 1], *g_commit[E_MAX_K + 1];
+    int graph_nv;             /* draft vocabulary the graphs were captured with */
+    int use_graphs;
+};
+
+/* forward.c */
+int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged);
+int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits);
+int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst);
+int e_set_pos(pinfer_ctx *c, int pos);
+
+/* spec.c */
+int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out, int n_max,
+               const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
+               pinfer_spec_stats *stats, int *status);
+void e_drop_graphs(pinfer_ctx *c);
+
+/* model.c */
+int e_model_load(pinfer_ctx *c, const char *path);
+
+#endif

@@ -1,0 +1,163 @@
+/* The forward pass of the Qwen3.5 hybrid on the device: the per-layer sequence of
+ * engine/src/forward.c:92-147 (forward_chunk), forward_lin.c:94-133 (pf_linear_attn),
+ * forward_attn.c:231-266 (pf_full_attn) and mtp.c:60-100 (pf_mtp_forward), each step an nmx
+ * kernel on the context's stream. Nothing here touches the host copy of any activation, so a
+ * sequence can be captured into a HIP graph; positions come from the control block c->ctl
+ * (ctl[0] = n_past at the start of the pass). Residual adds are fused into the following
+ * RMSNorm and every matmul input is A8-quantized by the kernel that produces it. */
+#include <math.h>
+#include <stdio.h>
+
+#include "engine.h"
+
+#define CK(call)                                                                              \
+    do {                                                                                      \
+        if ((call) != 0) {                                                                    \
+            fprintf(stderr, "pinfer: %s: %s\n", #call, nmx_error(c->dev));                    \
+            return PINFER_E_ARG;                                                              \
+        }                                                                                     \
+    } while (0)
+
+int e_set_pos(pinfer_ctx *c, int pos) {
+    CK(nmx_ctl_set(c->dev, c->ctl, 0, pos));
+    return PINFER_OK;
+}
+
+static size_t kv_layer(const pinfer_ctx *c) { return (size_t)c->n_kv * c->max_ctx * c->hd; }
+
+/* mix + MLP of one full-attention block on rows s->x (A8 of the normed input already in a_h);
+ * kc / vc: the block's caches; pos_off: position of row 0 relative to ctl[0]. */
+static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *vc, int pos_off) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    const int H = c->H, hd = c->hd, qw = 2 * c->n_heads * hd, kvw = c->n_kv * hd;
+    const void *W[3] = {L->q.w, L->k.w, L->v.w};
+    const int R[3] = {qw, kvw, kvw};
+    float *Y[3] = {s->ta, s->tb, s->tc};
+    CK(nmx_q4k_matmul_multi(D, 3, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
+    nmx_attn_args a = {n, c->n_heads, c->n_kv, hd, c->rot, c->max_ctx, s->ta, s->tb, s->tc,
+                       L->q_norm, L->k_norm, c->rms_eps, 1.0f / sqrtf((float)hd), c->rope_cos,
+                       c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w};
+    CK(nmx_attn_prep(D, &a));
+    CK(nmx_attn(D, &a));
+    CK(nmx_q4k_matmul(D, L->o.w, H, c->n_heads * hd, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->out,
+                      H, NULL));
+    return PINFER_OK;
+}
+
+/* post norm + SwiGLU MLP (engine/src/forward.c:49-58): x += mix out; xn = norm(x);
+ * out = down(silu(gate xn) * up xn). */
+static int mlp_block(pinfer_ctx *c, const e_layer *L, int n) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    const int H = c->H, F = c->ffn;
+    CK(nmx_rmsnorm(D, s->x, H, s->out, H, L->post_norm, n, H, c->rms_eps, NULL, 0, s->a_h));
+    const void *W[2] = {L->gate.w, L->up.w};
+    const int R[2] = {F, F};
+    float *Y[2] = {s->ta, s->tb};
+    CK(nmx_q4k_matmul_multi(D, 2, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
+    CK(nmx_silu_mul(D, s->ta, s->tb, F, n, F, NULL, s->a_f));
+    CK(nmx_q4k_matmul(D, L->down.w, H, F, n, s->a_f.q, s->a_f.d, s->a_f.fs, s->out, H, NULL));
+    return PINFER_OK;
+}
+
+/* Gated DeltaNet mixer (engine/src/forward_lin.c:94-133). logged: a verify pass (token 0
+ * committed in place, tokens 1.. logged for the commit); pending replays of the last commit
+ * are applied first (keep = ctl[2]). */
+static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    const int H = c->H, C = c->conv_dim, vd = c->vd, nv = c->lv_heads, li = L->lin;
+    const int logw = c->lk_dim + c->lv_dim + 1;
+    const size_t lrow = (size_t)c->cap * nv * logw;
+    const void *W[4] = {L->qkv.w, L->z.w, L->b.w, L->a.w};
+    const int R[4] = {C, vd, nv, nv};
+    float *Y[4] = {s->ta, s->tb, s->ba, s->aa};
+    CK(nmx_q4k_matmul_multi(D, 4, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
+    nmx_lin_pre_args p = {n, C, c->conv_k, c->lk_dim, c->kd, s->ta, C, s->conv,
+                          c->conv_state + (size_t)li * (c->conv_k - 1) * C, L->conv_w,
+                          logged ? c->xin + (size_t)li * c->cap * C : NULL,
+                          1.0f / sqrtf((float)c->lk_dim), 1e-6f, s->ba, s->aa, nv, nv, L->A_log,
+                          L->A, L->dt_bias, s->beta, s->decay};
+    CK(nmx_lin_pre(D, &p));
+    nmx_lin_args a = {n, nv, nv / c->lk_heads, c->lk_dim, c->lv_dim, C, vd, s->conv, s->decay,
+                      s->beta, c->rec + (size_t)li * nv * c->lk_dim * c->lv_dim, s->to,
+                      logged ? c->log + (size_t)li * lrow : NULL, c->pend + (size_t)li * lrow,
+                      c->cap - 1, 0, c->ctl + 2};
+    CK(nmx_lin_rule(D, &a));
+    CK(nmx_lin_post(D, s->to, vd, s->tb, vd, L->lin_norm, n, nv, c->lv_dim, c->rms_eps, NULL, 0,
+                    s->a_w));
+    CK(nmx_q4k_matmul(D, L->out.w, H, vd, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->out, H, NULL));
+    return PINFER_OK;
+}
+
+/* n tokens (device ids) at positions ctl[0].. through the main model; leaves the final-normed
+ * rows in s->xn and their A8 in s->a_h (the head's input). */
+int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    const int H = c->H;
+    CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, s->x, H));
+    const float *add = NULL;
+    for (int l = 0; l < c->n_layers; l++) {
+        const e_layer *L = &c->layers[l];
+        CK(nmx_rmsnorm(D, s->x, H, add, H, L->in_norm, n, H, c->rms_eps, NULL, 0, s->a_h));
+        int rc = L->is_full ? attn_block(c, L, n, c->kc + (size_t)L->full * kv_layer(c),
+                                         c->vc + (size_t)L->full * kv_layer(c), 0)
+                            : lin_block(c, L, n, logged);
+        if (rc) return rc;
+        if ((rc = mlp_block(c, L, n))) return rc;
+        add = s->out;
+    }
+    CK(nmx_rmsnorm(D, s->x, H, add, H, c->norm, n, H, c->rms_eps, s->xn, H, s->a_h));
+    CK(nmx_ctl_set(D, c->ctl, 2, 0)); /* every linear layer applied the pending rows */
+    return PINFER_OK;
+}
+
+/* Head of one row of s->xn (row index *idx + off): argmax over the first `rows` head rows to
+ * dst_dev (if not NULL); the logits of that row to c->logits when want_logits. */
+static int head_row(pinfer_ctx *c, const int32_t *idx, int off, int rows, int32_t *dst_dev,
+                    int want_logits) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    CK(nmx_select_row(D, s->xn, c->H, idx, off, c->H, s->row1));
+    CK(nmx_quant_a8(D, s->row1, 1, c->H, s->a_1.q, s->a_1.d, s->a_1.fs));
+    CK(nmx_head_accept(D, c->head.w, rows, c->H, 1, s->a_1.q, s->a_1.d, s->a_1.fs,
+                       want_logits ? c->logits : NULL, NULL, c->hwork, c->hout2));
+    if (dst_dev) CK(nmx_copy_d2d(D, dst_dev, c->hout2 + 1, sizeof(int32_t)));
+    return PINFER_OK;
+}
+
+int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits) {
+    return head_row(c, c->ctl + 15, n - 1, c->vocab, dst_dev, want_logits);
+}
+
+/* The MTP draft head (engine/src/mtp.c:60-100) over n rows: h_dev [n][H] final-normed
+ * hiddens, tok_dev [n] the tokens that follow them, positions ctl[0] + pos_off + i. The
+ * selected row (n - 1, or ctl[1] - 1 when head_row_dynamic) gives the draft (argmax over the
+ * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL). */
+int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    const int H = c->H;
+    const nmx_a8 none = {NULL, NULL, NULL};
+    CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, s->emb, H));
+    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)] */
+    CK(nmx_rmsnorm(D, s->emb, H, NULL, 0, c->mtp_norm_emb, n, H, c->rms_eps, s->cat, 2 * H, none));
+    CK(nmx_rmsnorm(D, (float *)h_dev, H, NULL, 0, c->mtp_norm_hid, n, H, c->rms_eps, s->cat + H,
+                   2 * H, none));
+    CK(nmx_quant_a8(D, s->cat, n, 2 * H, s->a_w.q, s->a_w.d, s->a_w.fs));
+    CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->x, H, NULL));
+    const e_layer *L = &c->mtp;
+    CK(nmx_rmsnorm(D, s->x, H, NULL, 0, L->in_norm, n, H, c->rms_eps, NULL, 0, s->a_h));
+    int rc = attn_block(c, L, n, c->mkc, c->mvc, pos_off);
+    if (rc) return rc;
+    if ((rc = mlp_block(c, L, n))) return rc;
+    CK(nmx_rmsnorm(D, s->x, H, s->out, H, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H, none));
+    const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
+    const int off = head_row_dynamic ? -1 : n - 1;
+    if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));
+    if (draft_dst) return head_row(c, idx, off, nv, draft_dst, 0);
+    return PINFER_OK;
+}

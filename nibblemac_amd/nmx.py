@@ -30,7 +30,7 @@ class LinArgs(ctypes.Structure):
     _fields_ = [("n", _i), ("heads", _i), ("rep", _i), ("dk", _i), ("dv", _i),
                 ("qkv_stride", _i), ("o_stride", _i), ("qkv", _vp), ("decay", _vp),
                 ("beta", _vp), ("S", _vp), ("o", _vp), ("log", _vp), ("pend", _vp),
-                ("keep", _i), ("log0", _i)]
+                ("keep", _i), ("log0", _i), ("keep_dev", _vp)]
 
 
 _SIGS: dict[str, tuple[object, list[object]]] = {
@@ -241,7 +241,7 @@ class Device:
     def lin_rule(self, *, n, heads, rep, dk, dv, qkv_stride, o_stride, qkv, decay, beta, S, o,
                  log=None, pend=None, keep=0, log0=False) -> None:
         a = LinArgs(n, heads, rep, dk, dv, qkv_stride, o_stride, _p(qkv), _p(decay), _p(beta),
-                    _p(S), _p(o), _p(log), _p(pend), keep, int(log0))
+                    _p(S), _p(o), _p(log), _p(pend), keep, int(log0), None)
         self.check(self.lib.nmx_lin_rule(self.ctx, ctypes.byref(a)), "lin_rule")
 
     def lin_apply(self, S, log, keep: int, heads: int, dk: int, dv: int) -> None:
