@@ -150,6 +150,12 @@ int nmx_embed_q4k(nmx_ctx *ctx, const void *W, int vocab, int cols, const int32_
 int nmx_rmsnorm(nmx_ctx *ctx, float *x, int x_stride, const float *add, int add_stride,
                 const float *w, int n, int cols, float eps, float *y, int y_stride, nmx_a8 a8);
 
+/* nmx_rmsnorm with the residual sum x + add written to xo instead of in place (xo NULL: not
+ * written; xo may equal x). */
+int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add, int add_stride,
+                   float *xo, int xo_stride, const float *w, int n, int cols, float eps, float *y,
+                   int y_stride, nmx_a8 a8);
+
 /* Gated DeltaNet pre (engine/src/forward_lin.c:36-67): causal conv + SiLU per channel with the
  * conv state, q/k L2 norm (+ q scale), beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)).
  * xin != NULL marks a logged pass: the state advances by token 0 only and the raw inputs of
@@ -176,13 +182,44 @@ int nmx_lin_post(nmx_ctx *ctx, const float *o, int o_stride, const float *z, int
                  const float *w, int n, int heads, int dv, float eps, float *y, int y_stride,
                  nmx_a8 a8);
 
+/* RMSNorm input of a fused matmul: rows x (+ add, the residual, added first) of [n][cols],
+ * normed with weight w (engine/src/forward_ops.c:191-200, forward.c pf_add_rows). x_out (if
+ * not NULL) receives x + add, written once; it must not alias x or add. */
+typedef struct {
+    const float *x;
+    int x_stride;
+    const float *add;
+    int add_stride;
+    float *x_out;
+    int xo_stride;
+    const float *w;
+    float eps;
+} nmx_norm_in;
+
+/* nmx_q4k_matmul_multi on the A8 of rmsnorm(in): the norm and the quantization run inside the
+ * matmul's workgroups (equal to nmx_rmsnorm + the matmul bit for bit). a8_tmp (n x cols A8
+ * buffers) is used only when the shape is outside the fused kernel's limits. */
+int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int *rows,
+                        float *const *Y, const int *y_stride, int cols, int n,
+                        const nmx_norm_in *in, nmx_a8 a8_tmp);
+
+/* The SwiGLU MLP input (engine/src/forward.c:49-58, forward_ops.c:98-110): h = silu(Wg a) *
+ * (Wu a) for a = the A8 input (q, d, fsum) or, when in is not NULL, the A8 of rmsnorm(in);
+ * h is written as A8 to out (and as floats [n][ffn] to y if not NULL). Fused into one launch
+ * when the shape fits; otherwise a8_tmp (n x cols) and gate_tmp / up_tmp ([n][ffn] floats)
+ * hold the intermediate results. */
+int nmx_q4k_swiglu(nmx_ctx *ctx, const void *Wg, const void *Wu, int ffn, int cols, int n,
+                   const int8_t *q, const float *d, const float *fsum, const nmx_norm_in *in,
+                   float *y, nmx_a8 out, nmx_a8 a8_tmp, float *gate_tmp, float *up_tmp);
+
 /* SwiGLU (pf_silu_mul, engine/src/forward_ops.c:98-110): y = silu(gate) * up (+ A8). */
 int nmx_silu_mul(nmx_ctx *ctx, const float *gate, const float *up, int stride, int n, int cols,
                  float *y, nmx_a8 a8);
 
 /* Gated full attention (engine/src/forward_attn.c:231-266). prep: k rows normed + RoPE and
  * stored with the v rows at position *pos + pos_off + t; query heads normed + RoPE in place.
- * attn: causal GQA softmax attention over rows [0, position], o *= sigmoid(gate), + A8. */
+ * attn: causal GQA softmax attention over rows [0, position], o *= sigmoid(gate), + A8; two
+ * launches (scores into the caller's workspace, then softmax + P.V). */
 typedef struct {
     int n, nh, nkv, hd, rot, max_ctx;
     float *q;                    /* [n][nh][2 hd] query | gate */
@@ -195,6 +232,7 @@ typedef struct {
     int pos_off;
     float *o;                    /* [n][nh hd] */
     nmx_a8 a8;
+    float *scores;               /* attn workspace: [n][nh][max_ctx] floats */
 } nmx_attn_args;
 int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p);
 int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p);

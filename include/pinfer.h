@@ -115,6 +115,12 @@ int pinfer_generate_greedy_cont(pinfer_ctx *ctx, const int32_t *prompt, int n_pr
                                 const pinfer_gen_opts *opts, pinfer_spec_stats *stats,
                                 int *status);
 
+/* Benchmark helper (the reference CLI's timing, engine/tools/pinfer_run.c:384-430): reset,
+ * prefill (timed), then exactly n_gen tokens with EOS ignored (timed). */
+int pinfer_bench_generate(pinfer_ctx *ctx, const int32_t *prompt, int n_prompt, int32_t *out,
+                          int n_gen, const pinfer_spec_params *sp, pinfer_spec_stats *stats,
+                          double *prefill_s, double *decode_s);
+
 int pinfer_n_vocab(const pinfer_ctx *ctx);
 int pinfer_n_past(const pinfer_ctx *ctx);
 int pinfer_eos_id(const pinfer_ctx *ctx);

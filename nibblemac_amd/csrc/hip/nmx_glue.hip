@@ -11,41 +11,36 @@
  * nmx_math.h in place of glibc's expf / log1pf. */
 #include "nmx_internal.h"
 #include "nmx_math.h"
+#include "nmx_a8.h"
 
 namespace {
 
-/* ---- A8 of one 32-value block held by a 32-lane half-wave (lane = column within block) ----
- * engine/src/kern_act.c:14-42: amax, id = 127 / amax, round-half-even codes, d = amax / 127,
- * fsum = d * sum(codes). Writes the block-major element (b, v). */
+/* ---- A8 of one 32-value block held by a 32-lane half-wave (lane = column within block),
+ * written as the block-major element (b, v) of an [nb][n] layout (nmx_a8.h). */
 __device__ __forceinline__ void a8_block(float x, int b, int v, int n, int8_t *q, float *d,
                                          float *fs) {
-    const int j = threadIdx.x & 31;
-    float amax = fabsf(x);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
-    const int c = (int)rintf(x * id);
-    int sum = c;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
     const size_t u = (size_t)b * n + v;
-    q[u * 32 + j] = (int8_t)(c > 127 ? 127 : c < -128 ? -128 : c);
-    if (j == 0) {
-        const float dd = amax / 127.0f;
-        d[u] = dd;
-        fs[u] = dd * (float)sum;
-    }
+    nmx_a8_store(x, q + u * 32, d + u, fs + u);
 }
 
 /* Sum in the reference's order (sumsq forward_ops.c:168-189, pf_softmax_exp :333-353):
  * partial l accumulates v[4m + l] for m ascending over the first cols/4*4 elements;
- * s = (c0 + c1) + (c2 + c3); the tail sequentially into t; result s + t. v[] is in LDS (the
- * squares for a norm); four lanes run the four chains. Every thread of the block gets it. */
+ * s = (c0 + c1) + (c2 + c3); the tail sequentially into t; result s + t. v[] is in LDS in
+ * element order; four lanes run the four chains, reading 16 values per batch so the LDS
+ * latency overlaps the dependent adds. Every thread of the block gets the result. */
 __device__ float ordered_sum4(const float *sq, int cols, float *red) {
     const int tid = threadIdx.x, m4 = cols >> 2;
     if (tid < 4) {
         float c = 0.0f;
-        for (int m = 0; m < m4; m++) c = c + sq[4 * m + tid];
+        int m = 0;
+        for (; m + 16 <= m4; m += 16) {
+            float b[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) b[u] = sq[4 * (m + u) + tid];
+#pragma unroll
+            for (int u = 0; u < 16; u++) c = c + b[u];
+        }
+        for (; m < m4; m++) c = c + sq[4 * m + tid];
         red[tid] = c;
     } else if (tid == 4) {
         float t = 0.0f;
@@ -58,6 +53,42 @@ __device__ float ordered_sum4(const float *sq, int cols, float *red) {
     __syncthreads();
     return r;
 }
+
+/* The same sum over values stored chain-major: chain l's m-th value at cm[l * s4 + m]
+ * (s4 a multiple of 4, so a chain is read as float4), the cols % 4 tail at cm[4 * s4 + k]. */
+__device__ float ordered_sum4_cm(const float *cm, int cols, int s4, float *red) {
+    const int tid = threadIdx.x, m4 = cols >> 2;
+    if (tid < 4) {
+        const float *ch = cm + tid * s4;
+        float c = 0.0f;
+        int m = 0;
+        for (; m + 32 <= m4; m += 32) {
+            float4 b[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + m + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                c = c + b[u].x;
+                c = c + b[u].y;
+                c = c + b[u].z;
+                c = c + b[u].w;
+            }
+        }
+        for (; m < m4; m++) c = c + ch[m];
+        red[tid] = c;
+    } else if (tid == 4) {
+        float t = 0.0f;
+        for (int i = m4 * 4; i < cols; i++) t = t + cm[4 * s4 + (i - m4 * 4)];
+        red[4] = t;
+    }
+    __syncthreads();
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    const float r = s + red[4];
+    __syncthreads();
+    return r;
+}
+
+__host__ __device__ constexpr int cm_stride(int cols) { return (((cols >> 2) + 3) & ~3) + 4; }
 
 /* ---- embedding rows of a Q4K matrix (engine/src/kern_act.c:53-88) ---- */
 __global__ __launch_bounds__(256) void embed_k(const uint8_t *__restrict__ W, int cols,
@@ -79,34 +110,61 @@ __global__ __launch_bounds__(256) void embed_k(const uint8_t *__restrict__ W, in
 
 /* ---- RMSNorm of rows (engine/src/forward_ops.c:191-200): optional residual add first
  * (x += add, written back, forward.c pf_add_rows), r = 1 / sqrtf(sumsq / cols + eps),
- * y = (x * r) * w; optional A8 of y for the next matmul. One workgroup per row. */
-__global__ __launch_bounds__(256) void rmsnorm_k(float *__restrict__ x, int x_stride,
-                                                 const float *__restrict__ add, int add_stride,
+ * y = (x * r) * w; optional A8 of y for the next matmul. One workgroup per row; every global
+ * load of the row (x, add, w) is issued before the first use, PER values per thread. */
+template <int PER>
+__global__ __launch_bounds__(256) void rmsnorm_k(const float *x, int x_stride,
+                                                 const float *add, int add_stride,
+                                                 float *xo, int xo_stride,
                                                  const float *__restrict__ w, int cols, float eps,
                                                  float *__restrict__ y, int y_stride,
                                                  int8_t *__restrict__ q, float *__restrict__ d,
                                                  float *__restrict__ fs, int n) {
-    extern __shared__ float sq[];
+    extern __shared__ float sq[]; /* chain-major squares */
     __shared__ float red[8];
     const int row = blockIdx.x, tid = threadIdx.x;
-    float *xr = x + (size_t)row * x_stride;
-    for (int i = tid; i < cols; i += 256) {
-        float v = xr[i];
-        if (add) {
-            v = v + add[(size_t)row * add_stride + i];
-            xr[i] = v;
+    const int m4 = cols >> 2, s4 = cm_stride(cols);
+    const float *xr = x + (size_t)row * x_stride;
+    float v[PER], wv[PER];
+    /* clamped (always in-bounds, branch-free) loads; values past cols are masked below */
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = tid + 256 * u;
+        v[u] = xr[i < cols ? i : cols - 1];
+        wv[u] = w[i < cols ? i : cols - 1];
+    }
+    if (add) {
+        float av[PER];
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = tid + 256 * u;
+            av[u] = add[(size_t)row * add_stride + (i < cols ? i : cols - 1)];
         }
-        sq[i] = v * v;
+#pragma unroll
+        for (int u = 0; u < PER; u++) v[u] = v[u] + av[u];
+    }
+    if (xo) {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = tid + 256 * u;
+            if (i < cols) xo[(size_t)row * xo_stride + i] = v[u];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = tid + 256 * u;
+        if (i < cols) sq[i < 4 * m4 ? (i & 3) * s4 + (i >> 2) : 4 * s4 + (i - 4 * m4)] = v[u] * v[u];
     }
     __syncthreads();
-    const float ss = ordered_sum4(sq, cols, red);
+    const float ss = ordered_sum4_cm(sq, cols, s4, red);
     const float r = 1.0f / sqrtf(ss / (float)cols + eps);
-    for (int base = 0; base < cols; base += 256) {
-        const int i = base + tid;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = tid + 256 * u;
         const bool live = i < cols;
-        const float v = live ? (xr[i] * r) * w[i] : 0.0f;
-        if (live && y) y[(size_t)row * y_stride + i] = v;
-        if (q && base + (tid & ~31) < cols) a8_block(v, i >> 5, row, n, q, d, fs);
+        const float o = live ? (v[u] * r) * wv[u] : 0.0f;
+        if (live && y) y[(size_t)row * y_stride + i] = o;
+        if (q && 256 * u + (tid & ~31) < cols) a8_block(o, i >> 5, row, n, q, d, fs);
     }
 }
 
@@ -131,9 +189,11 @@ struct LinPre {
     float *beta, *decay;     /* [n][heads] */
 };
 
+constexpr int PRE_TB = 8; /* tokens per batch: their loads issued together, norms in parallel */
+
 __global__ __launch_bounds__(256) void lin_pre_k(LinPre a) {
-    extern __shared__ float sq[]; /* [dk] squares */
-    __shared__ float red[8];
+    extern __shared__ float sq[]; /* [PRE_TB][dk] squares */
+    __shared__ float red[4 * PRE_TB];
     const int ngroups = (a.C + a.dk - 1) / a.dk;
     const int tid = threadIdx.x;
     if ((int)blockIdx.x == ngroups) { /* gates */
@@ -152,42 +212,79 @@ __global__ __launch_bounds__(256) void lin_pre_k(LinPre a) {
     const int ch = blockIdx.x * a.dk + tid;
     const bool live = tid < a.dk && ch < a.C;
     const int S = a.K - 1;
-    float win[8];
     const int cc = live ? ch : 0;
+    float win[8], wc[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) win[r] = (r < S) ? a.state[(size_t)r * a.C + cc] : 0.0f;
-    const float *wc = a.conv_w + (size_t)cc * a.K;
+    for (int r = 0; r < 8; r++) {
+        win[r] = (r < S) ? a.state[(size_t)r * a.C + cc] : 0.0f;
+        wc[r] = (r < a.K) ? a.conv_w[(size_t)cc * a.K + r] : 0.0f;
+    }
     const bool norm = blockIdx.x * a.dk < 2 * a.kd;  /* a q or k head */
     const float scale = blockIdx.x * a.dk < a.kd ? a.qscale : 1.0f;
-    for (int t = 0; t < a.n; t++) {
-        const float xt = a.raw[(size_t)t * a.raw_stride + cc];
-        /* taps in order over [state rows (oldest first), x_t] */
-        float acc = wc[0] * (S > 0 ? win[0] : xt);
+    const int m4 = a.dk >> 2;
+    for (int t0 = 0; t0 < a.n; t0 += PRE_TB) {
+        const int nb = a.n - t0 < PRE_TB ? a.n - t0 : PRE_TB;
+        float xt[PRE_TB], yv[PRE_TB];
 #pragma unroll
-        for (int j = 1; j < 8; j++)
-            if (j < a.K) acc = acc + wc[j] * (j < S ? win[j] : xt);
-        /* shift the window: it now ends with x_t */
+        for (int u = 0; u < PRE_TB; u++)
+            xt[u] = u < nb ? a.raw[(size_t)(t0 + u) * a.raw_stride + cc] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 7; j++)
-            if (j + 1 < S) win[j] = win[j + 1];
+        for (int u = 0; u < PRE_TB; u++) {
+            yv[u] = 0.0f;
+            if (u >= nb) continue;
+            const int t = t0 + u;
+            /* taps in order over [state rows (oldest first), x_t] */
+            float acc = wc[0] * (S > 0 ? win[0] : xt[u]);
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (j == S - 1) win[j] = xt;
-        if (t == 0 && a.xin && live) {  /* logged pass: token 0 is committed in place */
+            for (int j = 1; j < 8; j++)
+                if (j < a.K) acc = acc + wc[j] * (j < S ? win[j] : xt[u]);
+            /* shift the window: it now ends with x_t */
+#pragma unroll
+            for (int j = 0; j < 7; j++)
+                if (j + 1 < S) win[j] = win[j + 1];
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                if (j < S) a.state[(size_t)j * a.C + ch] = win[j];
+                if (j == S - 1) win[j] = xt[u];
+            if (t == 0 && a.xin && live) {  /* logged pass: token 0 is committed in place */
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (j < S) a.state[(size_t)j * a.C + ch] = win[j];
+            }
+            if (t > 0 && a.xin && live) a.xin[(size_t)t * a.C + ch] = xt[u];
+            yv[u] = nmx_silu(acc);
         }
-        if (t > 0 && a.xin && live) a.xin[(size_t)t * a.C + ch] = xt;
-        float yv = nmx_silu(acc);
-        if (norm) {
-            sq[tid] = live ? yv * yv : 0.0f;
+        if (norm) { /* L2 norm per token (forward_ops.c:204-212): chains of 4 per token */
+            __syncthreads(); /* the previous batch's reads of sq are done */
+#pragma unroll
+            for (int u = 0; u < PRE_TB; u++)
+                if (u < nb && tid < a.dk) sq[u * a.dk + tid] = live ? yv[u] * yv[u] : 0.0f;
             __syncthreads();
-            const float ss = ordered_sum4(sq, a.dk, red);
-            const float r = 1.0f / sqrtf(ss + a.l2eps);
-            yv = (yv * r) * scale;
+            if (tid < 4 * nb) {
+                const float *v = sq + (tid >> 2) * a.dk + (tid & 3);
+                float c = 0.0f;
+                int m = 0;
+                for (; m + 16 <= m4; m += 16) {
+                    float b[16];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) b[k] = v[4 * (m + k)];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) c = c + b[k];
+                }
+                for (; m < m4; m++) c = c + v[4 * m];
+                red[tid] = c;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < PRE_TB; u++) {
+                if (u >= nb) continue;
+                const float ss = ((red[4 * u] + red[4 * u + 1]) + (red[4 * u + 2] + red[4 * u + 3])) + 0.0f;
+                const float r = 1.0f / sqrtf(ss + a.l2eps);
+                yv[u] = (yv[u] * r) * scale;
+            }
         }
-        if (live) a.out[(size_t)t * a.C + ch] = yv;
+#pragma unroll
+        for (int u = 0; u < PRE_TB; u++)
+            if (u < nb && live) a.out[(size_t)(t0 + u) * a.C + ch] = yv[u];
     }
     if (!a.xin && live) {
 #pragma unroll
@@ -286,64 +383,177 @@ __global__ __launch_bounds__(512) void attn_prep_k(Attn a) {
     }
 }
 
-/* Scores (pf_dot's 16 interleaved partial sums, then * scale; forward_kv.c:281-303,
- * forward_ops.c:265-287), softmax (max; exp(a - max) with 4 partial sums + tail; * 1/sum;
- * forward_attn.c:171-181, forward_ops.c:294-353), P.V in row order from zero
- * (forward_ops.c:360-382), o *= sigmoid(gate) (forward_attn.c:217-220); + A8 of o for o_proj.
- * One workgroup of hd threads per (token, query head). */
-__global__ __launch_bounds__(512) void attn_k(Attn a) {
-    extern __shared__ float att[]; /* [np] */
-    __shared__ float qs[512];
-    __shared__ float red[8];
-    const int t = blockIdx.y, h = blockIdx.x, tid = threadIdx.x, hd = a.hd, nt = blockDim.x;
-    const int g = h / (a.nh / a.nkv);
+/* Scores (engine/src/forward_kv.c:281-303, pf_dot forward_ops.c:265-287): for every query
+ * head h of KV group g and position p <= pos(t), s = (pf_dot(q_h, k_p) + 0) * scale, where
+ * pf_dot keeps 16 interleaved partial sums c_l over elements i = l (mod 16) in i order and
+ * combines h_k = (c_4k + c_4k+1) + (c_4k+2 + c_4k+3), s = (h_0 + h_1) + (h_2 + h_3) (hd is a
+ * multiple of 16: no tail). Workgroup = (chunk of CP positions, token t, group g): the K rows
+ * of the chunk are staged in LDS (row stride hd + 4 floats, so lanes reading different rows
+ * hit different banks); lane = position (lane % CP) x part (lane / CP) of the 16 partial
+ * sums, the parts combined in the tree order by two cross-lane exchanges; wave w takes the
+ * group's query heads w, w + 4, ... */
+template <int CP>
+__global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ sc) {
+    constexpr int LP = 64 / CP, CPL = 16 / LP; /* lanes per position, partial sums per lane */
+    extern __shared__ float4 smem4[];
+    const int hd = a.hd, rep = a.nh / a.nkv, rs = hd + 4;
+    const int t = blockIdx.y, g = blockIdx.z, p0 = blockIdx.x * CP;
     const int np = *a.pos + a.pos_off + t + 1;
-    const float *qrow = a.q + ((size_t)t * a.nh + h) * 2 * hd;
-    qs[tid] = qrow[tid];
-    __syncthreads();
-    const float *K = a.kc + (size_t)g * a.max_ctx * hd;
-    const int i16 = hd / 16 * 16;
-    for (int p = tid; p < np; p += nt) {
-        const float *kr = K + (size_t)p * hd;
-        float c[16];
+    if (p0 >= np) return;
+    const int rows = np - p0 < CP ? np - p0 : CP;
+    float *ks = (float *)smem4;   /* [CP][rs] */
+    float *qs = ks + CP * rs;     /* [4][hd] */
+    const int f4 = hd >> 2;
+    const float *K = a.kc + ((size_t)g * a.max_ctx + p0) * hd;
+    for (int f0 = 0; f0 < rows * f4; f0 += 4 * 256) {
+        float4 b[4];
 #pragma unroll
-        for (int l = 0; l < 16; l++) c[l] = 0.0f;
-        for (int i = 0; i < i16; i += 16) {
-#pragma unroll
-            for (int l = 0; l < 16; l++) c[l] = c[l] + qs[i + l] * kr[i + l];
+        for (int u = 0; u < 4; u++) {
+            const int f = f0 + u * 256 + threadIdx.x;
+            b[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (f < rows * f4) b[u] = ((const float4 *)K)[f];
         }
-        float hs[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) hs[k] = (c[4 * k] + c[4 * k + 1]) + (c[4 * k + 2] + c[4 * k + 3]);
-        const float s = (hs[0] + hs[1]) + (hs[2] + hs[3]);
-        float tl = 0.0f;
-        for (int i = i16; i < hd; i++) tl = tl + qs[i] * kr[i];
-        att[p] = (s + tl) * a.scale;
+        for (int u = 0; u < 4; u++) {
+            const int f = f0 + u * 256 + threadIdx.x;
+            if (f < rows * f4) {
+                const int r = f / f4, c4 = f - r * f4;
+                *(float4 *)(ks + r * rs + 4 * c4) = b[u];
+            }
+        }
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int pl = lane % CP, lp = lane / CP;
+    const bool live = pl < rows;
+    const float *kr = ks + (live ? pl : 0) * rs + CPL * lp;
+    for (int hb = 0; hb < rep; hb += 4) {
+        __syncthreads(); /* K staged; previous heads' qs reads done */
+        for (int f = threadIdx.x; f < 4 * f4; f += 256) {
+            const int hh = f / f4, c4 = f - hh * f4;
+            if (hb + hh < rep)
+                *(float4 *)(qs + hh * hd + 4 * c4) =
+                    ((const float4 *)(a.q + ((size_t)t * a.nh + g * rep + hb + hh) * 2 * hd))[c4];
+        }
+        __syncthreads();
+        const int h = hb + w;
+        if (h >= rep) continue; /* uniform per wave */
+        const float *qr = qs + w * hd + CPL * lp;
+        float c[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; j++) c[j] = 0.0f;
+        for (int i = 0; i < hd; i += 16) {
+#pragma unroll
+            for (int j = 0; j < CPL; j += 4) {
+                const float4 kv = *(const float4 *)(kr + i + j);
+                const float4 qv = *(const float4 *)(qr + i + j);
+                c[j] = c[j] + qv.x * kv.x;
+                c[j + 1] = c[j + 1] + qv.y * kv.y;
+                c[j + 2] = c[j + 2] + qv.z * kv.z;
+                c[j + 3] = c[j + 3] + qv.w * kv.w;
+            }
+        }
+        float x;
+        if constexpr (LP == 2) { /* chains 8 lp .. 8 lp + 7: x = h_2lp + h_2lp+1 */
+            x = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+        } else {                 /* chains 4 lp .. 4 lp + 3: x = h_lp, then (h0 + h1), (h2 + h3) */
+            x = (c[0] + c[1]) + (c[2] + c[3]);
+            x = x + __shfl_xor(x, 16);
+        }
+        const float s = x + __shfl_xor(x, 32);
+        if (lp == 0 && live)
+            sc[((size_t)t * a.nh + g * rep + h) * a.max_ctx + p0 + pl] = (s + 0.0f) * a.scale;
+    }
+}
+
+/* Softmax and P.V (forward_attn.c:171-181, forward_ops.c:294-382, :360-382): max (exact in
+ * any order: only its value is used, and exp(x - (+-0)) agrees), e_p = exp(s_p - max) with
+ * 4 partial sums + tail, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] accumulated in p
+ * order from zero; o *= sigmoid(gate) (forward_attn.c:217-220); + A8 of o for o_proj.
+ * Workgroup = (64 output dims, head h, token t): all four waves stage V tiles of PV_TP rows
+ * (double-buffered, the next tile's loads in flight during the current tile's chain); wave 0
+ * runs the 64 per-dimension chains. */
+constexpr int PV_TP = 32;
+__global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict__ sc) {
+    extern __shared__ float4 smem4[];
+    __shared__ float red[8];
+    const int tid = threadIdx.x, d0 = blockIdx.x * 64, h = blockIdx.y, t = blockIdx.z;
+    const int hd = a.hd, g = h / (a.nh / a.nkv);
+    const int np = *a.pos + a.pos_off + t + 1;
+    float *att = (float *)smem4;                    /* [max_ctx] */
+    float *vt = att + ((a.max_ctx + 3) & ~3);       /* [2][PV_TP][64] */
+    const float *srow = sc + ((size_t)t * a.nh + h) * a.max_ctx;
+    for (int p0 = 0; p0 < np; p0 += 4 * 256) {
+        float b[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * 256 + tid;
+            b[u] = p < np ? srow[p] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * 256 + tid;
+            if (p < np) att[p] = b[u];
+        }
     }
     __syncthreads();
-    /* maximum: exact in any order (only its value is used, and exp(x - (+-0)) agrees) */
     float mx = -INFINITY;
-    for (int p = tid; p < np; p += nt) mx = fmaxf(mx, att[p]);
+    for (int p = tid; p < np; p += 256) mx = fmaxf(mx, att[p]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    mx = red[0];
-    for (int w = 1; w < nt / 64; w++) mx = fmaxf(mx, red[w]);
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
-    for (int p = tid; p < np; p += nt) att[p] = nmx_expf_cephes(att[p] - mx);
+    for (int p = tid; p < np; p += 256) att[p] = nmx_expf_cephes(att[p] - mx);
     __syncthreads();
-    const float sum = ordered_sum4(att, np, red);
-    const float inv = 1.0f / sum;
-    for (int p = tid; p < np; p += nt) att[p] = att[p] * inv;
-    __syncthreads();
-    const float *V = a.vc + (size_t)g * a.max_ctx * hd;
+    const float inv = 1.0f / ordered_sum4(att, np, red);
+    for (int p = tid; p < np; p += 256) att[p] = att[p] * inv;
+
+    /* V tiles: element (r, c4) of a tile = float4 c4 of dims d0.. of row p = tile base + r */
+    const float *V = a.vc + (size_t)g * a.max_ctx * hd + d0;
+    constexpr int PER = PV_TP * 16 / 256;
+    float4 nx[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int f = u * 256 + tid, r = f >> 4, c4 = f & 15;
+        nx[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < np) nx[u] = *(const float4 *)(V + (size_t)r * hd + 4 * c4);
+    }
     float o = 0.0f;
-    for (int p = 0; p < np; p++) o = o + att[p] * V[(size_t)p * hd + tid];
-    o = o * nmx_sigmoid(qrow[hd + tid]);
-    const int col = h * hd + tid;
-    a.o[(size_t)t * a.nh * hd + col] = o;
-    if (a.aq) a8_block(o, col >> 5, t, a.n, a.aq, a.ad, a.afs);
+    for (int base = 0, buf = 0; base < np; base += PV_TP, buf ^= 1) {
+        float *tile = vt + buf * PV_TP * 64;
+#pragma unroll
+        for (int u = 0; u < PER; u++) { /* rows past np hold zeros and are never read */
+            const int f = u * 256 + tid, r = f >> 4, c4 = f & 15;
+            *(float4 *)(tile + r * 64 + 4 * c4) = nx[u];
+        }
+        __syncthreads(); /* tile staged and att scaled */
+        const int nb = base + PV_TP;
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int f = u * 256 + tid, r = f >> 4, c4 = f & 15;
+            nx[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (nb + r < np) nx[u] = *(const float4 *)(V + (size_t)(nb + r) * hd + 4 * c4);
+        }
+        if (tid < 64) {
+            const int cnt = np - base < PV_TP ? np - base : PV_TP;
+            const float *ap = att + base;
+            if (cnt == PV_TP) {
+#pragma unroll
+                for (int r = 0; r < PV_TP; r++) o = o + ap[r] * tile[r * 64 + tid];
+            } else {
+                for (int r = 0; r < cnt; r++) o = o + ap[r] * tile[r * 64 + tid];
+            }
+        }
+    }
+    if (tid < 64) {
+        const int d = d0 + tid;
+        const float *qrow = a.q + ((size_t)t * a.nh + h) * 2 * hd;
+        o = o * nmx_sigmoid(qrow[hd + d]);
+        const int col = h * hd + d;
+        a.o[(size_t)t * a.nh * hd + col] = o;
+        if (a.aq) a8_block(o, col >> 5, t, a.n, a.aq, a.ad, a.afs);
+    }
 }
 
 /* ---- rollback commit over every linear layer (engine/src/forward_lin.c:185-204): with
@@ -421,18 +631,33 @@ int nmx_embed_q4k(nmx_ctx *ctx, const void *W, int vocab, int cols, const int32_
     return 0;
 }
 
+int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add, int add_stride,
+                   float *xo, int xo_stride, const float *w, int n, int cols, float eps, float *y,
+                   int y_stride, nmx_a8 a8) {
+    if (!ctx) return -1;
+    if (!x || !w || n < 1 || n > 4096 || cols < 1 || cols > 16384 || x_stride < cols ||
+        (add && add_stride < cols) || (y && y_stride < cols) || (xo && xo_stride < cols))
+        return nmx_fail(ctx, "nmx_rmsnorm: bad arguments n=%d cols=%d", n, cols);
+    if (a8.q && (cols % 32 || !a8.d || !a8.fs)) return nmx_fail(ctx, "nmx_rmsnorm: bad A8 output");
+    const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
+#define NMX_RMS(P)                                                                              \
+    rmsnorm_k<P><<<(unsigned)n, 256, lds, ctx->stream>>>(x, x_stride, add, add_stride, xo,      \
+                                                         xo_stride, w, cols, eps, y, y_stride,  \
+                                                         a8.q, a8.d, a8.fs, n)
+    if (cols <= 1024) NMX_RMS(4);
+    else if (cols <= 2048) NMX_RMS(8);
+    else if (cols <= 4096) NMX_RMS(16);
+    else NMX_RMS(64);
+#undef NMX_RMS
+    NMX_LAUNCHED(ctx, "rmsnorm");
+    return 0;
+}
+
 int nmx_rmsnorm(nmx_ctx *ctx, float *x, int x_stride, const float *add, int add_stride,
                 const float *w, int n, int cols, float eps, float *y, int y_stride,
                 nmx_a8 a8) {
-    if (!ctx) return -1;
-    if (!x || !w || n < 1 || n > 4096 || cols < 1 || cols > 16384 || x_stride < cols ||
-        (add && add_stride < cols) || (y && y_stride < cols))
-        return nmx_fail(ctx, "nmx_rmsnorm: bad arguments n=%d cols=%d", n, cols);
-    if (a8.q && (cols % 32 || !a8.d || !a8.fs)) return nmx_fail(ctx, "nmx_rmsnorm: bad A8 output");
-    rmsnorm_k<<<(unsigned)n, 256, (size_t)cols * 4, ctx->stream>>>(
-        x, x_stride, add, add_stride, w, cols, eps, y, y_stride, a8.q, a8.d, a8.fs, n);
-    NMX_LAUNCHED(ctx, "rmsnorm");
-    return 0;
+    return nmx_rmsnorm_xo(ctx, x, x_stride, add, add_stride, add ? x : nullptr, x_stride, w, n,
+                          cols, eps, y, y_stride, a8);
 }
 
 int nmx_lin_pre(nmx_ctx *ctx, const nmx_lin_pre_args *p) {
@@ -448,7 +673,7 @@ int nmx_lin_pre(nmx_ctx *ctx, const nmx_lin_pre_args *p) {
              p->A_log, p->A, p->dt_bias, p->beta, p->decay};
     const int groups = (p->C + p->dk - 1) / p->dk;
     const unsigned threads = p->dk < 64 ? 64 : (unsigned)p->dk;
-    lin_pre_k<<<(unsigned)(groups + 1), threads, (size_t)threads * 4, ctx->stream>>>(a);
+    lin_pre_k<<<(unsigned)(groups + 1), threads, (size_t)PRE_TB * p->dk * 4, ctx->stream>>>(a);
     NMX_LAUNCHED(ctx, "lin_pre");
     return 0;
 }
@@ -505,9 +730,17 @@ int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p) {
     if (!ctx) return -1;
     Attn a;
     if (attn_args(ctx, p, &a)) return -1;
-    dim3 grid((unsigned)p->nh, (unsigned)p->n);
-    attn_k<<<grid, (unsigned)p->hd, (size_t)p->max_ctx * 4, ctx->stream>>>(a);
-    NMX_LAUNCHED(ctx, "attn");
+    if (!p->scores) return nmx_fail(ctx, "nmx_attn: NULL scores workspace");
+    const int cp = p->hd <= 256 ? 32 : 16;
+    dim3 sgrid((unsigned)((p->max_ctx + cp - 1) / cp), (unsigned)p->n, (unsigned)p->nkv);
+    const size_t slds = ((size_t)cp * (p->hd + 4) + 4 * (size_t)p->hd) * 4;
+    if (cp == 32) attn_score_k<32><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
+    else attn_score_k<16><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
+    NMX_LAUNCHED(ctx, "attn_score");
+    dim3 pgrid((unsigned)(p->hd / 64), (unsigned)p->nh, (unsigned)p->n);
+    const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + 2 * PV_TP * 64) * 4;
+    attn_pv_k<<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
+    NMX_LAUNCHED(ctx, "attn_pv");
     return 0;
 }
 

@@ -46,6 +46,22 @@ int nmx_fail(nmx_ctx *ctx, const char *fmt, ...) __attribute__((format(printf, 2
         if (e_ != hipSuccess) return nmx_fail((ctx), "%s launch: %s", what, hipGetErrorString(e_)); \
     } while (0)
 
+/* One matrix of a small-row Q4K matmul launch. */
+struct nmx_mt_seg {
+    const uint8_t *W;
+    float *Y;
+    int rows;
+    int ystride;
+};
+
+/* Small-row Q4K matmul with every vector of a pass in one workgroup (nmx_mt.hip), optionally
+ * with the RMSNorm + A8 prologue (norm) and the SwiGLU + A8 epilogue (swiglu: segments gate,
+ * up). Returns 0, -1 on a launch error, or 1 when the shape is outside its limits. */
+int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int n,
+                  const int8_t *q, const float *d, const float *fs, const nmx_norm_in *norm,
+                  bool swiglu, nmx_a8 out);
+
+
 /* [a, a + na) and [b, b + nb) overlap (byte ranges). */
 static inline bool nmx_overlap(const void *a, size_t na, const void *b, size_t nb) {
     const char *pa = (const char *)a, *pb = (const char *)b;

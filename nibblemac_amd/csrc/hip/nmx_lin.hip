@@ -12,21 +12,47 @@
  * i in [c dk/4, (c+1) dk/4) of that column in VGPRs for the whole pass (all tokens, the
  * pending replays, the log), so the state is read from HBM once and written once. The
  * multiplies of both passes run on the 4 lanes in parallel; each ordered sum is carried lane
- * 0 -> 1 -> 2 -> 3 of the quad (the same left-to-right sequence of fp32 adds as the reference).
+ * 0 -> 1 -> 2 -> 3 of the quad by DPP (the same left-to-right sequence of fp32 adds as the
+ * reference).
  * q and k of the token are staged in LDS (broadcast reads, padded against bank conflicts).
  *
  * State layout in HBM (private to this contract, engine/src/ops.h:74-75): [heads][dv][dk],
  * i.e. column-major per head, so a lane's dk/4 keys are contiguous (128-bit loads).
  * Log rows keep the reference layout [n][heads][dk + dv + 1] = k | delta | decay. */
 #include "nmx_internal.h"
+#include "nmx_a8.h"
 
 namespace {
 
+/* The ordered sum over the quad: lane c adds its DK4 products to the running sum of lanes
+ * 0 .. c-1; the running sum moves to the next lane by a DPP broadcast of lane c within each
+ * quad (quad_perm [c, c, c, c]), so the adds form the reference's single left-to-right chain. */
 template <int DK4>
-__global__ __launch_bounds__(1024) void lin_rule_k(nmx_lin_args a) {
-    extern __shared__ float sm[]; /* [4][DK4 + 4] k, then [4][DK4 + 4] q */
-    constexpr int DK = DK4 * 4, PAD = DK4 + 4;
-    float *sk = sm, *sq = sm + 4 * PAD;
+__device__ __forceinline__ float quad_chain(const float (&p)[DK4]) {
+    float carry = 0.0f;
+#define NMX_QUAD_SEG(C)                                                                       \
+    {                                                                                         \
+        float acc = carry;                                                                    \
+        _Pragma("unroll") for (int r = 0; r < DK4; r++) acc = acc + p[r];                     \
+        carry = __int_as_float(nmx_dpp<(C) * 0x55>(__float_as_int(acc)));                     \
+    }
+    NMX_QUAD_SEG(0)
+    NMX_QUAD_SEG(1)
+    NMX_QUAD_SEG(2)
+    NMX_QUAD_SEG(3)
+#undef NMX_QUAD_SEG
+    return carry;
+}
+
+/* Tokens (or pending rows) staged per batch: their k / q rows in LDS, gates and v_j in
+ * registers, every load of a batch issued before the first is used. */
+constexpr int TB = 8;
+
+template <int DK4>
+__global__ __launch_bounds__(256) void lin_rule_k(nmx_lin_args a) {
+    extern __shared__ float sm[]; /* [TB][4][PAD] k, [TB][4][PAD] q, [TB] decay, [TB] beta */
+    constexpr int DK = DK4 * 4, PAD = DK4 + 4, ROW = 4 * PAD;
+    float *sk = sm, *sq = sm + TB * ROW, *sdec = sq + TB * ROW, *sbet = sdec + TB;
     const int h = blockIdx.x, tid = threadIdx.x, c = tid & 3;
     const int JW = blockDim.x >> 2;
     const int j = blockIdx.y * JW + (tid >> 2);
@@ -51,16 +77,44 @@ __global__ __launch_bounds__(1024) void lin_rule_k(nmx_lin_args a) {
         const int kd_ = *a.keep_dev;
         keep = kd_ < keep ? kd_ : keep;
     }
-    for (int u = 0; u < keep; u++) {
-        const float *pr = a.pend + ((size_t)u * heads + h) * logw;
-        __syncthreads();
-        for (int x = tid; x < DK; x += blockDim.x) sk[(x / DK4) * PAD + x % DK4] = pr[x];
-        __syncthreads();
-        const float pdec = pr[DK + dv], pdel = pr[DK + jj];
+    for (int u0 = 0; u0 < keep; u0 += TB) {
+        const int nb = keep - u0 < TB ? keep - u0 : TB;
+        float pdel[TB];
 #pragma unroll
-        for (int r = 0; r < DK4; r++) {
-            s[r] = s[r] * pdec;
-            s[r] = s[r] + sk[c * PAD + r] * pdel;
+        for (int u = 0; u < TB; u++)
+            pdel[u] = u < nb ? a.pend[((size_t)(u0 + u) * heads + h) * logw + DK + jj] : 0.0f;
+        __syncthreads();
+        for (int x0 = 0; x0 < nb * DK; x0 += 8 * (int)blockDim.x) {
+            float kb[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int x = x0 + e * (int)blockDim.x + tid;
+                const int xc = x < nb * DK ? x : nb * DK - 1;
+                const int u = xc / DK, i = xc - u * DK;
+                kb[e] = a.pend[((size_t)(u0 + u) * heads + h) * logw + i];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int x = x0 + e * (int)blockDim.x + tid;
+                if (x < nb * DK) {
+                    const int u = x / DK, i = x - u * DK;
+                    sk[u * ROW + (i / DK4) * PAD + i % DK4] = kb[e];
+                }
+            }
+        }
+        if (tid < nb) sdec[tid] = a.pend[((size_t)(u0 + tid) * heads + h) * logw + DK + dv];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TB; u++) {
+            if (u < nb) {
+                const float pdec = sdec[u];
+                const float *kk = sk + u * ROW + c * PAD;
+#pragma unroll
+                for (int r = 0; r < DK4; r++) {
+                    s[r] = s[r] * pdec;
+                    s[r] = s[r] + kk[r] * pdel[u];
+                }
+            }
         }
     }
 
@@ -70,73 +124,91 @@ __global__ __launch_bounds__(1024) void lin_rule_k(nmx_lin_args a) {
         for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
     }
 
-    for (int t = 0; t < a.n; t++) {
-        const float *row = a.qkv + (size_t)t * a.qkv_stride;
-        __syncthreads();
-        for (int x = tid; x < DK; x += blockDim.x) {
-            sq[(x / DK4) * PAD + x % DK4] = row[kh * DK + x];
-            sk[(x / DK4) * PAD + x % DK4] = row[kd + kh * DK + x];
-        }
-        __syncthreads();
-        const float dec = a.decay[(size_t)t * heads + h], bet = a.beta[(size_t)t * heads + h];
-        const float vj = row[2 * kd + h * dv + jj];
-
-        float p[DK4];
+    for (int t0 = 0; t0 < a.n; t0 += TB) {
+        const int nb = a.n - t0 < TB ? a.n - t0 : TB;
+        float vj[TB];
 #pragma unroll
-        for (int r = 0; r < DK4; r++) {
-            s[r] = s[r] * dec;
-            p[r] = s[r] * sk[c * PAD + r];
-        }
-        float carry = 0.0f;
+        for (int u = 0; u < TB; u++)
+            vj[u] = u < nb ? a.qkv[(size_t)(t0 + u) * a.qkv_stride + 2 * kd + h * dv + jj] : 0.0f;
+        __syncthreads(); /* the previous batch's LDS reads are done */
+        /* q / k rows of the batch: 8 elements per thread per round, loads issued first */
+        for (int x0 = 0; x0 < nb * DK; x0 += 8 * (int)blockDim.x) {
+            float qb[8], kb[8];
 #pragma unroll
-        for (int seg = 0; seg < 4; seg++) {
-            float acc = carry;
+            for (int e = 0; e < 8; e++) {
+                const int x = x0 + e * (int)blockDim.x + tid;
+                const int xc = x < nb * DK ? x : nb * DK - 1;
+                const int u = xc / DK, i = xc - u * DK;
+                const float *row = a.qkv + (size_t)(t0 + u) * a.qkv_stride;
+                qb[e] = row[kh * DK + i];
+                kb[e] = row[kd + kh * DK + i];
+            }
 #pragma unroll
-            for (int r = 0; r < DK4; r++) acc = acc + p[r];
-            carry = __shfl(acc, seg, 4);
-        }
-        const float del = (vj - carry) * bet;
-
-#pragma unroll
-        for (int r = 0; r < DK4; r++) {
-            s[r] = s[r] + sk[c * PAD + r] * del;
-            p[r] = s[r] * sq[c * PAD + r];
-        }
-        carry = 0.0f;
-#pragma unroll
-        for (int seg = 0; seg < 4; seg++) {
-            float acc = carry;
-#pragma unroll
-            for (int r = 0; r < DK4; r++) acc = acc + p[r];
-            carry = __shfl(acc, seg, 4);
-        }
-        if (live && c == 0) a.o[(size_t)t * a.o_stride + h * dv + j] = carry;
-
-        if (logged && (t > 0 || a.log0)) {
-            float *lr = a.log + ((size_t)t * heads + h) * logw;
-            if (live && c == 0) lr[DK + j] = del;
-            if (blockIdx.y == 0) {
-                for (int x = tid; x < DK; x += blockDim.x) lr[x] = sk[(x / DK4) * PAD + x % DK4];
-                if (tid == 0) lr[DK + dv] = dec;
+            for (int e = 0; e < 8; e++) {
+                const int x = x0 + e * (int)blockDim.x + tid;
+                if (x < nb * DK) {
+                    const int u = x / DK, i = x - u * DK;
+                    sq[u * ROW + (i / DK4) * PAD + i % DK4] = qb[e];
+                    sk[u * ROW + (i / DK4) * PAD + i % DK4] = kb[e];
+                }
             }
         }
-        /* the committed state: after token 0 of a reference-mode logged pass, after the last
-         * token of a plain pass */
-        const bool commit = logged ? (!a.log0 && t == 0) : (t == a.n - 1);
-        if (commit && live) {
+        if (tid < nb) {
+            sdec[tid] = a.decay[(size_t)(t0 + tid) * heads + h];
+            sbet[tid] = a.beta[(size_t)(t0 + tid) * heads + h];
+        }
+        __syncthreads();
 #pragma unroll
-            for (int r = 0; r < DK4; r += 4)
-                *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+        for (int u = 0; u < TB; u++) {
+            if (u >= nb) break;
+            const int t = t0 + u;
+            const float *kk = sk + u * ROW + c * PAD, *qq = sq + u * ROW + c * PAD;
+            const float dec = sdec[u], bet = sbet[u];
+            float p[DK4];
+#pragma unroll
+            for (int r = 0; r < DK4; r++) {
+                s[r] = s[r] * dec;
+                p[r] = s[r] * kk[r];
+            }
+            const float kv = quad_chain<DK4>(p);
+            const float del = (vj[u] - kv) * bet;
+
+#pragma unroll
+            for (int r = 0; r < DK4; r++) {
+                s[r] = s[r] + kk[r] * del;
+                p[r] = s[r] * qq[r];
+            }
+            const float ov = quad_chain<DK4>(p);
+            if (live && c == 0) a.o[(size_t)t * a.o_stride + h * dv + j] = ov;
+
+            if (logged && (t > 0 || a.log0)) {
+                float *lr = a.log + ((size_t)t * heads + h) * logw;
+                if (live && c == 0) lr[DK + j] = del;
+                if (blockIdx.y == 0) {
+                    for (int x = tid; x < DK; x += blockDim.x) lr[x] = sk[u * ROW + (x / DK4) * PAD + x % DK4];
+                    if (tid == 0) lr[DK + dv] = dec;
+                }
+            }
+            /* the committed state: after token 0 of a reference-mode logged pass, after the
+             * last token of a plain pass */
+            const bool commit = logged ? (!a.log0 && t == 0) : (t == a.n - 1);
+            if (commit && live) {
+#pragma unroll
+                for (int r = 0; r < DK4; r += 4)
+                    *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+            }
         }
     }
 }
 
 template <int DK4>
 int launch_rule(nmx_ctx *ctx, const nmx_lin_args &a) {
-    const int jw = a.dv < 256 ? a.dv : 256;
+    /* 32 value columns (128 threads) per workgroup: several workgroups per head, each with
+     * its state slice in VGPRs */
+    const int jw = a.dv < 32 ? a.dv : 32;
     dim3 grid((unsigned)a.heads, (unsigned)((a.dv + jw - 1) / jw));
     dim3 block((unsigned)(4 * jw));
-    const size_t lds = 2 * 4 * (DK4 + 4) * sizeof(float);
+    const size_t lds = (2 * TB * 4 * (DK4 + 4) + 2 * TB) * sizeof(float);
     lin_rule_k<DK4><<<grid, block, lds, ctx->stream>>>(a);
     NMX_LAUNCHED(ctx, "lin_rule");
     return 0;

@@ -1,0 +1,566 @@
+/* Q4K_G32 x A8 products of the verify step's small projections (a few thousand rows, k + 1
+ * activation rows) for gfx950, with an optional fused RMSNorm + A8 prologue and an optional
+ * fused SwiGLU + A8 epilogue.
+ *
+ * Exactness contract (the reference's kern_q4k, engine/src/kern_quant.c:148-245): for every
+ * output row r and vector v the fp32 accumulator runs over the 32-column blocks in column
+ * order, acc = fma((float)dot, (D*s)*d_v, acc); acc = fma(-(M*m), fsum_v, acc), with dot the
+ * exact int32 sum of 32 nibble x int8 products.
+ *
+ * One workgroup owns R output rows and every vector of the pass, so each weight byte is
+ * fetched once per launch. Three phases, separated by barriers:
+ *   0. the thread's weight unit (one row x half a 256-column superblock: the 64-byte scale
+ *      line and the row's four 16-byte code chunks) is loaded first; meanwhile the pass's A8
+ *      activations are staged into LDS (copied, or computed by the RMSNorm prologue);
+ *   1. every unit decodes its sub-scales and computes its 4 blocks x NV exact int32 dots with
+ *      v_dot4_i32_i8, storing ((float)dot, (D*s)*d_v) pairs and -(M*m) to LDS laid out
+ *      [block][vector][row] (up to 160 KB of LDS per workgroup on gfx950);
+ *   2. one lane per (row, vector) runs the fp32 chain over the blocks in column order, two
+ *      FMAs per block from three conflict-free LDS reads, then stores the row (or, for
+ *      SwiGLU, the workgroup combines its gate and up halves, silu(g) * u, and quantizes the
+ *      result to A8).
+ * The RMSNorm prologue restates engine/src/forward_ops.c:168-200 (sumsq as 4 interleaved
+ * partial sums + tail, r = 1 / sqrtf(ss / cols + eps), y = (x * r) * w) and the A8 of
+ * engine/src/kern_act.c:14-42, so the activations equal those of the separate kernels. */
+#include "nmx_internal.h"
+#include "nmx_math.h"
+#include "nmx_a8.h"
+
+namespace {
+
+constexpr int MT_MAX_NV = 8;
+constexpr int MT_MAX_THREADS = 1024;
+constexpr int MT_LDS = 159 * 1024; /* dynamic LDS per workgroup (gfx950: 160 KB) */
+constexpr int MT_NORM_CPT = 8; /* columns per thread in the norm prologue */
+constexpr int MT_NORM_THREADS = 512; /* the prologue keeps NV x MT_NORM_CPT values in VGPRs */
+
+struct MtTab {
+    nmx_mt_seg s[NMX_MAX_SEGS];
+    int g0[NMX_MAX_SEGS]; /* first workgroup of each segment */
+    int count;
+};
+
+__device__ __forceinline__ float half_bits(uint32_t h) {
+    const unsigned short b = (unsigned short)h;
+    _Float16 f;
+    __builtin_memcpy(&f, &b, 2);
+    return (float)f;
+}
+
+/* The four 6-bit values s[4k + i], k = 4 half .. 4 half + 3, of row i from a packed array
+ * (engine/FORMAT.md: 16 B of low nibbles, then 8 B of high bit pairs): L0..L3 the low-nibble
+ * dwords, H0 / H1 the high-pair dwords, sh8 = 8 i. */
+__device__ __forceinline__ void decode6_half(uint32_t L0, uint32_t L1, uint32_t L2, uint32_t L3,
+                                             uint32_t H0, uint32_t H1, int sh8, int half,
+                                             int out[4]) {
+    const uint32_t hs = 4u * half; /* nibble of the low bits, and the high-pair shift base */
+    const uint32_t b[4] = {(L0 >> sh8) & 0xffu, (L1 >> sh8) & 0xffu, (L2 >> sh8) & 0xffu,
+                           (L3 >> sh8) & 0xffu};
+    const uint32_t h0 = (H0 >> sh8) & 0xffu, h1 = (H1 >> sh8) & 0xffu;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t h = (k & 1) ? h1 : h0;
+        out[k] = (int)(((b[k] >> hs) & 15u) | (((h >> (hs + 2 * (k >> 1))) & 3u) << 4));
+    }
+}
+
+/* Byte offset of block b's NV x 32 activation codes in LDS: 16 bytes of padding per
+ * superblock, so the units of different superblocks read different banks. */
+__host__ __device__ constexpr int aq_off(int b, int nv) { return b * nv * 32 + (b >> 3) * 16; }
+
+__host__ __device__ constexpr int cm_stride4(int cols) { return (((cols >> 2) + 3) & ~3) + 4; }
+
+struct MtLayout {
+    int aq, ad, afs, work, res, total;
+};
+
+__host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm, bool swiglu,
+                                              bool sact) {
+    const int nb = cols >> 5;
+    MtLayout L{};
+    L.aq = 0;
+    L.ad = sact ? 0 : (aq_off(nb, nv) + 15) & ~15;
+    L.afs = L.ad + (sact ? 0 : nb * nv * 4);
+    L.work = (L.afs + (sact ? 0 : nb * nv * 4) + 15) & ~15;
+    /* ((float)dot, (D*s)*d) [nb][nv][R] float2, then -(M*m) [nb][R] */
+    int work = nb * nv * R * 8 + nb * R * 4;
+    const int nwork = nv * (4 * cm_stride4(cols) + 4) * 4;
+    if (norm && nwork > work) work = nwork;
+    L.res = L.work + work;
+    L.total = L.res + (swiglu ? nv * R * 4 : 0);
+    return L;
+}
+
+/* SACT: R == 64, so each wave's units share one half superblock and, in the chain, each
+ * wave serves one vector: the activations (codes, d, fsum) are wave-uniform and are read with
+ * scalar loads into SGPRs instead of being staged in LDS. */
+template <int NV, bool NORM, bool SWI, bool SACT>
+__global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_mt_k(
+    MtTab tab, int cols, int n, int v0, int R, const int8_t *__restrict__ q,
+    const float *__restrict__ d, const float *__restrict__ fs, nmx_norm_in nm,
+    int8_t *__restrict__ oq, float *__restrict__ od, float *__restrict__ ofs) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float red[5 * MT_MAX_NV];
+    const int tid = threadIdx.x, T = blockDim.x;
+    const int nb = cols >> 5, nsb = cols >> 8;
+    const MtLayout L = mt_layout(cols, NV, R, NORM, SWI, SACT);
+    int8_t *aq = (int8_t *)(smem + L.aq);
+    float *ad = (float *)(smem + L.ad), *afs = (float *)(smem + L.afs);
+    float2 *lp = (float2 *)(smem + L.work);  /* [nb][NV][R] ((float)dot, (D*s)*d) */
+    float *lof = (float *)(lp + nb * NV * R); /* [nb][R] -(M*m) */
+
+    /* ---- segment and rows of this workgroup ---- */
+    const int g = blockIdx.x;
+    int si = 0;
+#pragma unroll
+    for (int t = 1; t < NMX_MAX_SEGS; t++)
+        if (t < tab.count && g >= tab.g0[t]) si = t;
+    const int lg = g - tab.g0[si];
+
+    /* ---- phase 0a: first round of activation / norm-input loads, issued before the weight
+     * loads so that waiting for them does not wait for the weights ---- */
+    const int nq = nb * NV * 2, ns = nb * NV; /* 16-byte code halves; (block, vector) pairs */
+    int4 buf[8];
+    float bd[4], bf[4];
+    if constexpr (!NORM && !SACT) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = u * T + tid;
+            buf[u] = make_int4(0, 0, 0, 0);
+            if (e < nq) {
+                const int b = e / (2 * NV), rem = e - b * 2 * NV;
+                buf[u] = *(const int4 *)(q + ((size_t)b * n + v0 + (rem >> 1)) * 32 + 16 * (rem & 1));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = u * T + tid;
+            const int b = e / NV, v = e - b * NV;
+            const size_t gi = e < ns ? (size_t)b * n + v0 + v : 0;
+            bd[u] = d[gi];
+            bf[u] = fs[gi];
+        }
+    }
+    float xv[NORM ? NV : 1][MT_NORM_CPT], wv[MT_NORM_CPT];
+    if constexpr (NORM) { /* rows v0 .. v0 + NV - 1 (+ add): thread columns c = tid + T j */
+#pragma unroll
+        for (int j = 0; j < MT_NORM_CPT; j++) {
+            const int cc = tid + T * j;
+            const int ci = cc < cols ? cc : cols - 1;
+            wv[j] = 0.0f;
+#pragma unroll
+            for (int v = 0; v < NV; v++) xv[v][j] = 0.0f;
+            if (T * j >= cols) continue; /* uniform: slot unused by every thread */
+            wv[j] = nm.w[ci];
+#pragma unroll
+            for (int v = 0; v < NV; v++) xv[v][j] = nm.x[(size_t)(v0 + v) * nm.x_stride + ci];
+            if (nm.add) {
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    xv[v][j] = xv[v][j] + nm.add[(size_t)(v0 + v) * nm.add_stride + ci];
+            }
+        }
+    }
+
+    /* ---- phase 0b: weight unit loads: unit = (row u_r, half superblock u_h) ---- */
+    const bool has_unit = tid < R * 2 * nsb;
+    const int u_h = has_unit ? tid / R : 0, u_r = has_unit ? tid - u_h * R : 0;
+    const int u_sb = u_h >> 1, u_k0 = 4 * (u_h & 1);
+    int wseg = si, wrow;
+    if (SWI) { /* rows [0, R/2) gate, [R/2, R) up, both at output index lg * R/2 + r mod R/2 */
+        wseg = u_r < R / 2 ? 0 : 1;
+        wrow = lg * (R / 2) + (u_r & (R / 2 - 1));
+    } else {
+        wrow = lg * R + u_r;
+    }
+    const int wrows = tab.s[wseg].rows;
+    const int lrow = wrow < wrows ? wrow : wrows - 1;
+    const uint4 *p = (const uint4 *)(tab.s[wseg].W + ((size_t)(lrow >> 2) * nsb + u_sb) * 576);
+    const int ti = lrow & 3;
+    uint4 a0 = {}, a1 = {}, a2 = {}, a3 = {}, c[4] = {};
+    if (has_unit) {
+        a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+#pragma unroll
+        for (int k = 0; k < 4; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
+    }
+
+    /* ---- phase 0c: activations into LDS ---- */
+    if constexpr (!NORM && !SACT) {
+        for (int r0 = 0; r0 * 8 * T < nq || r0 * 4 * T < ns; r0++) {
+            if (r0 > 0) { /* rare: more than one round (very wide rows) */
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int e = (r0 * 8 + u) * T + tid;
+                    if (e < nq) {
+                        const int b = e / (2 * NV), rem = e - b * 2 * NV;
+                        buf[u] = *(const int4 *)(q + ((size_t)b * n + v0 + (rem >> 1)) * 32 + 16 * (rem & 1));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int e = (r0 * 4 + u) * T + tid;
+                    const int b = e / NV, v = e - b * NV;
+                    const size_t gi = e < ns ? (size_t)b * n + v0 + v : 0;
+                    bd[u] = d[gi];
+                    bf[u] = fs[gi];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int e = (r0 * 8 + u) * T + tid;
+                if (e < nq) {
+                    const int b = e / (2 * NV), rem = e - b * 2 * NV;
+                    *(int4 *)(aq + aq_off(b, NV) + (rem >> 1) * 32 + 16 * (rem & 1)) = buf[u];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int e = (r0 * 4 + u) * T + tid;
+                if (e < ns) {
+                    ad[e] = bd[u];
+                    afs[e] = bf[u];
+                }
+            }
+        }
+    }
+    if constexpr (NORM) {
+        /* RMSNorm (sumsq: 4 interleaved partial sums + tail, chain-major squares in LDS) */
+        const int s4 = cm_stride4(cols), rsz = 4 * s4 + 4, m4 = cols >> 2;
+        float *sq = (float *)(smem + L.work);
+#pragma unroll
+        for (int j = 0; j < MT_NORM_CPT; j++) {
+            const int cc = tid + T * j;
+            if (cc >= cols) continue;
+            const int ix = cc < 4 * m4 ? (cc & 3) * s4 + (cc >> 2) : 4 * s4 + (cc - 4 * m4);
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                sq[v * rsz + ix] = xv[v][j] * xv[v][j];
+                if (nm.x_out && blockIdx.x == 0) nm.x_out[(size_t)(v0 + v) * nm.xo_stride + cc] = xv[v][j];
+            }
+        }
+        __syncthreads();
+        if (tid < 4 * NV) { /* chain l of row v */
+            const float *ch = sq + (tid >> 2) * rsz + (tid & 3) * s4;
+            float a = 0.0f;
+            int m = 0;
+            for (; m + 32 <= m4; m += 32) {
+                float4 b[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + m + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    a = a + b[u].x;
+                    a = a + b[u].y;
+                    a = a + b[u].z;
+                    a = a + b[u].w;
+                }
+            }
+            for (; m < m4; m++) a = a + ch[m];
+            red[tid] = a;
+        } else if (tid < 5 * NV) { /* the cols % 4 tail of row v */
+            const int v = tid - 4 * NV;
+            float t = 0.0f;
+            for (int i = 4 * m4; i < cols; i++) t = t + sq[v * rsz + 4 * s4 + (i - 4 * m4)];
+            red[tid] = t;
+        }
+        __syncthreads();
+        float rv[NV];
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const float s = (red[4 * v] + red[4 * v + 1]) + (red[4 * v + 2] + red[4 * v + 3]);
+            rv[v] = 1.0f / sqrtf((s + red[4 * NV + v]) / (float)cols + nm.eps);
+        }
+#pragma unroll
+        for (int j = 0; j < MT_NORM_CPT; j++) {
+            const int cc = tid + T * j;
+            if (T * j + (tid & ~31) >= cols) continue; /* whole half-wave past the row */
+            const int b = cc >> 5;
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const float y = (xv[v][j] * rv[v]) * wv[j];
+                nmx_a8_store(y, aq + aq_off(b, NV) + v * 32, ad + b * NV + v, afs + b * NV + v);
+            }
+        }
+    }
+    __syncthreads();
+
+    /* ---- phase 1: exact int32 dots of the unit ---- */
+    if (has_unit) {
+        const int sh8 = 8 * ti;
+        const uint32_t dw = (ti & 2) ? a0.y : a0.x, mw = (ti & 2) ? a0.w : a0.z;
+        const float D = half_bits(dw >> (16 * (ti & 1)));
+        const float M = half_bits(mw >> (16 * (ti & 1)));
+        int s6[4], m6[4];
+        decode6_half(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, u_h & 1, s6);
+        decode6_half(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, u_h & 1, m6);
+        const int hs = SACT ? __builtin_amdgcn_readfirstlane(u_h) : u_h;
+        const int blk0 = (hs >> 1) * 8 + 4 * (hs & 1);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int blk = blk0 + k;
+            const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
+            const float of = M * (float)m6[k];
+            lof[blk * R + u_r] = -of;
+            const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
+            const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
+            const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
+            const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                int4 x0, x1;
+                float dv;
+                if constexpr (SACT) {
+                    const int4 *xa = (const int4 *)(q + ((size_t)blk * n + v0 + v) * 32);
+                    x0 = xa[0], x1 = xa[1];
+                    dv = d[(size_t)blk * n + v0 + v];
+                } else {
+                    const int8_t *xb = aq + aq_off(blk, NV) + v * 32;
+                    x0 = *(const int4 *)xb, x1 = *(const int4 *)(xb + 16);
+                    dv = ad[blk * NV + v];
+                }
+                int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
+                dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
+                dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
+                dot = __builtin_amdgcn_sdot4(lo3, x0.w, dot, false);
+                dot = __builtin_amdgcn_sdot4(hi0, x1.x, dot, false);
+                dot = __builtin_amdgcn_sdot4(hi1, x1.y, dot, false);
+                dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
+                dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
+                lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * dv);
+            }
+        }
+    }
+    __syncthreads();
+
+    /* ---- phase 2: the fp32 chain of (row, vector) in column order ---- */
+    const bool chain = tid < R * NV;
+    const int cv = chain ? (SACT ? __builtin_amdgcn_readfirstlane(tid / R) : tid / R) : 0;
+    const int cr = chain ? tid - cv * R : 0;
+    float acc = 0.0f;
+    if (chain) {
+        /* per block: acc = fma((float)dot, (D*s)*d_v, acc); acc = fma(-(M*m), fsum_v, acc) */
+        const float2 *pp = lp + cv * R + cr;
+        const float *op = lof + cr;
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            float2 pv[8];
+            float of[8], ff[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                pv[u] = pp[(b + u) * NV * R];
+                of[u] = op[(b + u) * R];
+                ff[u] = SACT ? fs[(size_t)(b + u) * n + v0 + cv] : afs[(b + u) * NV + cv];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = __builtin_fmaf(pv[u].x, pv[u].y, acc);
+                acc = __builtin_fmaf(of[u], ff[u], acc);
+            }
+        }
+        for (; b < nb; b++) {
+            const float2 pv = pp[b * NV * R];
+            const float ff = SACT ? fs[(size_t)b * n + v0 + cv] : afs[b * NV + cv];
+            acc = __builtin_fmaf(pv.x, pv.y, acc);
+            acc = __builtin_fmaf(op[b * R], ff, acc);
+        }
+    }
+    if constexpr (!SWI) {
+        if (chain) {
+            const int row = lg * R + cr;
+            if (row < tab.s[si].rows)
+                tab.s[si].Y[(size_t)(v0 + cv) * tab.s[si].ystride + row] = acc;
+        }
+    } else {
+        /* SwiGLU (engine/src/forward_ops.c:98-110): y = silu(gate) * up, then its A8 */
+        float *res = (float *)(smem + L.res);
+        if (chain) res[cv * R + cr] = acc;
+        __syncthreads();
+        const int H2 = R / 2; /* == 32: one A8 block per vector */
+        if (tid < NV * H2) {
+            const int v = tid / H2, j = tid - v * H2;
+            const int col = lg * H2 + j;
+            const float y = nmx_silu(res[v * R + j]) * res[v * R + H2 + j];
+            if (tab.s[0].Y) tab.s[0].Y[(size_t)(v0 + v) * tab.s[0].ystride + col] = y;
+            const size_t u = (size_t)(col >> 5) * n + v0 + v;
+            nmx_a8_store(y, oq + u * 32, od + u, ofs + u);
+        }
+    }
+}
+
+/* Rows per workgroup for a pass of nv vectors: the largest R (64, 32, ... 4) whose LDS and
+ * thread counts fit; SwiGLU needs R = 64 (32 gate + 32 up rows = one A8 block). With R = 64
+ * and no norm prologue the activations are read as scalars (sact). */
+int pick_rows(int cols, int nv, bool norm, bool swiglu, int *threads, bool *sact) {
+    const int nsb = cols >> 8;
+    for (int R = 64; R >= 4; R >>= 1) {
+        if (swiglu && R != 64) break;
+        const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
+        if (t > (norm ? MT_NORM_THREADS : MT_MAX_THREADS)) continue;
+        const bool sa = R == 64 && !norm;
+        if (mt_layout(cols, nv, R, norm, swiglu, sa).total > MT_LDS) continue;
+        if (norm && cols > t * MT_NORM_CPT) continue;
+        *threads = t;
+        *sact = sa;
+        return R;
+    }
+    return 0;
+}
+
+template <int NV, bool NORM, bool SWI, bool SACT>
+int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
+               const int8_t *q, const float *d, const float *fs, const nmx_norm_in &nm,
+               nmx_a8 out) {
+    static bool ready = false; /* idempotent: a racing second call sets the same value */
+    if (!ready) {
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI, SACT>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, MT_LDS));
+        ready = true;
+    }
+    const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI, SACT).total;
+    q4k_mt_k<NV, NORM, SWI, SACT><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
+        tab, cols, n, v0, R, q, d, fs, nm, out.q, out.d, out.fs);
+    NMX_LAUNCHED(ctx, "q4k_mt");
+    return 0;
+}
+
+template <int NV>
+int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
+              bool sact, const int8_t *q, const float *d, const float *fs, const nmx_norm_in *nm,
+              bool swiglu, nmx_a8 out) {
+    const nmx_norm_in none{};
+    if (nm && swiglu) return launch_one<NV, true, true, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (nm) return launch_one<NV, true, false, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (swiglu) {
+        if (sact) return launch_one<NV, false, true, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+        return launch_one<NV, false, true, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    }
+    if (sact) return launch_one<NV, false, false, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    return launch_one<NV, false, false, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+}
+
+} // namespace
+
+int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int n,
+                  const int8_t *q, const float *d, const float *fs, const nmx_norm_in *norm,
+                  bool swiglu, nmx_a8 out) {
+    /* more rows than one pass: the row-per-lane / K-split kernels read the weights once for
+     * all of them (prefill chunks) */
+    if (count < 1 || count > NMX_MAX_SEGS || cols % 256 || n < 1 || n > MT_MAX_NV) return 1;
+    if (swiglu && (count != 2 || segs[0].rows != segs[1].rows || segs[0].rows % 32)) return 1;
+    /* equal-size passes of at most MT_MAX_NV vectors, larger first: every pass performs the
+     * same per-vector operations, so the split does not change any result */
+    const int passes = (n + MT_MAX_NV - 1) / MT_MAX_NV;
+    int T = 0;
+    bool sact = false;
+    const int nv_max = (n + passes - 1) / passes;
+    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, &T, &sact);
+    if (!R) return 1;
+    MtTab tab{};
+    tab.count = count;
+    int groups = 0;
+    for (int s = 0; s < count; s++) {
+        tab.s[s] = segs[s];
+        tab.g0[s] = groups;
+        if (!swiglu) groups += (segs[s].rows + R - 1) / R;
+    }
+    if (swiglu) {
+        groups = segs[0].rows / (R / 2);
+        tab.g0[1] = groups; /* never selected: both halves are addressed from segment 0 */
+    }
+    for (int v0 = 0; v0 < n;) {
+        const int left = n - v0, np = (left + MT_MAX_NV - 1) / MT_MAX_NV, nv = (left + np - 1) / np;
+        const int Tn = T; /* the first (largest) pass's thread count covers every pass */
+        int rc;
+        switch (nv) {
+        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        }
+        if (rc) return rc;
+        v0 += nv;
+    }
+    return 0;
+}
+
+extern "C" {
+
+int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int *rows,
+                        float *const *Y, const int *y_stride, int cols, int n,
+                        const nmx_norm_in *in, nmx_a8 a8_tmp) {
+    if (!ctx) return -1;
+    if (!in || !in->x || !in->w || count < 1 || count > NMX_MAX_SEGS || !W || !rows || !Y ||
+        !y_stride || cols <= 0 || cols % 256 || cols > 65536 || n < 1 || n > 64 ||
+        in->x_stride < cols || (in->add && in->add_stride < cols) ||
+        (in->x_out && in->xo_stride < cols))
+        return nmx_fail(ctx, "nmx_q4k_matmul_norm: bad arguments");
+    const size_t xb = ((size_t)(n - 1) * in->x_stride + cols) * 4;
+    if (in->x_out) {
+        const size_t ob = ((size_t)(n - 1) * in->xo_stride + cols) * 4;
+        if (nmx_overlap(in->x_out, ob, in->x, xb) ||
+            (in->add && nmx_overlap(in->x_out, ob, in->add, ((size_t)(n - 1) * in->add_stride + cols) * 4)))
+            return nmx_fail(ctx, "nmx_q4k_matmul_norm: x_out aliases x or add");
+    }
+    nmx_mt_seg segs[NMX_MAX_SEGS];
+    int total = 0;
+    for (int s = 0; s < count; s++) {
+        if (!W[s] || !Y[s] || rows[s] <= 0 || rows[s] % 4 || y_stride[s] < rows[s])
+            return nmx_fail(ctx, "nmx_q4k_matmul_norm: bad matrix %d", s);
+        const size_t yb = ((size_t)(n - 1) * y_stride[s] + rows[s]) * 4;
+        if (nmx_overlap(Y[s], yb, in->x, xb) ||
+            (in->add && nmx_overlap(Y[s], yb, in->add, ((size_t)(n - 1) * in->add_stride + cols) * 4)))
+            return nmx_fail(ctx, "nmx_q4k_matmul_norm: output %d aliases the norm input", s);
+        segs[s] = nmx_mt_seg{(const uint8_t *)W[s], Y[s], rows[s], y_stride[s]};
+        total += rows[s];
+    }
+    if (total < 32768) {
+        const int rc = nmx_mt_matmul(ctx, count, segs, cols, n, nullptr, nullptr, nullptr, in,
+                                     false, nmx_a8{});
+        if (rc <= 0) return rc;
+    }
+    if (!a8_tmp.q || !a8_tmp.d || !a8_tmp.fs)
+        return nmx_fail(ctx, "nmx_q4k_matmul_norm: shape needs the a8_tmp buffers");
+    if (nmx_rmsnorm_xo(ctx, in->x, in->x_stride, in->add, in->add_stride, in->x_out,
+                       in->xo_stride, in->w, n, cols, in->eps, nullptr, 0, a8_tmp))
+        return -1;
+    return nmx_q4k_matmul_multi(ctx, count, W, rows, Y, y_stride, cols, n, a8_tmp.q, a8_tmp.d,
+                                a8_tmp.fs);
+}
+
+int nmx_q4k_swiglu(nmx_ctx *ctx, const void *Wg, const void *Wu, int ffn, int cols, int n,
+                   const int8_t *q, const float *d, const float *fsum, const nmx_norm_in *in,
+                   float *y, nmx_a8 out, nmx_a8 a8_tmp, float *gate_tmp, float *up_tmp) {
+    if (!ctx) return -1;
+    if (!Wg || !Wu || ffn <= 0 || ffn % 32 || cols <= 0 || cols % 256 || cols > 65536 || n < 1 ||
+        n > 64 || !out.q || !out.d || !out.fs || (!in && (!q || !d || !fsum)) ||
+        (in && (!in->x || !in->w || in->x_stride < cols || (in->add && in->add_stride < cols) ||
+                (in->x_out && in->xo_stride < cols))))
+        return nmx_fail(ctx, "nmx_q4k_swiglu: bad arguments");
+    if (in && in->x_out && nmx_overlap(in->x_out, ((size_t)(n - 1) * in->xo_stride + cols) * 4,
+                                       in->x, ((size_t)(n - 1) * in->x_stride + cols) * 4))
+        return nmx_fail(ctx, "nmx_q4k_swiglu: x_out aliases x");
+    const nmx_mt_seg segs[2] = {{(const uint8_t *)Wg, y, ffn, ffn}, {(const uint8_t *)Wu, nullptr, ffn, ffn}};
+    if (2 * ffn < 65536) {
+        const int rc = nmx_mt_matmul(ctx, 2, segs, cols, n, q, d, fsum, in, true, out);
+        if (rc <= 0) return rc;
+    }
+    if (!gate_tmp || !up_tmp || (in && (!a8_tmp.q || !a8_tmp.d || !a8_tmp.fs)))
+        return nmx_fail(ctx, "nmx_q4k_swiglu: shape needs the temporary buffers");
+    if (in) {
+        if (nmx_rmsnorm_xo(ctx, in->x, in->x_stride, in->add, in->add_stride, in->x_out,
+                           in->xo_stride, in->w, n, cols, in->eps, nullptr, 0, a8_tmp))
+            return -1;
+        q = a8_tmp.q, d = a8_tmp.d, fsum = a8_tmp.fs;
+    }
+    const void *W[2] = {Wg, Wu};
+    const int R[2] = {ffn, ffn};
+    float *Y[2] = {gate_tmp, up_tmp};
+    if (nmx_q4k_matmul_multi(ctx, 2, W, R, Y, R, cols, n, q, d, fsum)) return -1;
+    return nmx_silu_mul(ctx, gate_tmp, up_tmp, ffn, n, ffn, y, out);
+}
+
+} /* extern "C" */

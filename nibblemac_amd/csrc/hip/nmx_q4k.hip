@@ -18,6 +18,7 @@
  *     once per superblock.
  * Several matrices that share one input run in one launch (segment table). */
 #include "nmx_internal.h"
+#include "nmx_a8.h"
 
 namespace {
 
@@ -340,27 +341,12 @@ __global__ __launch_bounds__(1024) void q4k_mv_ks_k(SegTable tab, int cols, int 
 __global__ __launch_bounds__(256) void quant_a8_k(const float *__restrict__ X, int n, int cols,
                                                   int8_t *__restrict__ q, float *__restrict__ d,
                                                   float *__restrict__ fs) {
-    const int unit = (blockIdx.x * 256 + threadIdx.x) >> 5, j = threadIdx.x & 31;
+    const int unit = (blockIdx.x * 256 + threadIdx.x) >> 5;
     const int nb = cols >> 5;
-    const bool live = unit < nb * n;
-    const int u = live ? unit : 0;
-    const int b = u / n, v = u - b * n;
-    const float x = X[(size_t)v * cols + b * 32 + j];
-    float amax = fabsf(x);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
-    const int c = (int)rintf(x * id);
-    int sum = c;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
-    if (!live) return;
-    q[(size_t)u * 32 + j] = (int8_t)(c > 127 ? 127 : c < -128 ? -128 : c);
-    if (j == 0) {
-        const float dd = amax / 127.0f;
-        d[u] = dd;
-        fs[u] = dd * (float)sum;
-    }
+    if (unit >= nb * n) return; /* the whole half-wave leaves together */
+    const int b = unit / n, v = unit - b * n;
+    const float x = X[(size_t)v * cols + b * 32 + (threadIdx.x & 31)];
+    nmx_a8_store(x, q + (size_t)unit * 32, d + unit, fs + unit);
 }
 
 template <int NV>
@@ -398,6 +384,13 @@ int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8
                   const float *d, const float *fs, int32_t *dots, unsigned long long *am = nullptr) {
     int total_rows = 0;
     for (int s = 0; s < tab.count; s++) total_rows += tab.s[s].rows;
+    if (!am && !dots && total_rows < KSPLIT_MAX_ROWS) {
+        nmx_mt_seg segs[NMX_MAX_SEGS];
+        for (int s = 0; s < tab.count; s++)
+            segs[s] = nmx_mt_seg{tab.s[s].W, tab.s[s].Y, tab.s[s].rows, tab.s[s].ystride};
+        const int rc = nmx_mt_matmul(ctx, tab.count, segs, cols, n, q, d, fs, nullptr, false, nmx_a8{});
+        if (rc <= 0) return rc;
+    }
     if (!am && total_rows < KSPLIT_MAX_ROWS && cols <= 16 * 2 * 256)
         return launch_ksplit(ctx, tab, tab.total_waves, cols, n, q, d, fs, dots);
     /* n vectors in ceil(n / MAX_NV) passes of equal size (+-1), larger first, like the

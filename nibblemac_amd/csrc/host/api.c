@@ -29,7 +29,12 @@ pinfer_spec_params pinfer_default_spec_params(void) {
 
 static void *dalloc(pinfer_ctx *c, size_t bytes, int *ok) {
     if (!*ok) return NULL;
+    if (c->n_allocs == E_MAX_ALLOCS) {
+        *ok = 0;
+        return NULL;
+    }
     void *p = nmx_alloc(c->dev, bytes ? bytes : 4);
+    if (p) c->allocs[c->n_allocs++] = p;
     if (!p || nmx_fill_zero(c->dev, p, bytes ? bytes : 4)) {
         *ok = 0;
         return NULL;
@@ -98,6 +103,7 @@ static int alloc_state(pinfer_ctx *c) {
     const int wb = imax(imax(c->vd, kvw), c->ffn);
     const int wide = imax(imax(c->vd, c->n_heads * c->hd), 2 * H);
     s->x = dalloc(c, (size_t)B * H * 4, &ok);
+    s->x2 = dalloc(c, (size_t)B * H * 4, &ok);
     s->xn = dalloc(c, (size_t)B * H * 4, &ok);
     s->out = dalloc(c, (size_t)B * H * 4, &ok);
     s->ta = dalloc(c, (size_t)B * wa * 4, &ok);
@@ -111,6 +117,7 @@ static int alloc_state(pinfer_ctx *c) {
     s->decay = dalloc(c, (size_t)B * c->lv_heads * 4, &ok);
     s->cat = dalloc(c, (size_t)B * 2 * H * 4, &ok);
     s->emb = dalloc(c, (size_t)B * H * 4, &ok);
+    s->sc = dalloc(c, (size_t)B * imax(c->n_heads, 1) * c->max_ctx * 4, &ok);
     s->row1 = dalloc(c, (size_t)H * 4, &ok);
     s->a_h = a8_alloc(c, H, B, &ok);
     s->a_w = a8_alloc(c, wide, B, &ok);
@@ -175,15 +182,8 @@ void pinfer_free(pinfer_ctx *c) {
     if (c->dev) {
         e_drop_graphs(c);
         nmx_sync(c->dev);
-        /* every device allocation of the context */
-        void *ptrs[] = {c->blob, c->conv_state, c->rec, c->kc, c->vc, c->mkc, c->mvc, c->xin,
-                        c->log, c->pend, c->rope_cos, c->rope_sin, c->s.x, c->s.xn, c->s.out,
-                        c->s.ta, c->s.tb, c->s.tc, c->s.to, c->s.conv, c->s.ba, c->s.aa,
-                        c->s.beta, c->s.decay, c->s.cat, c->s.emb, c->s.row1, c->s.a_h.q,
-                        c->s.a_h.d, c->s.a_h.fs, c->s.a_w.q, c->s.a_w.d, c->s.a_w.fs, c->s.a_f.q,
-                        c->s.a_f.d, c->s.a_f.fs, c->s.a_1.q, c->s.a_1.d, c->s.a_1.fs, c->hbuf,
-                        c->mbuf, c->ctl, c->vt, c->tok, c->hout, c->hout2, c->hwork, c->logits};
-        for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; i++) nmx_free(c->dev, ptrs[i]);
+        nmx_free(c->dev, c->blob);
+        for (int i = 0; i < c->n_allocs; i++) nmx_free(c->dev, c->allocs[i]);
         nmx_destroy(c->dev);
     }
     free(c->layers);
@@ -295,5 +295,18 @@ int pinfer_generate_greedy(pinfer_ctx *c, const int32_t *prompt, int n_prompt, i
     int status;
     const int n = pinfer_generate_greedy_ex(c, prompt, n_prompt, out, n_max, sp, NULL, stats,
                                             &status);
+    return status != PINFER_OK ? status : n;
+}
+
+/* The timing of the reference CLI's benchmark (engine/tools/pinfer_run.c:384-397,425-430):
+ * reset, prefill the prompt (timed), then generate n_gen tokens ignoring EOS (timed); decode
+ * tok/s is (n_gen - 1) / decode seconds. Returns the count or a negative PINFER_E* code. */
+int pinfer_bench_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
+                          int n_gen, const pinfer_spec_params *sp, pinfer_spec_stats *stats,
+                          double *prefill_s, double *decode_s) {
+    int status;
+    if (c) pinfer_reset(c);
+    const int n = e_generate_timed(c, prompt, n_prompt, out, n_gen, sp, NULL, stats, &status, 1,
+                                   prefill_s, decode_s);
     return status != PINFER_OK ? status : n;
 }

@@ -12,6 +12,7 @@
 
 #define E_MAX_BATCH 64   /* rows per forward chunk (the reference's PF_MAX_BATCH) */
 #define E_MAX_K PINFER_SPEC_MAX_K
+#define E_MAX_ALLOCS 96  /* device allocations per context besides the weight blob */
 
 /* .pq dtypes and layout constants (engine/src/pq_format.h, pq_quant.h) */
 enum { PQ_F32 = 0, PQ_BF16 = 1, PQ_Q4K = 4 };
@@ -37,7 +38,8 @@ typedef struct {
 
 /* one set of per-row scratch buffers (E_MAX_BATCH rows) */
 typedef struct {
-    float *x, *xn, *out, *ta, *tb, *tc, *to, *conv, *ba, *aa, *beta, *decay, *cat, *emb;
+    float *x, *x2, *xn, *out, *ta, *tb, *tc, *to, *conv, *ba, *aa, *beta, *decay, *cat, *emb;
+    float *sc; /* attention scores [B][n_heads][max_ctx] */
     nmx_a8 a_h;        /* A8 of width hidden */
     nmx_a8 a_w;        /* A8 of the wide inputs: vd, n_heads * head_dim, 2 * hidden */
     nmx_a8 a_f;        /* A8 of width ffn */
@@ -94,6 +96,8 @@ struct pinfer_ctx {
     nmx_graph *g_verify[E_MAX_K + 1], *g_commit[E_MAX_K + 1];
     int graph_nv;             /* draft vocabulary the graphs were captured with */
     int use_graphs;
+    void *allocs[E_MAX_ALLOCS]; /* every device allocation besides the weight blob */
+    int n_allocs;
 };
 
 /* forward.c */
@@ -107,6 +111,10 @@ int e_set_pos(pinfer_ctx *c, int pos);
 int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out, int n_max,
                const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
                pinfer_spec_stats *stats, int *status);
+int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
+                     int n_max, const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
+                     pinfer_spec_stats *stats, int *status, int no_eos, double *t_prefill,
+                     double *t_decode);
 void e_drop_graphs(pinfer_ctx *c);
 
 /* model.c */

@@ -4,7 +4,8 @@
  * kernel on the context's stream. Nothing here touches the host copy of any activation, so a
  * sequence can be captured into a HIP graph; positions come from the control block c->ctl
  * (ctl[0] = n_past at the start of the pass). Residual adds are fused into the following
- * RMSNorm and every matmul input is A8-quantized by the kernel that produces it. */
+ * RMSNorm, SwiGLU into the gate/up matmul's epilogue, and every matmul input is A8-quantized
+ * by the kernel that produces it. */
 #include <math.h>
 #include <stdio.h>
 
@@ -18,6 +19,12 @@
         }                                                                                     \
     } while (0)
 
+#define TRY(expr)                                                                             \
+    do {                                                                                      \
+        int rc_ = (expr);                                                                     \
+        if (rc_ != PINFER_OK) return rc_;                                                     \
+    } while (0)
+
 int e_set_pos(pinfer_ctx *c, int pos) {
     CK(nmx_ctl_set(c->dev, c->ctl, 0, pos));
     return PINFER_OK;
@@ -25,8 +32,31 @@ int e_set_pos(pinfer_ctx *c, int pos) {
 
 static size_t kv_layer(const pinfer_ctx *c) { return (size_t)c->n_kv * c->max_ctx * c->hd; }
 
-/* mix + MLP of one full-attention block on rows s->x (A8 of the normed input already in a_h);
- * kc / vc: the block's caches; pos_off: position of row 0 relative to ctl[0]. */
+/* The residual stream: rows in one of two buffers; a fused norm reads the current one (plus
+ * the pending residual add) and writes the sum to the other, which becomes current. */
+typedef struct {
+    float *cur, *alt;
+    const float *add; /* residual to add before the next norm (NULL: none) */
+} e_resid;
+
+/* RMSNorm of cur (+ add, the sum then current) into the A8 buffers a (the next matmul's
+ * input). A separate launch: on gfx950 it costs less than the same norm as a matmul prologue
+ * (nmx_q4k_matmul_norm), whose workgroups would each redo it. */
+static int norm_a8(pinfer_ctx *c, e_resid *r, const float *w, int n, nmx_a8 a) {
+    CK(nmx_rmsnorm_xo(c->dev, r->cur, c->H, r->add, c->H, r->add ? r->alt : NULL, c->H, w, n,
+                      c->H, c->rms_eps, NULL, 0, a));
+    if (r->add) {
+        float *t = r->cur;
+        r->cur = r->alt;
+        r->alt = t;
+        r->add = NULL;
+    }
+    return PINFER_OK;
+}
+
+/* Gated full attention (engine/src/forward_attn.c:231-266) on the normed rows (A8 in s->a_h):
+ * q (query | gate per head), k, v in one launch; kc / vc: the block's caches; pos_off:
+ * position of row 0 relative to ctl[0]. Output (o_proj) to s->out. */
 static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *vc, int pos_off) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
@@ -37,7 +67,7 @@ static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *
     CK(nmx_q4k_matmul_multi(D, 3, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
     nmx_attn_args a = {n, c->n_heads, c->n_kv, hd, c->rot, c->max_ctx, s->ta, s->tb, s->tc,
                        L->q_norm, L->k_norm, c->rms_eps, 1.0f / sqrtf((float)hd), c->rope_cos,
-                       c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w};
+                       c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w, s->sc};
     CK(nmx_attn_prep(D, &a));
     CK(nmx_attn(D, &a));
     CK(nmx_q4k_matmul(D, L->o.w, H, c->n_heads * hd, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->out,
@@ -46,24 +76,23 @@ static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *
 }
 
 /* post norm + SwiGLU MLP (engine/src/forward.c:49-58): x += mix out; xn = norm(x);
- * out = down(silu(gate xn) * up xn). */
-static int mlp_block(pinfer_ctx *c, const e_layer *L, int n) {
+ * out = down(silu(gate xn) * up xn); the norm and the SwiGLU fused into the gate/up launch. */
+static int mlp_block(pinfer_ctx *c, const e_layer *L, int n, e_resid *r) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H, F = c->ffn;
-    CK(nmx_rmsnorm(D, s->x, H, s->out, H, L->post_norm, n, H, c->rms_eps, NULL, 0, s->a_h));
-    const void *W[2] = {L->gate.w, L->up.w};
-    const int R[2] = {F, F};
-    float *Y[2] = {s->ta, s->tb};
-    CK(nmx_q4k_matmul_multi(D, 2, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
-    CK(nmx_silu_mul(D, s->ta, s->tb, F, n, F, NULL, s->a_f));
+    r->add = s->out;
+    TRY(norm_a8(c, r, L->post_norm, n, s->a_h));
+    CK(nmx_q4k_swiglu(D, L->gate.w, L->up.w, F, H, n, s->a_h.q, s->a_h.d, s->a_h.fs, NULL, NULL,
+                      s->a_f, s->a_h, s->ta, s->tb));
     CK(nmx_q4k_matmul(D, L->down.w, H, F, n, s->a_f.q, s->a_f.d, s->a_f.fs, s->out, H, NULL));
+    r->add = s->out;
     return PINFER_OK;
 }
 
-/* Gated DeltaNet mixer (engine/src/forward_lin.c:94-133). logged: a verify pass (token 0
- * committed in place, tokens 1.. logged for the commit); pending replays of the last commit
- * are applied first (keep = ctl[2]). */
+/* Gated DeltaNet mixer (engine/src/forward_lin.c:94-133) on the normed rows (A8 in s->a_h).
+ * logged: a verify pass (token 0 committed in place, tokens 1.. logged for the commit);
+ * pending replays of the last commit are applied first (keep = ctl[2]). */
 static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
@@ -97,19 +126,18 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H;
-    CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, s->x, H));
-    const float *add = NULL;
+    e_resid r = {s->x, s->x2, NULL};
+    CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, r.cur, H));
     for (int l = 0; l < c->n_layers; l++) {
         const e_layer *L = &c->layers[l];
-        CK(nmx_rmsnorm(D, s->x, H, add, H, L->in_norm, n, H, c->rms_eps, NULL, 0, s->a_h));
+        TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
         int rc = L->is_full ? attn_block(c, L, n, c->kc + (size_t)L->full * kv_layer(c),
                                          c->vc + (size_t)L->full * kv_layer(c), 0)
                             : lin_block(c, L, n, logged);
         if (rc) return rc;
-        if ((rc = mlp_block(c, L, n))) return rc;
-        add = s->out;
+        if ((rc = mlp_block(c, L, n, &r))) return rc;
     }
-    CK(nmx_rmsnorm(D, s->x, H, add, H, c->norm, n, H, c->rms_eps, s->xn, H, s->a_h));
+    CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->norm, n, H, c->rms_eps, s->xn, H, s->a_h));
     CK(nmx_ctl_set(D, c->ctl, 2, 0)); /* every linear layer applied the pending rows */
     return PINFER_OK;
 }
@@ -148,13 +176,15 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     CK(nmx_rmsnorm(D, (float *)h_dev, H, NULL, 0, c->mtp_norm_hid, n, H, c->rms_eps, s->cat + H,
                    2 * H, none));
     CK(nmx_quant_a8(D, s->cat, n, 2 * H, s->a_w.q, s->a_w.d, s->a_w.fs));
-    CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->x, H, NULL));
+    e_resid r = {s->x, s->x2, NULL};
+    CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H, NULL));
     const e_layer *L = &c->mtp;
-    CK(nmx_rmsnorm(D, s->x, H, NULL, 0, L->in_norm, n, H, c->rms_eps, NULL, 0, s->a_h));
+    TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
     int rc = attn_block(c, L, n, c->mkc, c->mvc, pos_off);
     if (rc) return rc;
-    if ((rc = mlp_block(c, L, n))) return rc;
-    CK(nmx_rmsnorm(D, s->x, H, s->out, H, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H, none));
+    if ((rc = mlp_block(c, L, n, &r))) return rc;
+    CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H,
+                      none));
     const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
     const int off = head_row_dynamic ? -1 : n - 1;
     if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));

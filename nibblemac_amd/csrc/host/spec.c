@@ -11,9 +11,11 @@
  * Both graphs are captured once per draft count and replayed at any position (the kernels read
  * n_past, e and keep from the device control block). Tokens emitted equal plain greedy
  * decoding whatever the drafts are. */
+#define _POSIX_C_SOURCE 200809L
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "engine.h"
 
@@ -208,9 +210,16 @@ static int flush_pending(pinfer_ctx *c, int *pend_n, int pend_pos, const int32_t
     return PINFER_OK;
 }
 
-int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out, int n_max,
-               const pinfer_spec_params *sp_in, const pinfer_gen_opts *opts,
-               pinfer_spec_stats *st, int *status) {
+static double now_sec(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
+}
+
+int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
+                     int n_max, const pinfer_spec_params *sp_in, const pinfer_gen_opts *opts,
+                     pinfer_spec_stats *st, int *status, int no_eos, double *t_prefill,
+                     double *t_decode) {
     pinfer_spec_params plain = {0, 0, 0, 0};
     const pinfer_spec_params *sp = sp_in ? sp_in : &plain;
     int dummy;
@@ -225,12 +234,15 @@ int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
         if (prompt[i] < 0 || prompt[i] >= c->vocab) return *status = PINFER_E_ARG;
     if (n_prompt > c->max_ctx - c->n_past) return *status = PINFER_E_CTX_FULL;
     const int use_mtp = sp->k > 0, nv = draft_vocab(c, sp);
-    e_stop stop = {c->eos, opts ? opts->stop_ids : NULL, opts ? opts->n_stop : 0,
+    e_stop stop = {no_eos ? -1 : c->eos, opts ? opts->stop_ids : NULL, opts ? opts->n_stop : 0,
                    opts ? opts->on_token : NULL, opts ? opts->user : NULL};
+    const double t0 = now_sec();
     int rc = prefill(c, prompt, n_prompt, use_mtp, nv);
     if (rc != PINFER_OK) return *status = rc;
     int32_t cur;
     if (nmx_download(c->dev, &cur, c->vt, sizeof cur)) return *status = PINFER_E_ARG;
+    const double t1 = now_sec();
+    if (t_prefill) *t_prefill = t1 - t0;
     int count = 0, done = emit(out, &count, n_max, cur, &stop);
     int pend_n = 0, pend_pos = 0;
     int32_t pend_tok[E_MAX_K + 2];
@@ -278,6 +290,13 @@ int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
     int frc = lin_flush(c);
     if (rc == PINFER_OK) rc = frc;
     if (nmx_sync(c->dev) && rc == PINFER_OK) rc = PINFER_E_ARG;
+    if (t_decode) *t_decode = now_sec() - t1;
     *status = rc;
     return count;
+}
+
+int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out, int n_max,
+               const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
+               pinfer_spec_stats *st, int *status) {
+    return e_generate_timed(c, prompt, n_prompt, out, n_max, sp, opts, st, status, 0, NULL, NULL);
 }

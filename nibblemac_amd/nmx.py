@@ -33,6 +33,19 @@ class LinArgs(ctypes.Structure):
                 ("keep", _i), ("log0", _i), ("keep_dev", _vp)]
 
 
+class A8(ctypes.Structure):
+    """Mirror of nmx_a8: block-major int8 codes, per-block scale d and d * sum(codes)."""
+
+    _fields_ = [("q", _vp), ("d", _vp), ("fs", _vp)]
+
+
+class NormIn(ctypes.Structure):
+    """Mirror of nmx_norm_in (the RMSNorm input of a fused matmul)."""
+
+    _fields_ = [("x", _vp), ("x_stride", _i), ("add", _vp), ("add_stride", _i), ("x_out", _vp),
+                ("xo_stride", _i), ("w", _vp), ("eps", ctypes.c_float)]
+
+
 _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_create": (_vp, [_i]),
     "nmx_create_error": (ctypes.c_char_p, []),
@@ -62,6 +75,13 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_lin_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "nmx_head_work_bytes": (_sz, [_i, _i]),
     "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nmx_rmsnorm_xo": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _i,
+                            A8]),
+    "nmx_silu_mul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, A8]),
+    "nmx_q4k_matmul_norm": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, ctypes.POINTER(NormIn),
+                                 A8]),
+    "nmx_q4k_swiglu": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, ctypes.POINTER(NormIn),
+                            _vp, A8, A8, _vp, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -237,6 +257,41 @@ class Device:
         self.check(self.lib.nmx_q4k_matmul_multi(self.ctx, c, w, r, y, s, cols, n, _p(q), _p(d),
                                                  _p(fs)), "q4k_matmul_multi")
 
+
+    def rmsnorm(self, x, n: int, cols: int, w, eps: float, *, add=None, xo=None, y=None,
+                a8=(None, None, None)) -> None:
+        """Rows [n][cols] (contiguous): xo = x + add (if given), y / a8 of rmsnorm(...) * w."""
+        self.check(self.lib.nmx_rmsnorm_xo(self.ctx, _p(x), cols, _p(add), cols, _p(xo), cols,
+                                           _p(w), n, cols, eps, _p(y), cols,
+                                           A8(*[_p(t) for t in a8])), "rmsnorm")
+
+    def silu_mul(self, gate, up, n: int, cols: int, y=None, a8=(None, None, None)) -> None:
+        self.check(self.lib.nmx_silu_mul(self.ctx, _p(gate), _p(up), cols, n, cols, _p(y),
+                                         A8(*[_p(t) for t in a8])), "silu_mul")
+
+    def q4k_matmul_norm(self, Ws, rows, Ys, cols: int, n: int, x, w, eps: float, *, add=None,
+                        xo=None, a8_tmp=(None, None, None)) -> None:
+        c = len(Ws)
+        arr = lambda t, xs: (t * c)(*xs)  # noqa: E731
+        nin = NormIn(_p(x), cols, _p(add), cols, _p(xo), cols, _p(w), eps)
+        self.check(self.lib.nmx_q4k_matmul_norm(
+            self.ctx, c, arr(ctypes.c_void_p, [_p(t) for t in Ws]), arr(ctypes.c_int, rows),
+            arr(ctypes.c_void_p, [_p(t) for t in Ys]), arr(ctypes.c_int, rows), cols, n,
+            ctypes.byref(nin), A8(*[_p(t) for t in a8_tmp])), "q4k_matmul_norm")
+
+    def q4k_swiglu(self, Wg, Wu, ffn: int, cols: int, n: int, out, *, a8=(None, None, None),
+                   norm=None, y=None, a8_tmp=(None, None, None), gate_tmp=None,
+                   up_tmp=None) -> None:
+        """norm: (x, w, eps, add, xo) for the fused RMSNorm input, else the A8 input a8."""
+        nin = None
+        if norm is not None:
+            x, w, eps, add, xo = norm
+            nin = ctypes.byref(NormIn(_p(x), cols, _p(add), cols, _p(xo), cols, _p(w), eps))
+        q, d, fs = [_p(t) for t in a8]
+        self.check(self.lib.nmx_q4k_swiglu(self.ctx, _p(Wg), _p(Wu), ffn, cols, n, q, d, fs, nin,
+                                           _p(y), A8(*[_p(t) for t in out]),
+                                           A8(*[_p(t) for t in a8_tmp]), _p(gate_tmp),
+                                           _p(up_tmp)), "q4k_swiglu")
 
     def lin_rule(self, *, n, heads, rep, dk, dv, qkv_stride, o_stride, qkv, decay, beta, S, o,
                  log=None, pend=None, keep=0, log0=False) -> None:

@@ -23,10 +23,12 @@ class Model:
     """A loaded .pq model on the MI355X."""
 
     def __init__(self, path: str, max_ctx: int = 4096, lib: Lib | None = None,
-                 lib_path: str | None = None):
+                 lib_path: str | None = None, n_threads: int | None = None):
         self.lib = lib or load_library(lib_path)
         p = self.lib.pinfer_default_params()
         p.max_ctx = max_ctx
+        if n_threads is not None:
+            p.n_threads = n_threads
         err = ctypes.c_int(0)
         self.ctx = self.lib.pinfer_load(str(path).encode(), ctypes.byref(p), ctypes.byref(err))
         if not self.ctx:
@@ -78,3 +80,21 @@ class Model:
         if n < 0 or (status.value != 0 and n == 0):
             raise PinferError(status.value or n, "pinfer_generate_greedy")
         return [int(x) for x in out[:n]], st
+
+    def bench_generate(self, prompt, n_gen: int, k: int = 4, draft_vocab: int = 32768):
+        """The reference CLI's benchmark timing (engine/tools/pinfer_run.c:384-430): reset,
+        prefill, then exactly n_gen tokens with EOS ignored. Returns (tokens, stats, prefill
+        seconds, decode seconds); decode tok/s is (n_gen - 1) / decode seconds."""
+        if self.lib.pinfer_bench_generate is None:
+            raise PinferError(-4, f"{self.lib.path} has no pinfer_bench_generate")
+        t = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(n_gen, np.int32)
+        sp, st = SpecParams(k, draft_vocab, 0, 0), SpecStats()
+        tp, td = ctypes.c_double(0.0), ctypes.c_double(0.0)
+        n = self.lib.pinfer_bench_generate(
+            self.ctx, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), t.size,
+            out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), n_gen, ctypes.byref(sp),
+            ctypes.byref(st), ctypes.byref(tp), ctypes.byref(td))
+        if n != n_gen:
+            raise PinferError(n if n < 0 else -4, f"pinfer_bench_generate returned {n}")
+        return [int(x) for x in out], st, tp.value, td.value

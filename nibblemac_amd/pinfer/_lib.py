@@ -69,6 +69,11 @@ _OPTIONAL = {
     "pinfer_generate_greedy_cont": (ctypes.c_int, _GEN_EX),
     "pinfer_eval_select": (ctypes.c_int, [ctypes.c_void_p, _c_int32_p, ctypes.c_int, _c_int32_p,
                                           ctypes.c_int, _c_float_p]),
+    "pinfer_bench_generate": (ctypes.c_int, [ctypes.c_void_p, _c_int32_p, ctypes.c_int, _c_int32_p,
+                                             ctypes.c_int, ctypes.POINTER(SpecParams),
+                                             ctypes.POINTER(SpecStats),
+                                             ctypes.POINTER(ctypes.c_double),
+                                             ctypes.POINTER(ctypes.c_double)]),
 }
 
 

@@ -12,6 +12,7 @@ replays), and the 0.8B shape itself.
 """
 from __future__ import annotations
 
+import os
 from dataclasses import replace
 
 import numpy as np
@@ -19,6 +20,7 @@ import pytest
 
 from nibblemac_amd import pqfile
 from nibblemac_amd.pinfer import Model
+from nibblemac_amd.synth import QWEN35_08B
 from oracle import HERE as ORACLE_DIR
 
 pytestmark = pytest.mark.gpu
@@ -41,7 +43,9 @@ def pair(path, max_ctx=512):
     from nibblemac_amd.pinfer import load_library
 
     ref_lib = load_library(str(REF))
-    return Model(str(path), max_ctx=max_ctx), Model(str(path), max_ctx=max_ctx, lib=ref_lib)
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    return (Model(str(path), max_ctx=max_ctx),
+            Model(str(path), max_ctx=max_ctx, lib=ref_lib, n_threads=threads))
 
 
 def bits(a):
@@ -115,6 +119,27 @@ def test_generate_continuation_and_stop_ids(models):
     sg_, _ = gpu.generate(prompt, 30, k=4, draft_vocab=1024, stop_ids=stop)
     sr_, _ = ref.generate(prompt, 30, k=4, draft_vocab=1024, stop_ids=stop)
     assert sg_ == sr_ and sg_[-1] == stop[0]
+    gpu.close(), ref.close()
+
+
+@needs_ref
+def test_qwen35_08b_shape(tmp_path):
+    """The 0.8B shape itself (24 layers, vocab 248320, tied Q4K head, MTP): prefill logits
+    bit-exact, then the benchmark sequence (prefill, k = 4 decode with EOS ignored) generating
+    the same tokens and statistics as the reference engine."""
+    path = pqfile.write_model(tmp_path / "q08.pq", QWEN35_08B, seed=1)
+    gpu, ref = pair(path, max_ctx=256)
+    prompt = np.random.default_rng(8).integers(0, QWEN35_08B.vocab, 12)
+    print("[case] 0.8B shape eval 12 tokens", flush=True)
+    a, b = gpu.eval(prompt), ref.eval(prompt)
+    assert np.array_equal(bits(a), bits(b)), f"max diff {np.abs(a - b).max()}"
+    print("[case] 0.8B shape generate 9 tokens k=4", flush=True)
+    tg, sg = gpu.generate(prompt, 9, k=4, draft_vocab=32768)
+    tr, sr = ref.generate(prompt, 9, k=4, draft_vocab=32768)
+    assert tg == tr
+    assert (sg.rounds, sg.drafted, sg.accepted) == (sr.rounds, sr.drafted, sr.accepted)
+    toks, st, tp, td = gpu.bench_generate(prompt, 9, k=4, draft_vocab=32768)
+    assert toks[:len(tg)] == tg and tp > 0 and td > 0
     gpu.close(), ref.close()
 
 

@@ -1,0 +1,136 @@
+"""GPU parity of the fused entry points against the separate kernels they replace.
+
+nmx_q4k_matmul_norm = nmx_rmsnorm_xo (residual add + RMSNorm + A8) followed by the Q4K matmul;
+nmx_q4k_swiglu = [RMSNorm + A8 +] gate / up matmuls + nmx_silu_mul (+ A8). Bar: bit-exact
+(outputs, the residual sum, and the A8 codes / scales of the SwiGLU output). Shapes cover the
+fused kernel (every 0.8B projection at 1..8 rows), several vector passes (13, 64 rows) and the
+fallback to the separate kernels (widths whose workgroup tile does not fit in LDS). The
+separate kernels are themselves checked against the oracle (test_gpu_q4k.py) and, through the
+reference engine, against the reference's RMSNorm and SwiGLU (test_gpu_e2e.py); the RMSNorm is
+also checked here against a float32 restatement of its summation order.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.test_gpu_q4k import assert_bits_equal, gaussian_q4k
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def rmsnorm_restated(x, w, eps):
+    """engine/src/forward_ops.c:168-200 in float32: 4 interleaved partial sums of squares over
+    the first cols/4*4 columns, (c0 + c1) + (c2 + c3) + tail, r = 1 / sqrtf(ss / cols + eps),
+    y = (x * r) * w."""
+    x = x.astype(np.float32)
+    n, cols = x.shape
+    sq = x * x
+    c = np.zeros((n, 4), np.float32)
+    m4 = cols // 4
+    for m in range(m4):
+        c = c + sq[:, 4 * m:4 * m + 4]
+    t = np.zeros(n, np.float32)
+    for i in range(4 * m4, cols):
+        t = t + sq[:, i]
+    s = ((c[:, 0] + c[:, 1]) + (c[:, 2] + c[:, 3])) + t
+    r = np.float32(1.0) / np.sqrt(s / np.float32(cols) + np.float32(eps))
+    return (x * r[:, None]) * w[None, :]
+
+
+def a8_bufs(dev, n, cols):
+    return (dev.zeros((cols // 32, n, 32), np.int8), dev.zeros((cols // 32, n), np.float32),
+            dev.zeros((cols // 32, n), np.float32))
+
+
+@pytest.mark.parametrize("cols,shapes", [(1024, [6144, 2048, 16, 16]), (1024, [4096, 512, 512]),
+                                         (2048, [1024]), (3584, [1024]), (8192, [64])])
+@pytest.mark.parametrize("n", [1, 5, 8, 13, 64])
+def test_matmul_norm_equals_separate(dev, cols, shapes, n):
+    print(f"[case] matmul_norm cols={cols} rows={shapes} n={n}", flush=True)
+    rng = np.random.default_rng(cols + n)
+    Ws = [gaussian_q4k(rng, r, cols) for r in shapes]
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    add = rng.standard_normal((n, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    dWs = [dev.to_device(t) for t in Ws]
+    dx, dadd, dw = dev.to_device(x), dev.to_device(add), dev.to_device(w)
+    # separate kernels
+    xo_ref = dev.zeros((n, cols), np.float32)
+    a8 = a8_bufs(dev, n, cols)
+    dev.rmsnorm(dx, n, cols, dw, EPS, add=dadd, xo=xo_ref, a8=a8)
+    Yref = [dev.zeros((n, r), np.float32) for r in shapes]
+    dev.q4k_matmul_multi(dWs, shapes, Yref, shapes, cols, n, *a8)
+    # fused
+    xo = dev.zeros((n, cols), np.float32)
+    tmp = a8_bufs(dev, n, cols)
+    Y = [dev.zeros((n, r), np.float32) for r in shapes]
+    dev.q4k_matmul_norm(dWs, shapes, Y, cols, n, dx, dw, EPS, add=dadd, xo=xo, a8_tmp=tmp)
+    dev.sync()
+    assert_bits_equal(xo.numpy(), x + add, "residual sum")
+    assert_bits_equal(xo.numpy(), xo_ref.numpy(), "residual sum (separate)")
+    for r, a, b in zip(shapes, Y, Yref):
+        assert_bits_equal(a.numpy(), b.numpy(), f"rows={r}")
+    # the separate RMSNorm against the restated order (its A8 through the oracle)
+    q, d, fs = oracle.quant_a8(rmsnorm_restated(x + add, w, EPS))
+    assert_bits_equal(a8[0].numpy(), q, "A8 codes of the norm")
+    assert_bits_equal(a8[1].numpy(), d, "A8 scales of the norm")
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 6, 8, 13])
+@pytest.mark.parametrize("fused_norm", [True, False])
+def test_swiglu_equals_separate(dev, n, fused_norm):
+    print(f"[case] swiglu n={n} norm={fused_norm}", flush=True)
+    ffn, cols = 3584, 1024
+    rng = np.random.default_rng(100 + n)
+    Wg, Wu = gaussian_q4k(rng, ffn, cols), gaussian_q4k(rng, ffn, cols)
+    dWg, dWu = dev.to_device(Wg), dev.to_device(Wu)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    add = rng.standard_normal((n, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    dx, dadd, dw = dev.to_device(x), dev.to_device(add), dev.to_device(w)
+    a8_in = a8_bufs(dev, n, cols)
+    dev.rmsnorm(dx, n, cols, dw, EPS, add=dadd, a8=a8_in)
+    # separate: matmuls + silu_mul
+    g, u = dev.zeros((n, ffn), np.float32), dev.zeros((n, ffn), np.float32)
+    dev.q4k_matmul_multi([dWg, dWu], [ffn, ffn], [g, u], [ffn, ffn], cols, n, *a8_in)
+    yref = dev.zeros((n, ffn), np.float32)
+    outref = a8_bufs(dev, n, ffn)
+    dev.silu_mul(g, u, n, ffn, y=yref, a8=outref)
+    # fused
+    y = dev.zeros((n, ffn), np.float32)
+    out = a8_bufs(dev, n, ffn)
+    tmp = a8_bufs(dev, n, cols)
+    gt, ut = dev.zeros((n, ffn), np.float32), dev.zeros((n, ffn), np.float32)
+    xo = dev.zeros((n, cols), np.float32)
+    if fused_norm:
+        dev.q4k_swiglu(dWg, dWu, ffn, cols, n, out, norm=(dx, dw, EPS, dadd, xo), y=y,
+                       a8_tmp=tmp, gate_tmp=gt, up_tmp=ut)
+    else:
+        dev.q4k_swiglu(dWg, dWu, ffn, cols, n, out, a8=a8_in, y=y, gate_tmp=gt, up_tmp=ut)
+    dev.sync()
+    assert_bits_equal(y.numpy(), yref.numpy(), "silu(gate) * up")
+    for a, b, what in zip(out, outref, ("codes", "scales", "fsum")):
+        assert_bits_equal(a.numpy(), b.numpy(), f"A8 {what}")
+    if fused_norm:
+        assert_bits_equal(xo.numpy(), x + add, "residual sum")
+
+
+def test_fused_invalid_calls_rejected(dev):
+    from nibblemac_amd.nmx import NmxError
+    W = dev.zeros(576 * 4, np.uint8)
+    x = dev.zeros((2, 256), np.float32)
+    w = dev.zeros(256, np.float32)
+    Y = dev.zeros((2, 16), np.float32)
+    with pytest.raises(NmxError):   # x_out aliases x
+        dev.q4k_matmul_norm([W], [16], [Y], 256, 2, x, w, EPS, add=x, xo=x)
+    with pytest.raises(NmxError):   # output aliases the norm input
+        dev.q4k_matmul_norm([W], [16], [x], 256, 2, x, w, EPS)
+    with pytest.raises(NmxError):   # cols not a multiple of 256
+        dev.q4k_matmul_norm([W], [16], [Y], 255, 2, x, w, EPS)
+    out = a8_bufs(dev, 2, 32)
+    with pytest.raises(NmxError):   # no input
+        dev.q4k_swiglu(W, W, 32, 256, 2, out)

@@ -67,6 +67,9 @@ def assert_bits_equal(a, b, what):
 
 
 def check_case(dev, W, rows, cols, X, dots=True):
+    """Both device paths: the one that also returns the int32 sub-block sums (row-per-lane /
+    K-split kernels) and the production one (small-row shapes: every vector of a pass in one
+    workgroup, chains from LDS)."""
     q, d, fs = oracle.quant_a8(X)
     ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, X.shape[0], want_dots=dots)
     Yr, Dr = ref if dots else (ref, None)
@@ -76,6 +79,8 @@ def check_case(dev, W, rows, cols, X, dots=True):
     assert_bits_equal(got["fs"], fs, "A8 fsum")
     if dots:
         assert_bits_equal(got["dots"], Dr, "int32 sub-block sums")
+        assert_bits_equal(got["Y"], Yr, "fp32 outputs (dots path)")
+        got = run_gpu(dev, W, rows, cols, X, want_dots=False)
     assert_bits_equal(got["Y"], Yr, "fp32 outputs")
 
 
