@@ -64,12 +64,22 @@ def time_graph(dev: Device, g, reps: int) -> float:
     return dev.elapsed_ms(e0, e1)
 
 
-def head_roofline(reps: int = 20, graphs: int = 5) -> dict:
+def head_roofline(reps: int = 20, graphs: int = 5, eager: bool = False,
+                  copy_mib: int = 0) -> dict:
     """The Q4K matvec of the LM head (248320 x 1024) over k + 1 = 5 A8 rows, logits written,
-    two rotating weight copies (cold), `reps` launches per graph, timed with HIP events."""
+    two rotating weight copies (cold), `reps` launches per graph, timed with HIP events on the
+    stream the kernels run on. eager: plain stream launches instead of graph replays (for
+    profiler counter runs); copy_mib: first copy that many MiB device to device (the plain copy
+    whose counters scale the HBM traffic readings)."""
     s, n = QWEN35_08B, K_DRAFT + 1
     thr = host_threads()
     with Device(0) as dev:
+        if copy_mib:
+            a = dev.zeros(copy_mib << 20, np.uint8)
+            b = dev.zeros(copy_mib << 20, np.uint8)
+            dev.copy(b, a, copy_mib << 20)
+            dev.sync()
+            a.free(), b.free()
         W = pqtool.gauss_q4k(7, 10_000, s.vocab, s.hidden, 0.02, thr)
         heads = [dev.to_device(W), dev.to_device(W)]
         X = dev.to_device(np.random.default_rng(7).standard_normal((n, s.hidden))
@@ -79,13 +89,27 @@ def head_roofline(reps: int = 20, graphs: int = 5) -> dict:
         fs = dev.empty((s.hidden // 32, n), np.float32)
         dev.quant_a8(X, n, s.hidden, q, d, fs)
         logits = dev.empty((n, s.vocab), np.float32)
-        dev.graph_begin()
-        for r in range(reps):
-            dev.q4k_matmul(heads[r % 2], s.vocab, s.hidden, n, q, d, fs, logits)
-        g = dev.graph_end()
-        dev.graph_launch(g)
-        dev.sync()
-        ms = time_graph(dev, g, graphs) / (reps * graphs)
+
+        def launches():
+            for r in range(reps):
+                dev.q4k_matmul(heads[r % 2], s.vocab, s.hidden, n, q, d, fs, logits)
+
+        if eager:
+            launches()
+            dev.sync()
+            e0, e1 = dev.event(), dev.event()
+            dev.record(e0)
+            for _ in range(graphs):
+                launches()
+            dev.record(e1)
+            ms = dev.elapsed_ms(e0, e1) / (reps * graphs)
+        else:
+            dev.graph_begin()
+            launches()
+            g = dev.graph_end()
+            dev.graph_launch(g)
+            dev.sync()
+            ms = time_graph(dev, g, graphs) / (reps * graphs)
         dev.sync()
     wbytes = s.vocab // 4 * (s.hidden // 256) * 576
     algo = wbytes + n * s.hidden + 2 * 4 * n * (s.hidden // 32) + 4 * n * s.vocab
@@ -96,7 +120,8 @@ def head_roofline(reps: int = 20, graphs: int = 5) -> dict:
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "q4k_mv_k<5,false,false> (LM head 248320x1024 Q4K x 5 A8 rows, cold)",
-            "us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": algo}
+            "us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": algo,
+            "timing": "eager stream launches" if eager else "graph replays"}
 
 
 class PfStop(ctypes.Structure):
@@ -167,13 +192,17 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the LM-head matvec launches (for counter runs)")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --roofline-only: stream launches instead of graph replays")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="with --roofline-only: a device copy of this size first (counter scale)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
               "(the multi-GPU sharding is a design, not a measured path)", file=sys.stderr)
         return 2
     if a.roofline_only:
-        roof = head_roofline()
+        roof = head_roofline(eager=a.eager, copy_mib=a.copy_mib)
         log(f"head matvec: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
         print(json.dumps({"roofline": roof}), flush=True)
         return 0

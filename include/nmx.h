@@ -182,6 +182,26 @@ int nmx_lin_post(nmx_ctx *ctx, const float *o, int o_stride, const float *z, int
                  const float *w, int n, int heads, int dv, float eps, float *y, int y_stride,
                  nmx_a8 a8);
 
+/* The Gated DeltaNet mixer between in_proj and out_proj in one launch (engine/src/
+ * forward_lin.c:36-81, 94-133): nmx_lin_pre for the q / k / v channels and gates of each value
+ * head, nmx_lin_rule and nmx_lin_post (gated RMSNorm of o with z and norm_w, output y and / or
+ * its A8), with identical results; the conv outputs, gates and o stay on chip. pre.out,
+ * pre.beta, pre.decay, rule.qkv, rule.decay, rule.beta and rule.o are only used (and then
+ * must be valid buffers) when the shape is outside the fused kernel's limits and the three
+ * kernels run instead. */
+typedef struct {
+    nmx_lin_pre_args pre;
+    nmx_lin_args rule;
+    const float *z;
+    int z_stride;
+    const float *norm_w;
+    float eps;
+    float *y;
+    int y_stride;
+    nmx_a8 a8;
+} nmx_lin_mix_args;
+int nmx_lin_mix(nmx_ctx *ctx, const nmx_lin_mix_args *a);
+
 /* RMSNorm input of a fused matmul: rows x (+ add, the residual, added first) of [n][cols],
  * normed with weight w (engine/src/forward_ops.c:191-200, forward.c pf_add_rows). x_out (if
  * not NULL) receives x + add, written once; it must not alias x or add. */

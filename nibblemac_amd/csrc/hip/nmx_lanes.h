@@ -1,0 +1,62 @@
+/* Cross-lane helpers for gfx950 wave64 kernels.
+ *
+ * nmx_dpp<CTRL>: a DPP lane move (row_mask / bank_mask all, bound_ctrl); nmx_swz16: lane ^ 16
+ * within each 32-lane group (ds_swizzle). nmx_max32 / nmx_sum32 reduce over each 32-lane
+ * half-wave (every lane of the half active): DPP quad permutes and row mirrors inside the
+ * 16-lane rows, one swizzle across them; max and integer sums are exact in any order.
+ * nmx_quad_chain: a left-to-right fp32 sum over a quad of lanes, lane c holding the c-th
+ * quarter of the terms; the running sum moves to the next lane by a DPP broadcast of lane c
+ * (quad_perm [c, c, c, c]), so the adds are one sequential chain. */
+#ifndef NMX_LANES_H
+#define NMX_LANES_H
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+template <int CTRL>
+__device__ __forceinline__ int nmx_dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+
+/* lane ^ 16 within each 32-lane group (swizzle bit mode: and 0x1f, or 0, xor 0x10) */
+__device__ __forceinline__ int nmx_swz16(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+
+constexpr int NMX_DPP_XOR1 = 0xB1;        /* quad_perm [1, 0, 3, 2] */
+constexpr int NMX_DPP_XOR2 = 0x4E;        /* quad_perm [2, 3, 0, 1] */
+constexpr int NMX_DPP_HALF_MIRROR = 0x141; /* lane i <- 7 - i within 8 */
+constexpr int NMX_DPP_MIRROR = 0x140;      /* lane i <- 15 - i within 16 */
+
+__device__ __forceinline__ float nmx_max32(float v) {
+    v = fmaxf(v, __int_as_float(nmx_dpp<NMX_DPP_XOR1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(nmx_dpp<NMX_DPP_XOR2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(nmx_dpp<NMX_DPP_HALF_MIRROR>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(nmx_dpp<NMX_DPP_MIRROR>(__float_as_int(v))));
+    return fmaxf(v, __int_as_float(nmx_swz16(__float_as_int(v))));
+}
+
+__device__ __forceinline__ int nmx_sum32(int v) {
+    v += nmx_dpp<NMX_DPP_XOR1>(v);
+    v += nmx_dpp<NMX_DPP_XOR2>(v);
+    v += nmx_dpp<NMX_DPP_HALF_MIRROR>(v);
+    v += nmx_dpp<NMX_DPP_MIRROR>(v);
+    return v + nmx_swz16(v);
+}
+
+template <int DK4>
+__device__ __forceinline__ float nmx_quad_chain(const float (&p)[DK4]) {
+    float carry = 0.0f;
+#define NMX_QUAD_SEG(C)                                                                       \
+    {                                                                                         \
+        float acc = carry;                                                                    \
+        _Pragma("unroll") for (int r = 0; r < DK4; r++) acc = acc + p[r];                     \
+        carry = __int_as_float(nmx_dpp<(C) * 0x55>(__float_as_int(acc)));                     \
+    }
+    NMX_QUAD_SEG(0)
+    NMX_QUAD_SEG(1)
+    NMX_QUAD_SEG(2)
+    NMX_QUAD_SEG(3)
+#undef NMX_QUAD_SEG
+    return carry;
+}
+
+#endif

@@ -24,26 +24,6 @@
 
 namespace {
 
-/* The ordered sum over the quad: lane c adds its DK4 products to the running sum of lanes
- * 0 .. c-1; the running sum moves to the next lane by a DPP broadcast of lane c within each
- * quad (quad_perm [c, c, c, c]), so the adds form the reference's single left-to-right chain. */
-template <int DK4>
-__device__ __forceinline__ float quad_chain(const float (&p)[DK4]) {
-    float carry = 0.0f;
-#define NMX_QUAD_SEG(C)                                                                       \
-    {                                                                                         \
-        float acc = carry;                                                                    \
-        _Pragma("unroll") for (int r = 0; r < DK4; r++) acc = acc + p[r];                     \
-        carry = __int_as_float(nmx_dpp<(C) * 0x55>(__float_as_int(acc)));                     \
-    }
-    NMX_QUAD_SEG(0)
-    NMX_QUAD_SEG(1)
-    NMX_QUAD_SEG(2)
-    NMX_QUAD_SEG(3)
-#undef NMX_QUAD_SEG
-    return carry;
-}
-
 /* Tokens (or pending rows) staged per batch: their k / q rows in LDS, gates and v_j in
  * registers, every load of a batch issued before the first is used. */
 constexpr int TB = 8;
@@ -170,7 +150,7 @@ __global__ __launch_bounds__(256) void lin_rule_k(nmx_lin_args a) {
                 s[r] = s[r] * dec;
                 p[r] = s[r] * kk[r];
             }
-            const float kv = quad_chain<DK4>(p);
+            const float kv = nmx_quad_chain<DK4>(p);
             const float del = (vj[u] - kv) * bet;
 
 #pragma unroll
@@ -178,7 +158,7 @@ __global__ __launch_bounds__(256) void lin_rule_k(nmx_lin_args a) {
                 s[r] = s[r] + kk[r] * del;
                 p[r] = s[r] * qq[r];
             }
-            const float ov = quad_chain<DK4>(p);
+            const float ov = nmx_quad_chain<DK4>(p);
             if (live && c == 0) a.o[(size_t)t * a.o_stride + h * dv + j] = ov;
 
             if (logged && (t > 0 || a.log0)) {

@@ -1,0 +1,336 @@
+/* The Gated DeltaNet mixer of one verify pass in one launch for gfx950 (include/nmx.h
+ * nmx_lin_mix): for every value head, the causal conv + SiLU of the head's q / k / v channels
+ * with the conv state and the rollback inputs, the q / k L2 norms and the beta / decay gates
+ * (engine/src/forward_lin.c:36-67, forward_ops.c:204-260), the recurrence with the pending
+ * replays and the per-token log (matvec_ref.c:114-188), and the gated RMSNorm + A8 of the
+ * output (forward_lin.c:70-81). Every value is computed with the same operations in the same
+ * order as nmx_lin_pre, nmx_lin_rule and nmx_lin_post, so the results are identical; the conv
+ * outputs, gates and o stay in LDS between the three stages instead of going through HBM and
+ * three kernel boundaries.
+ *
+ * One workgroup per value head (one value head per key head, so every conv channel belongs to
+ * one workgroup), 4 dv threads: the recurrence keeps the quad-per-column mapping
+ * of nmx_lin_rule (lane c of the quad holds keys [c dk/4, (c+1) dk/4) of its column in VGPRs);
+ * the conv stage has one thread per channel; the norms run as 4-lane ordered chains. */
+#include "nmx_internal.h"
+#include "nmx_math.h"
+#include "nmx_a8.h"
+
+namespace {
+
+constexpr int MIX_TB = 8;          /* tokens per batch of conv-input loads; pending rows per batch */
+constexpr int MIX_MAX_THREADS = 512;
+constexpr int MIX_LDS = 157 * 1024; /* dynamic LDS: 160 KB less the static reduction array */
+
+struct LinMix {
+    /* pre */
+    int n, C, K, kd;
+    const float *raw;
+    int raw_stride;
+    float *state;
+    const float *conv_w;
+    float *xin;
+    float qscale, l2eps;
+    const float *b_in, *a_in;
+    int g_stride;
+    const float *A_log, *A, *dt_bias;
+    /* rule */
+    int heads, rep, dv;
+    float *S;
+    float *log;
+    const float *pend;
+    int keep, log0;
+    const int32_t *keep_dev;
+    /* post */
+    const float *z;
+    int z_stride;
+    const float *w;
+    float eps;
+    float *y;
+    int y_stride;
+    int8_t *aq;
+    float *ad, *afs;
+};
+
+__host__ __device__ constexpr int mix_lds_floats(int n, int dk, int dv) {
+    /* q, k (rule layout [n][4][dk/4 + 4]), v, o [n][dv], pending rows [MIX_TB][4][dk/4 + 4],
+     * beta, decay [n] */
+    return 2 * n * 4 * (dk / 4 + 4) + 2 * n * dv + MIX_TB * 4 * (dk / 4 + 4) + 2 * n;
+}
+
+template <int DK4>
+__global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[8 * 64];
+    constexpr int DK = DK4 * 4, PAD = DK4 + 4, ROW = 4 * PAD;
+    const int n = a.n, dv = a.dv, heads = a.heads;
+    const int h = blockIdx.x, tid = threadIdx.x, T = blockDim.x, c = tid & 3;
+    const int j = tid >> 2; /* value column of the quad (T = 4 dv) */
+    const int kh = h / a.rep, kd = a.kd;
+    const size_t logw = (size_t)DK + dv + 1;
+    const bool logged = a.log != nullptr;
+    float *sq = sm, *sk = sq + n * ROW, *sv = sk + n * ROW, *so = sv + n * dv;
+    float *sp = so + n * dv, *sbet = sp + MIX_TB * ROW, *sdec = sbet + n;
+    auto kidx = [](int i) { return (i / DK4) * PAD + i % DK4; }; /* rule layout of key i */
+
+    /* ---- recurrence state of the quad's keys (loaded first) ---- */
+    float *Sp = a.S + ((size_t)h * dv + j) * DK + c * DK4;
+    float s[DK4];
+#pragma unroll
+    for (int r = 0; r < DK4; r += 4) {
+        const float4 x = *(const float4 *)(Sp + r);
+        s[r] = x.x, s[r + 1] = x.y, s[r + 2] = x.z, s[r + 3] = x.w;
+    }
+
+    /* ---- the deferred commit of the previous pass (matvec_ref.c:169-188 arithmetic) ---- */
+    int keep = a.keep;
+    if (a.keep_dev) {
+        const int kd_ = *a.keep_dev;
+        keep = kd_ < keep ? kd_ : keep;
+    }
+    for (int u0 = 0; u0 < keep; u0 += MIX_TB) {
+        const int nb = keep - u0 < MIX_TB ? keep - u0 : MIX_TB;
+        float pdel[MIX_TB];
+#pragma unroll
+        for (int u = 0; u < MIX_TB; u++)
+            pdel[u] = u < nb ? a.pend[((size_t)(u0 + u) * heads + h) * logw + DK + j] : 0.0f;
+        __syncthreads();
+        for (int x0 = 0; x0 < nb * DK; x0 += 8 * T) {
+            float kb[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int x = x0 + e * T + tid, xc = x < nb * DK ? x : nb * DK - 1;
+                const int u = xc / DK, i = xc - u * DK;
+                kb[e] = a.pend[((size_t)(u0 + u) * heads + h) * logw + i];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int x = x0 + e * T + tid;
+                if (x < nb * DK) {
+                    const int u = x / DK, i = x - u * DK;
+                    sp[u * ROW + kidx(i)] = kb[e];
+                }
+            }
+        }
+        if (tid < nb) red[tid] = a.pend[((size_t)(u0 + tid) * heads + h) * logw + DK + dv];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < MIX_TB; u++) {
+            if (u < nb) {
+                const float pdec = red[u];
+                const float *kk = sp + u * ROW + c * PAD;
+#pragma unroll
+                for (int r = 0; r < DK4; r++) {
+                    s[r] = s[r] * pdec;
+                    s[r] = s[r] + kk[r] * pdel[u];
+                }
+            }
+        }
+    }
+    const bool store_now = a.log0 && keep > 0;
+    if (store_now) {
+#pragma unroll
+        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+    }
+
+    /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv) ---- */
+    const int S1 = a.K - 1, nch = 2 * DK + dv;
+    for (int ci = tid; ci < nch; ci += T) {
+        const int gc = ci < DK ? kh * DK + ci : ci < 2 * DK ? kd + kh * DK + (ci - DK)
+                                                            : 2 * kd + h * dv + (ci - 2 * DK);
+        float win[8], wc[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            win[r] = r < S1 ? a.state[(size_t)r * a.C + gc] : 0.0f;
+            wc[r] = r < a.K ? a.conv_w[(size_t)gc * a.K + r] : 0.0f;
+        }
+        for (int t0 = 0; t0 < n; t0 += MIX_TB) {
+            const int nb = n - t0 < MIX_TB ? n - t0 : MIX_TB;
+            float xt[MIX_TB];
+#pragma unroll
+            for (int u = 0; u < MIX_TB; u++)
+                xt[u] = u < nb ? a.raw[(size_t)(t0 + u) * a.raw_stride + gc] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < MIX_TB; u++) {
+                if (u >= nb) continue;
+                const int t = t0 + u;
+                /* taps in order over [state rows (oldest first), x_t] */
+                float acc = wc[0] * (S1 > 0 ? win[0] : xt[u]);
+#pragma unroll
+                for (int q = 1; q < 8; q++)
+                    if (q < a.K) acc = acc + wc[q] * (q < S1 ? win[q] : xt[u]);
+#pragma unroll
+                for (int q = 0; q < 7; q++)
+                    if (q + 1 < S1) win[q] = win[q + 1];
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (q == S1 - 1) win[q] = xt[u];
+                if (t == 0 && a.xin) { /* logged pass: token 0 is committed in place */
+#pragma unroll
+                    for (int q = 0; q < 8; q++)
+                        if (q < S1) a.state[(size_t)q * a.C + gc] = win[q];
+                }
+                if (t > 0 && a.xin) a.xin[(size_t)t * a.C + gc] = xt[u];
+                const float yv = nmx_silu(acc);
+                if (ci < DK) sq[t * ROW + kidx(ci)] = yv;
+                else if (ci < 2 * DK) sk[t * ROW + kidx(ci - DK)] = yv;
+                else sv[t * dv + (ci - 2 * DK)] = yv;
+            }
+        }
+        if (!a.xin) {
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (q < S1) a.state[(size_t)q * a.C + gc] = win[q];
+        }
+    }
+    /* gates: beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)), A = -exp(A_log) */
+    for (int t = tid; t < n; t += T) {
+        const float b = a.b_in[(size_t)t * a.g_stride + h];
+        const float av = a.a_in[(size_t)t * a.g_stride + h];
+        sbet[t] = 1.0f / (1.0f + nmx_gate_expf(-b));
+        const float A = a.A ? a.A[h] : -nmx_gate_expf(a.A_log[h]);
+        float sp_ = av + a.dt_bias[h];
+        sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf(sp_));
+        sdec[t] = nmx_gate_expf(A * sp_);
+    }
+    __syncthreads();
+
+    /* ---- q / k L2 norms (4 partial sums of squares + empty tail), q scaled ---- */
+    for (int x = tid; x < 8 * n; x += T) {
+        const int t = x >> 3, w = (x >> 2) & 1, l = x & 3;
+        const float *v = (w ? sk : sq) + t * ROW;
+        float cs = 0.0f;
+#pragma unroll 8
+        for (int m = 0; m < DK4; m++) {
+            const float e = v[kidx(4 * m + l)];
+            cs = cs + e * e;
+        }
+        red[x] = cs;
+    }
+    __syncthreads();
+    for (int x = tid; x < n * DK; x += T) {
+        const int t = x / DK, i = x - t * DK;
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const float *r4 = red + 8 * t + 4 * w;
+            const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
+            const float r = 1.0f / sqrtf(ss + a.l2eps);
+            float *v = (w ? sk : sq) + t * ROW + kidx(i);
+            *v = (*v * r) * (w ? 1.0f : a.qscale);
+        }
+    }
+    __syncthreads();
+
+    /* ---- recurrence over the tokens (nmx_lin_rule arithmetic) ---- */
+    for (int t = 0; t < n; t++) {
+        const float *kk = sk + t * ROW + c * PAD, *qq = sq + t * ROW + c * PAD;
+        const float dec = sdec[t], bet = sbet[t];
+        float p[DK4];
+#pragma unroll
+        for (int r = 0; r < DK4; r++) {
+            s[r] = s[r] * dec;
+            p[r] = s[r] * kk[r];
+        }
+        const float kv = nmx_quad_chain<DK4>(p);
+        const float del = (sv[t * dv + j] - kv) * bet;
+#pragma unroll
+        for (int r = 0; r < DK4; r++) {
+            s[r] = s[r] + kk[r] * del;
+            p[r] = s[r] * qq[r];
+        }
+        const float ov = nmx_quad_chain<DK4>(p);
+        if (c == 0) so[t * dv + j] = ov;
+        if (logged && (t > 0 || a.log0)) {
+            float *lr = a.log + ((size_t)t * heads + h) * logw;
+            if (c == 0) lr[DK + j] = del;
+            for (int x = tid; x < DK; x += T) lr[x] = sk[t * ROW + kidx(x)];
+            if (tid == 0) lr[DK + dv] = dec;
+        }
+        /* the committed state: after token 0 of a reference-mode logged pass, after the last
+         * token of a plain pass */
+        const bool commit = logged ? (!a.log0 && t == 0) : (t == n - 1);
+        if (commit) {
+#pragma unroll
+            for (int r = 0; r < DK4; r += 4)
+                *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+        }
+    }
+    __syncthreads();
+
+    /* ---- gated RMSNorm of o per token (4 partial sums of squares), * w * silu(z), A8 ---- */
+    const int m4 = dv >> 2;
+    for (int x = tid; x < 4 * n; x += T) {
+        const int t = x >> 2, l = x & 3;
+        const float *v = so + t * dv + l;
+        float cs = 0.0f;
+#pragma unroll 8
+        for (int m = 0; m < m4; m++) cs = cs + v[4 * m] * v[4 * m];
+        red[x] = cs;
+    }
+    __syncthreads();
+    for (int x = tid; x < n * dv; x += T) { /* a 32-lane half-wave holds one A8 block */
+        const int t = x / dv, jj = x - t * dv;
+        const float *r4 = red + 4 * t;
+        const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
+        const float r = 1.0f / sqrtf(ss / (float)dv + a.eps);
+        const float ov = so[t * dv + jj];
+        float yv = (ov * r) * a.w[jj];
+        yv = yv * nmx_silu(a.z[(size_t)t * a.z_stride + h * dv + jj]);
+        const int col = h * dv + jj;
+        if (a.y) a.y[(size_t)t * a.y_stride + col] = yv;
+        if (a.aq) {
+            const size_t u = (size_t)(col >> 5) * n + t;
+            nmx_a8_store(yv, a.aq + u * 32, a.ad + u, a.afs + u);
+        }
+    }
+}
+
+template <int DK4>
+int launch_mix(nmx_ctx *ctx, const LinMix &m, size_t lds) {
+    static bool ready = false; /* idempotent */
+    if (!ready) {
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)lin_mix_k<DK4>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, MIX_LDS));
+        ready = true;
+    }
+    lin_mix_k<DK4><<<dim3((unsigned)m.heads), dim3((unsigned)(4 * m.dv)), lds, ctx->stream>>>(m);
+    NMX_LAUNCHED(ctx, "lin_mix");
+    return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+int nmx_lin_mix(nmx_ctx *ctx, const nmx_lin_mix_args *a) {
+    if (!ctx) return -1;
+    if (!a) return nmx_fail(ctx, "nmx_lin_mix: NULL args");
+    const nmx_lin_pre_args &p = a->pre;
+    const nmx_lin_args &r = a->rule;
+    const int n = p.n, dk = p.dk, dv = r.dv;
+    if (n < 1 || n > 64 || n != r.n || dk != r.dk || p.heads != r.heads || !a->z || !a->norm_w ||
+        a->z_stride < r.heads * dv || (a->y && a->y_stride < r.heads * dv) || dv % 32 ||
+        p.kd != (r.heads / r.rep) * dk || p.C != 2 * p.kd + r.heads * dv)
+        return nmx_fail(ctx, "nmx_lin_mix: inconsistent arguments");
+    const size_t lds = (size_t)mix_lds_floats(n, dk, dv) * 4;
+    /* one value head per key head: with shared key heads, a workgroup could read a shared
+     * q / k channel's conv state after its owner committed token 0 into it */
+    const bool fused = r.rep == 1 && (dk == 64 || dk == 128) && 4 * dv <= MIX_MAX_THREADS &&
+                       lds <= MIX_LDS && p.conv_k >= 1 && p.conv_k <= 8 && !(r.log0 && !r.log);
+    if (!fused) { /* the separate kernels, through the intermediate buffers of the structs */
+        if (nmx_lin_pre(ctx, &p) || nmx_lin_rule(ctx, &r)) return -1;
+        return nmx_lin_post(ctx, r.o, r.o_stride, a->z, a->z_stride, a->norm_w, n, r.heads, dv,
+                            a->eps, a->y, a->y_stride, a->a8);
+    }
+    if (!p.raw || !p.state || !p.conv_w || !p.b_in || !p.a_in || !p.dt_bias ||
+        (!p.A_log && !p.A) || !r.S || (r.keep > 0 && !r.pend) || p.raw_stride < p.C ||
+        p.g_stride < p.heads || r.heads % r.rep || r.keep < 0 || r.keep > 64)
+        return nmx_fail(ctx, "nmx_lin_mix: bad arguments");
+    LinMix m{n, p.C, p.conv_k, p.kd, p.raw, p.raw_stride, p.state, p.conv_w, p.xin, p.qscale,
+             p.l2eps, p.b_in, p.a_in, p.g_stride, p.A_log, p.A, p.dt_bias, r.heads, r.rep, dv,
+             r.S, r.log, r.pend, r.keep, r.log0, r.keep_dev, a->z, a->z_stride, a->norm_w,
+             a->eps, a->y, a->y_stride, a->a8.q, a->a8.d, a->a8.fs};
+    return dk == 64 ? launch_mix<16>(ctx, m, lds) : launch_mix<32>(ctx, m, lds);
+}
+
+} /* extern "C" */

@@ -74,14 +74,13 @@ struct MtLayout {
     int aq, ad, afs, work, res, total;
 };
 
-__host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm, bool swiglu,
-                                              bool sact) {
+__host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm, bool swiglu) {
     const int nb = cols >> 5;
     MtLayout L{};
     L.aq = 0;
-    L.ad = sact ? 0 : (aq_off(nb, nv) + 15) & ~15;
-    L.afs = L.ad + (sact ? 0 : nb * nv * 4);
-    L.work = (L.afs + (sact ? 0 : nb * nv * 4) + 15) & ~15;
+    L.ad = (aq_off(nb, nv) + 15) & ~15;
+    L.afs = L.ad + nb * nv * 4;
+    L.work = (L.afs + nb * nv * 4 + 15) & ~15;
     /* ((float)dot, (D*s)*d) [nb][nv][R] float2, then -(M*m) [nb][R] */
     int work = nb * nv * R * 8 + nb * R * 4;
     const int nwork = nv * (4 * cm_stride4(cols) + 4) * 4;
@@ -91,10 +90,7 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     return L;
 }
 
-/* SACT: R == 64, so each wave's units share one half superblock and, in the chain, each
- * wave serves one vector: the activations (codes, d, fsum) are wave-uniform and are read with
- * scalar loads into SGPRs instead of being staged in LDS. */
-template <int NV, bool NORM, bool SWI, bool SACT>
+template <int NV, bool NORM, bool SWI>
 __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_mt_k(
     MtTab tab, int cols, int n, int v0, int R, const int8_t *__restrict__ q,
     const float *__restrict__ d, const float *__restrict__ fs, nmx_norm_in nm,
@@ -103,7 +99,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
     __shared__ float red[5 * MT_MAX_NV];
     const int tid = threadIdx.x, T = blockDim.x;
     const int nb = cols >> 5, nsb = cols >> 8;
-    const MtLayout L = mt_layout(cols, NV, R, NORM, SWI, SACT);
+    const MtLayout L = mt_layout(cols, NV, R, NORM, SWI);
     int8_t *aq = (int8_t *)(smem + L.aq);
     float *ad = (float *)(smem + L.ad), *afs = (float *)(smem + L.afs);
     float2 *lp = (float2 *)(smem + L.work);  /* [nb][NV][R] ((float)dot, (D*s)*d) */
@@ -122,7 +118,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
     const int nq = nb * NV * 2, ns = nb * NV; /* 16-byte code halves; (block, vector) pairs */
     int4 buf[8];
     float bd[4], bf[4];
-    if constexpr (!NORM && !SACT) {
+    if constexpr (!NORM) {
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const int e = u * T + tid;
@@ -185,7 +181,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
     }
 
     /* ---- phase 0c: activations into LDS ---- */
-    if constexpr (!NORM && !SACT) {
+    if constexpr (!NORM) {
         for (int r0 = 0; r0 * 8 * T < nq || r0 * 4 * T < ns; r0++) {
             if (r0 > 0) { /* rare: more than one round (very wide rows) */
 #pragma unroll
@@ -293,8 +289,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
         int s6[4], m6[4];
         decode6_half(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, u_h & 1, s6);
         decode6_half(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, u_h & 1, m6);
-        const int hs = SACT ? __builtin_amdgcn_readfirstlane(u_h) : u_h;
-        const int blk0 = (hs >> 1) * 8 + 4 * (hs & 1);
+        const int blk0 = u_sb * 8 + u_k0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int blk = blk0 + k;
@@ -307,17 +302,9 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
             const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
 #pragma unroll
             for (int v = 0; v < NV; v++) {
-                int4 x0, x1;
-                float dv;
-                if constexpr (SACT) {
-                    const int4 *xa = (const int4 *)(q + ((size_t)blk * n + v0 + v) * 32);
-                    x0 = xa[0], x1 = xa[1];
-                    dv = d[(size_t)blk * n + v0 + v];
-                } else {
-                    const int8_t *xb = aq + aq_off(blk, NV) + v * 32;
-                    x0 = *(const int4 *)xb, x1 = *(const int4 *)(xb + 16);
-                    dv = ad[blk * NV + v];
-                }
+                const int8_t *xb = aq + aq_off(blk, NV) + v * 32;
+                const int4 x0 = *(const int4 *)xb, x1 = *(const int4 *)(xb + 16);
+                const float dv = ad[blk * NV + v];
                 int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
                 dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
                 dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
@@ -334,7 +321,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
 
     /* ---- phase 2: the fp32 chain of (row, vector) in column order ---- */
     const bool chain = tid < R * NV;
-    const int cv = chain ? (SACT ? __builtin_amdgcn_readfirstlane(tid / R) : tid / R) : 0;
+    const int cv = chain ? tid / R : 0;
     const int cr = chain ? tid - cv * R : 0;
     float acc = 0.0f;
     if (chain) {
@@ -349,7 +336,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
             for (int u = 0; u < 8; u++) {
                 pv[u] = pp[(b + u) * NV * R];
                 of[u] = op[(b + u) * R];
-                ff[u] = SACT ? fs[(size_t)(b + u) * n + v0 + cv] : afs[(b + u) * NV + cv];
+                ff[u] = afs[(b + u) * NV + cv];
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
@@ -359,7 +346,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
         }
         for (; b < nb; b++) {
             const float2 pv = pp[b * NV * R];
-            const float ff = SACT ? fs[(size_t)b * n + v0 + cv] : afs[b * NV + cv];
+            const float ff = afs[b * NV + cv];
             acc = __builtin_fmaf(pv.x, pv.y, acc);
             acc = __builtin_fmaf(op[b * R], ff, acc);
         }
@@ -388,36 +375,33 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
 }
 
 /* Rows per workgroup for a pass of nv vectors: the largest R (64, 32, ... 4) whose LDS and
- * thread counts fit; SwiGLU needs R = 64 (32 gate + 32 up rows = one A8 block). With R = 64
- * and no norm prologue the activations are read as scalars (sact). */
-int pick_rows(int cols, int nv, bool norm, bool swiglu, int *threads, bool *sact) {
+ * thread counts fit; SwiGLU needs R = 64 (32 gate + 32 up rows = one A8 block). */
+int pick_rows(int cols, int nv, bool norm, bool swiglu, int *threads) {
     const int nsb = cols >> 8;
     for (int R = 64; R >= 4; R >>= 1) {
         if (swiglu && R != 64) break;
         const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
         if (t > (norm ? MT_NORM_THREADS : MT_MAX_THREADS)) continue;
-        const bool sa = R == 64 && !norm;
-        if (mt_layout(cols, nv, R, norm, swiglu, sa).total > MT_LDS) continue;
+        if (mt_layout(cols, nv, R, norm, swiglu).total > MT_LDS) continue;
         if (norm && cols > t * MT_NORM_CPT) continue;
         *threads = t;
-        *sact = sa;
         return R;
     }
     return 0;
 }
 
-template <int NV, bool NORM, bool SWI, bool SACT>
+template <int NV, bool NORM, bool SWI>
 int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
                const int8_t *q, const float *d, const float *fs, const nmx_norm_in &nm,
                nmx_a8 out) {
     static bool ready = false; /* idempotent: a racing second call sets the same value */
     if (!ready) {
-        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI, SACT>,
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, MT_LDS));
         ready = true;
     }
-    const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI, SACT).total;
-    q4k_mt_k<NV, NORM, SWI, SACT><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
+    const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI).total;
+    q4k_mt_k<NV, NORM, SWI><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
         tab, cols, n, v0, R, q, d, fs, nm, out.q, out.d, out.fs);
     NMX_LAUNCHED(ctx, "q4k_mt");
     return 0;
@@ -425,17 +409,13 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
 
 template <int NV>
 int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
-              bool sact, const int8_t *q, const float *d, const float *fs, const nmx_norm_in *nm,
-              bool swiglu, nmx_a8 out) {
+              const int8_t *q, const float *d, const float *fs, const nmx_norm_in *nm, bool swiglu,
+              nmx_a8 out) {
     const nmx_norm_in none{};
-    if (nm && swiglu) return launch_one<NV, true, true, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
-    if (nm) return launch_one<NV, true, false, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
-    if (swiglu) {
-        if (sact) return launch_one<NV, false, true, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
-        return launch_one<NV, false, true, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
-    }
-    if (sact) return launch_one<NV, false, false, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
-    return launch_one<NV, false, false, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    if (nm && swiglu) return launch_one<NV, true, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (nm) return launch_one<NV, true, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (swiglu) return launch_one<NV, false, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    return launch_one<NV, false, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
 }
 
 } // namespace
@@ -451,9 +431,8 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
      * same per-vector operations, so the split does not change any result */
     const int passes = (n + MT_MAX_NV - 1) / MT_MAX_NV;
     int T = 0;
-    bool sact = false;
     const int nv_max = (n + passes - 1) / passes;
-    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, &T, &sact);
+    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, &T);
     if (!R) return 1;
     MtTab tab{};
     tab.count = count;
@@ -472,14 +451,14 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
         const int Tn = T; /* the first (largest) pass's thread count covers every pass */
         int rc;
         switch (nv) {
-        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
-        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, sact, q, d, fs, norm, swiglu, out); break;
+        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
         }
         if (rc) return rc;
         v0 += nv;

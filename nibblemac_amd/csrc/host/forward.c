@@ -108,14 +108,13 @@ static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged) {
                           logged ? c->xin + (size_t)li * c->cap * C : NULL,
                           1.0f / sqrtf((float)c->lk_dim), 1e-6f, s->ba, s->aa, nv, nv, L->A_log,
                           L->A, L->dt_bias, s->beta, s->decay};
-    CK(nmx_lin_pre(D, &p));
     nmx_lin_args a = {n, nv, nv / c->lk_heads, c->lk_dim, c->lv_dim, C, vd, s->conv, s->decay,
                       s->beta, c->rec + (size_t)li * nv * c->lk_dim * c->lv_dim, s->to,
                       logged ? c->log + (size_t)li * lrow : NULL, c->pend + (size_t)li * lrow,
                       c->cap - 1, 0, c->ctl + 2};
-    CK(nmx_lin_rule(D, &a));
-    CK(nmx_lin_post(D, s->to, vd, s->tb, vd, L->lin_norm, n, nv, c->lv_dim, c->rms_eps, NULL, 0,
-                    s->a_w));
+    /* conv + gates, recurrence, gated norm + A8 of o: one launch */
+    nmx_lin_mix_args m = {p, a, s->tb, vd, L->lin_norm, c->rms_eps, NULL, 0, s->a_w};
+    CK(nmx_lin_mix(D, &m));
     CK(nmx_q4k_matmul(D, L->out.w, H, vd, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->out, H, NULL));
     return PINFER_OK;
 }

@@ -33,6 +33,16 @@ class LinArgs(ctypes.Structure):
                 ("keep", _i), ("log0", _i), ("keep_dev", _vp)]
 
 
+class LinPreArgs(ctypes.Structure):
+    """Mirror of nmx_lin_pre_args (include/nmx.h)."""
+
+    _fields_ = [("n", _i), ("C", _i), ("conv_k", _i), ("dk", _i), ("kd", _i), ("raw", _vp),
+                ("raw_stride", _i), ("out", _vp), ("state", _vp), ("conv_w", _vp), ("xin", _vp),
+                ("qscale", ctypes.c_float), ("l2eps", ctypes.c_float), ("b_in", _vp),
+                ("a_in", _vp), ("g_stride", _i), ("heads", _i), ("A_log", _vp), ("A", _vp),
+                ("dt_bias", _vp), ("beta", _vp), ("decay", _vp)]
+
+
 class A8(ctypes.Structure):
     """Mirror of nmx_a8: block-major int8 codes, per-block scale d and d * sum(codes)."""
 
@@ -44,6 +54,14 @@ class NormIn(ctypes.Structure):
 
     _fields_ = [("x", _vp), ("x_stride", _i), ("add", _vp), ("add_stride", _i), ("x_out", _vp),
                 ("xo_stride", _i), ("w", _vp), ("eps", ctypes.c_float)]
+
+
+class LinMixArgs(ctypes.Structure):
+    """Mirror of nmx_lin_mix_args."""
+
+    _fields_ = [("pre", LinPreArgs), ("rule", LinArgs), ("z", _vp), ("z_stride", _i),
+                ("norm_w", _vp), ("eps", ctypes.c_float), ("y", _vp), ("y_stride", _i),
+                ("a8", A8)]
 
 
 _SIGS: dict[str, tuple[object, list[object]]] = {
@@ -80,6 +98,9 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_silu_mul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, A8]),
     "nmx_q4k_matmul_norm": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, ctypes.POINTER(NormIn),
                                  A8]),
+    "nmx_lin_pre": (_i, [_vp, ctypes.POINTER(LinPreArgs)]),
+    "nmx_lin_post": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp, _i, A8]),
+    "nmx_lin_mix": (_i, [_vp, ctypes.POINTER(LinMixArgs)]),
     "nmx_q4k_swiglu": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, ctypes.POINTER(NormIn),
                             _vp, A8, A8, _vp, _vp]),
 }
@@ -206,6 +227,10 @@ class Device:
     def free(self, b: Buffer) -> None:
         self.check(self.lib.nmx_free(self.ctx, b.ptr), "free")
 
+    def copy(self, dst, src, nbytes: int) -> None:
+        """Device-to-device copy of nbytes on the context's stream."""
+        self.check(self.lib.nmx_copy_d2d(self.ctx, _p(dst), _p(src), nbytes), "copy")
+
     def sync(self) -> None:
         self.check(self.lib.nmx_sync(self.ctx), "sync")
 
@@ -298,6 +323,18 @@ class Device:
         a = LinArgs(n, heads, rep, dk, dv, qkv_stride, o_stride, _p(qkv), _p(decay), _p(beta),
                     _p(S), _p(o), _p(log), _p(pend), keep, int(log0), None)
         self.check(self.lib.nmx_lin_rule(self.ctx, ctypes.byref(a)), "lin_rule")
+
+    def lin_pre(self, args: "LinPreArgs") -> None:
+        self.check(self.lib.nmx_lin_pre(self.ctx, ctypes.byref(args)), "lin_pre")
+
+    def lin_post(self, o, o_stride, z, z_stride, w, n, heads, dv, eps, y=None, y_stride=0,
+                 a8=(None, None, None)) -> None:
+        self.check(self.lib.nmx_lin_post(self.ctx, _p(o), o_stride, _p(z), z_stride, _p(w), n,
+                                         heads, dv, eps, _p(y), y_stride,
+                                         A8(*[_p(t) for t in a8])), "lin_post")
+
+    def lin_mix(self, args: "LinMixArgs") -> None:
+        self.check(self.lib.nmx_lin_mix(self.ctx, ctypes.byref(args)), "lin_mix")
 
     def lin_apply(self, S, log, keep: int, heads: int, dk: int, dv: int) -> None:
         self.check(self.lib.nmx_lin_apply(self.ctx, _p(S), _p(log), keep, heads, dk, dv),

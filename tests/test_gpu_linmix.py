@@ -1,0 +1,115 @@
+"""GPU parity of the fused Gated DeltaNet mixer (nmx_lin_mix) against the three kernels it
+replaces (nmx_lin_pre + nmx_lin_rule + nmx_lin_post), which are themselves checked against the
+oracle (test_gpu_lin.py) and, through the reference engine, end to end (test_gpu_e2e.py).
+
+Bar: bit-exact for every output and every piece of state the mixer leaves behind: the A8 of
+the gated-normed output and its float rows, the recurrent state, the conv state, the logged
+raw inputs (xin) and the rollback log rows. Cases: verify passes (logged) of 1..8 tokens with
+and without pending replays, the reference-mode and extension logs, plain passes up to a
+64-token prefill chunk, dk = dv = 64 and 128, and shared key heads (rep = 2, which runs the
+three kernels inside nmx_lin_mix).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from nibblemac_amd.nmx import A8, LinArgs, LinMixArgs, LinPreArgs
+from tests.test_gpu_q4k import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def p(b):
+    return None if b is None else b.ptr
+
+
+def make_case(dev, rng, n, heads, rep, dk, dv, K=4, logged=True, keep=0, log0=False):
+    kh = heads // rep
+    kd = kh * dk
+    C = 2 * kd + heads * dv
+    cap = 9
+    host = dict(
+        raw=rng.standard_normal((n, C)).astype(np.float32),
+        z=rng.standard_normal((n, heads * dv)).astype(np.float32),
+        b=rng.standard_normal((n, heads)).astype(np.float32),
+        a=rng.standard_normal((n, heads)).astype(np.float32) * 2,
+        A_log=rng.uniform(np.log(0.2), np.log(0.4), heads).astype(np.float32),
+        dt_bias=rng.uniform(-4.5, -3.5, heads).astype(np.float32),
+        conv_w=rng.uniform(-0.5, 0.5, (C, K)).astype(np.float32),
+        state=rng.standard_normal((K - 1, C)).astype(np.float32),
+        S=(rng.standard_normal((heads, dv, dk)) * 0.05).astype(np.float32),
+        pend=(rng.standard_normal((cap, heads, dk + dv + 1)) * 0.1).astype(np.float32),
+        norm_w=rng.uniform(0.5, 1.5, dv).astype(np.float32),
+    )
+    host["pend"][:, :, dk + dv] = rng.uniform(0.9, 1.0, (cap, heads))
+    return dict(n=n, heads=heads, rep=rep, dk=dk, dv=dv, K=K, kd=kd, C=C, cap=cap, logged=logged,
+                keep=keep, log0=log0, host=host)
+
+
+def run(dev, case, fused):
+    h = case["host"]
+    n, heads, dk, dv, C, cap = case["n"], case["heads"], case["dk"], case["dv"], case["C"], case["cap"]
+    d = {k: dev.to_device(v) for k, v in h.items()}
+    conv = dev.zeros((n, C), np.float32)
+    beta = dev.zeros((n, heads), np.float32)
+    decay = dev.zeros((n, heads), np.float32)
+    o = dev.zeros((n, heads * dv), np.float32)
+    xin = dev.zeros((cap, C), np.float32) if case["logged"] else None
+    log = dev.zeros((cap, heads, dk + dv + 1), np.float32) if case["logged"] else None
+    y = dev.zeros((n, heads * dv), np.float32)
+    nb = heads * dv // 32
+    aq, ad, afs = (dev.zeros((nb, n, 32), np.int8), dev.zeros((nb, n), np.float32),
+                   dev.zeros((nb, n), np.float32))
+    pre = LinPreArgs(n, C, case["K"], dk, case["kd"], p(d["raw"]), C, p(conv), p(d["state"]),
+                     p(d["conv_w"]), p(xin), np.float32(1.0 / np.sqrt(dk)), 1e-6, p(d["b"]),
+                     p(d["a"]), heads, heads, p(d["A_log"]), None, p(d["dt_bias"]), p(beta),
+                     p(decay))
+    rule = LinArgs(n, heads, case["rep"], dk, dv, C, heads * dv, p(conv), p(decay), p(beta),
+                   p(d["S"]), p(o), p(log), p(d["pend"]), case["keep"], int(case["log0"]), None)
+    if fused:
+        dev.lin_mix(LinMixArgs(pre, rule, p(d["z"]), heads * dv, p(d["norm_w"]), 1e-6, p(y),
+                               heads * dv, A8(p(aq), p(ad), p(afs))))
+    else:
+        dev.lin_pre(pre)
+        dev.lin_rule(n=n, heads=heads, rep=case["rep"], dk=dk, dv=dv, qkv_stride=C,
+                     o_stride=heads * dv, qkv=conv, decay=decay, beta=beta, S=d["S"], o=o,
+                     log=log, pend=d["pend"], keep=case["keep"], log0=case["log0"])
+        dev.lin_post(o, heads * dv, d["z"], heads * dv, d["norm_w"], n, heads, dv, 1e-6, y,
+                     heads * dv, (aq, ad, afs))
+    dev.sync()
+    out = dict(aq=aq.numpy(), ad=ad.numpy(), afs=afs.numpy(), y=y.numpy(), S=d["S"].numpy(),
+               state=d["state"].numpy())
+    if case["logged"]:
+        out["xin"] = xin.numpy()[1:n]
+        out["log"] = log.numpy()[(0 if case["log0"] else 1):n]
+    return out
+
+
+CASES = [
+    # n, heads, rep, dk, dv, logged, keep, log0
+    (5, 16, 1, 128, 128, True, 0, False),
+    (5, 16, 1, 128, 128, True, 3, False),
+    (1, 16, 1, 128, 128, True, 0, False),
+    (8, 4, 1, 128, 128, True, 7, False),
+    (5, 4, 1, 128, 128, True, 2, True),
+    (1, 4, 1, 128, 128, False, 0, False),
+    (13, 4, 1, 128, 128, False, 4, False),
+    (64, 4, 1, 128, 128, False, 0, False),
+    (5, 4, 1, 64, 64, True, 1, False),
+    (33, 4, 1, 64, 64, False, 0, False),
+    (5, 4, 2, 64, 64, True, 2, False),   # shared key heads: the three-kernel path
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "n%d_h%d_rep%d_dk%d_%s_keep%d%s" % (
+    c[0], c[1], c[2], c[3], "logged" if c[5] else "plain", c[6], "_log0" if c[7] else ""))
+def test_lin_mix_equals_three_kernels(dev, case):
+    n, heads, rep, dk, dv, logged, keep, log0 = case
+    print(f"[case] lin_mix {case}", flush=True)
+    rng = np.random.default_rng(n * 131 + heads + dk + keep)
+    c = make_case(dev, rng, n, heads, rep, dk, dv, logged=logged, keep=keep, log0=log0)
+    want = run(dev, c, fused=False)
+    got = run(dev, c, fused=True)
+    for k in want:
+        assert_bits_equal(got[k], want[k], k)
