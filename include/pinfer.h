@@ -115,6 +115,27 @@ int pinfer_generate_greedy_cont(pinfer_ctx *ctx, const int32_t *prompt, int n_pr
                                 const pinfer_gen_opts *opts, pinfer_spec_stats *stats,
                                 int *status);
 
+/* ---- conversation state (engine/include/pinfer.h:139-175) -------------------------------
+ * A snapshot of everything the context keeps for the tokens consumed so far (conv and
+ * recurrent states, KV rows, the MTP head's rows), in the reference's blob format (header
+ * with the model fingerprint; state format version 2), so blobs move between engines.
+ * Restoring it and feeding more tokens gives bit-identical results. */
+size_t pinfer_state_size(const pinfer_ctx *ctx);   /* bytes a save needs right now */
+/* PINFER_OK, or PINFER_E_ARG when cap < pinfer_state_size(ctx). */
+int pinfer_state_save(const pinfer_ctx *ctx, void *buf, size_t cap);
+/* Replaces the context's state. PINFER_E_FORMAT: not a state blob of this model file / KV
+ * format; PINFER_E_CTX_FULL: more tokens than max_ctx. Drops the checkpoint. */
+int pinfer_state_load(pinfer_ctx *ctx, const void *buf, size_t len);
+
+/* In-context checkpoint: one rewind point (a device copy of the conv and recurrent states and
+ * the position). pinfer_reset, pinfer_state_load and pinfer_generate_greedy / _ex drop it;
+ * pinfer_eval, pinfer_eval_select and pinfer_generate_greedy_cont keep it; its memory stays
+ * until pinfer_checkpoint_clear or pinfer_free. */
+int pinfer_checkpoint(pinfer_ctx *ctx);   /* PINFER_OK, PINFER_E_ARG (NULL), PINFER_E_NOMEM */
+int pinfer_rewind(pinfer_ctx *ctx);       /* PINFER_E_ARG if there is no checkpoint */
+void pinfer_checkpoint_clear(pinfer_ctx *ctx);
+int pinfer_checkpoint_n_past(const pinfer_ctx *ctx); /* its position, or -1 if none */
+
 /* Benchmark helper (the reference CLI's timing, engine/tools/pinfer_run.c:384-430): reset,
  * prefill (timed), then exactly n_gen tokens with EOS ignored (timed). */
 int pinfer_bench_generate(pinfer_ctx *ctx, const int32_t *prompt, int n_prompt, int32_t *out,

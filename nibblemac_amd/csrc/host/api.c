@@ -181,6 +181,7 @@ void pinfer_free(pinfer_ctx *c) {
     if (!c) return;
     if (c->dev) {
         e_drop_graphs(c);
+        pinfer_checkpoint_clear(c);
         nmx_sync(c->dev);
         nmx_free(c->dev, c->blob);
         for (int i = 0; i < c->n_allocs; i++) nmx_free(c->dev, c->allocs[i]);
@@ -203,6 +204,7 @@ void pinfer_reset(pinfer_ctx *c) {
     c->n_past = 0;
     c->mtp_rows = 0;
     c->keep = 0;
+    c->ck_valid = 0; /* the checkpoint's memory is kept until pinfer_checkpoint_clear */
     nmx_sync(c->dev);
 }
 

@@ -98,6 +98,10 @@ struct pinfer_ctx {
     int use_graphs;
     void *allocs[E_MAX_ALLOCS]; /* every device allocation besides the weight blob */
     int n_allocs;
+    uint64_t model_fp;          /* fingerprint of the .pq file (state blobs) */
+    /* in-context checkpoint: device copy of the conv and recurrent states */
+    void *ck_dev;
+    int ck_valid, ck_n_past, ck_mtp_rows;
 };
 
 /* forward.c */

@@ -231,6 +231,31 @@ static int map_mtp(const loader *L, pinfer_ctx *c) {
     return rc ? PINFER_E_FORMAT : PINFER_OK;
 }
 
+/* 64-bit FNV-1a (offset basis 14695981039346656037, prime 1099511628211) */
+static uint64_t fnv1a(uint64_t h, const void *p, size_t n) {
+    const unsigned char *b = p;
+    for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 1099511628211ull;
+    return h;
+}
+
+/* The model fingerprint a state blob carries (engine/src/model.c:142-154): FNV-1a over the
+ * header, the directory, and the first, middle and last 64 bytes of every tensor. */
+static uint64_t fingerprint(const loader *L) {
+    const pq_hdr *h = L->h;
+    uint64_t f = fnv1a(14695981039346656037ull, h, sizeof(pq_hdr));
+    const uint8_t *dir = L->map + h->dir_offset;
+    f = fnv1a(f, dir, (size_t)h->n_tensors * sizeof(pq_entry));
+    for (uint32_t i = 0; i < h->n_tensors; i++) {
+        const pq_entry *e = (const pq_entry *)(dir + (size_t)i * sizeof(pq_entry));
+        const unsigned char *d = (const unsigned char *)L->map + e->offset;
+        const size_t n = (size_t)e->nbytes, s = n < 64 ? n : 64;
+        f = fnv1a(f, d, s);
+        f = fnv1a(f, d + (n - s) / 2, s);
+        f = fnv1a(f, d + (n - s), s);
+    }
+    return f;
+}
+
 int e_model_load(pinfer_ctx *c, const char *path) {
     int fd = open(path, O_RDONLY);
     if (fd < 0) {
@@ -305,6 +330,7 @@ int e_model_load(pinfer_ctx *c, const char *path) {
     for (uint32_t i = 0; rc == PINFER_OK && i < h->n_layers; i++)
         rc = build_layer(&L, (int)i, &c->layers[i], c);
     if (rc == PINFER_OK && c->has_mtp) rc = map_mtp(&L, c);
+    if (rc == PINFER_OK) c->model_fp = fingerprint(&L);
     munmap(map, L.size);
     return rc;
 }

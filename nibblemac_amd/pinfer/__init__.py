@@ -81,6 +81,34 @@ class Model:
             raise PinferError(status.value or n, "pinfer_generate_greedy")
         return [int(x) for x in out[:n]], st
 
+    def state_save(self) -> bytes:
+        """The context state as a blob (pinfer_state_save)."""
+        n = self.lib.pinfer_state_size(self.ctx)
+        buf = ctypes.create_string_buffer(n)
+        rc = self.lib.pinfer_state_save(self.ctx, buf, n)
+        if rc != 0:
+            raise PinferError(rc, "pinfer_state_save")
+        return buf.raw
+
+    def state_load(self, blob: bytes) -> None:
+        rc = self.lib.pinfer_state_load(self.ctx, blob, len(blob))
+        if rc != 0:
+            raise PinferError(rc, "pinfer_state_load")
+
+    def checkpoint(self) -> None:
+        rc = self.lib.pinfer_checkpoint(self.ctx)
+        if rc != 0:
+            raise PinferError(rc, "pinfer_checkpoint")
+
+    def rewind(self) -> None:
+        rc = self.lib.pinfer_rewind(self.ctx)
+        if rc != 0:
+            raise PinferError(rc, "pinfer_rewind")
+
+    @property
+    def checkpoint_n_past(self) -> int:
+        return self.lib.pinfer_checkpoint_n_past(self.ctx)
+
     def bench_generate(self, prompt, n_gen: int, k: int = 4, draft_vocab: int = 32768):
         """The reference CLI's benchmark timing (engine/tools/pinfer_run.c:384-430): reset,
         prefill, then exactly n_gen tokens with EOS ignored. Returns (tokens, stats, prefill

@@ -69,6 +69,13 @@ _OPTIONAL = {
     "pinfer_generate_greedy_cont": (ctypes.c_int, _GEN_EX),
     "pinfer_eval_select": (ctypes.c_int, [ctypes.c_void_p, _c_int32_p, ctypes.c_int, _c_int32_p,
                                           ctypes.c_int, _c_float_p]),
+    "pinfer_state_size": (ctypes.c_size_t, [ctypes.c_void_p]),
+    "pinfer_state_save": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "pinfer_state_load": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "pinfer_checkpoint": (ctypes.c_int, [ctypes.c_void_p]),
+    "pinfer_rewind": (ctypes.c_int, [ctypes.c_void_p]),
+    "pinfer_checkpoint_clear": (None, [ctypes.c_void_p]),
+    "pinfer_checkpoint_n_past": (ctypes.c_int, [ctypes.c_void_p]),
     "pinfer_bench_generate": (ctypes.c_int, [ctypes.c_void_p, _c_int32_p, ctypes.c_int, _c_int32_p,
                                              ctypes.c_int, ctypes.POINTER(SpecParams),
                                              ctypes.POINTER(SpecStats),

@@ -152,3 +152,93 @@ def test_invalid_arguments(models):
         gpu.eval(np.zeros(65, np.int32))           # more than max_ctx
     assert gpu.n_past == 0
     gpu.close()
+
+
+@needs_ref
+def test_state_blob_matches_reference(models):
+    """After the same prefill, and after the same speculative generation (MTP rows included),
+    the GPU engine's state blob is byte-identical to the reference engine's: the blob format,
+    the model fingerprint, the transposed recurrent state and every KV row agree."""
+    gpu, ref = pair(models["small"])
+    prompt = np.random.default_rng(11).integers(0, pqfile.SMALL.vocab, 37)
+    gpu.eval(prompt), ref.eval(prompt)
+    assert gpu.state_save() == ref.state_save(), "state after prefill"
+    gpu.generate(prompt, 20, k=4, draft_vocab=1024)
+    ref.generate(prompt, 20, k=4, draft_vocab=1024)
+    assert gpu.state_save() == ref.state_save(), "state after a speculative generation"
+    gpu.close(), ref.close()
+
+
+@needs_ref
+def test_state_load_across_engines(models):
+    """A reference blob loaded into the GPU engine (and a GPU blob into the reference)
+    continues bit-identically; a GPU round trip (save, more tokens, reset, load) too."""
+    gpu, ref = pair(models["small"])
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, pqfile.SMALL.vocab, 45)
+    more = rng.integers(0, pqfile.SMALL.vocab, 9)
+    ref.eval(prompt)
+    blob_r = ref.state_save()
+    gpu.state_load(blob_r)
+    assert gpu.n_past == 45
+    a, b = gpu.eval(more), ref.eval(more)
+    assert np.array_equal(bits(a), bits(b)), "reference blob -> GPU"
+    blob_g = gpu.state_save()
+    ref.reset()
+    ref.state_load(blob_g)
+    c, d = ref.eval([3, 4]), gpu.eval([3, 4])
+    assert np.array_equal(bits(c), bits(d)), "GPU blob -> reference"
+    # round trip on the GPU
+    gpu.reset()
+    gpu.eval(prompt)
+    blob = gpu.state_save()
+    x = gpu.eval(more)
+    gpu.reset()
+    gpu.state_load(blob)
+    y = gpu.eval(more)
+    assert np.array_equal(bits(x), bits(y)), "GPU round trip"
+    # blobs of another shape or corrupted headers are refused
+    from nibblemac_amd.pinfer import PinferError
+    bad = bytearray(blob)
+    bad[0] ^= 1
+    with pytest.raises(PinferError):
+        gpu.state_load(bytes(bad))
+    with pytest.raises(PinferError):
+        gpu.state_load(blob[:100])
+    gpu.close(), ref.close()
+
+
+@needs_ref
+def test_checkpoint_rewind(models):
+    """checkpoint / rewind (engine/include/pinfer.h:153-175): after a rewind, feeding other
+    tokens gives exactly what feeding them at the checkpoint gives, on both engines."""
+    gpu, ref = pair(models["small"])
+    rng = np.random.default_rng(13)
+    prefix = rng.integers(0, pqfile.SMALL.vocab, 30)
+    a_toks = rng.integers(0, pqfile.SMALL.vocab, 6)
+    b_toks = rng.integers(0, pqfile.SMALL.vocab, 4)
+    from nibblemac_amd.pinfer import PinferError
+    with pytest.raises(PinferError):
+        gpu.rewind()                      # no checkpoint yet
+    assert gpu.checkpoint_n_past == -1
+    for m in (gpu, ref):
+        m.eval(prefix)
+        m.checkpoint()
+        m.eval(a_toks)
+        m.rewind()
+    assert gpu.n_past == ref.n_past == 30 and gpu.checkpoint_n_past == 30
+    x, y = gpu.eval(b_toks), ref.eval(b_toks)
+    assert np.array_equal(bits(x), bits(y)), "after rewind vs reference"
+    fresh = Model(str(models["small"]), max_ctx=512)
+    z = fresh.eval(np.concatenate([prefix, b_toks]))
+    assert np.array_equal(bits(x), bits(z)), "after rewind vs a fresh context"
+    gpu.rewind()                          # one checkpoint serves any number of rewinds
+    tg, _ = gpu.generate(b_toks, 8, k=4, draft_vocab=1024, cont=True)
+    ref.rewind()
+    tr, _ = ref.generate(b_toks, 8, k=4, draft_vocab=1024, cont=True)
+    assert tg == tr
+    gpu.reset()                           # reset drops the checkpoint
+    assert gpu.checkpoint_n_past == -1
+    with pytest.raises(PinferError):
+        gpu.rewind()
+    fresh.close(), gpu.close(), ref.close()
