@@ -9,8 +9,9 @@
  * linking -lnmx from nibblemac_amd/lib.
  *
  * Weights: each Q4K_G32 matrix is uploaded on its first product (or by pf_pool_gpu_enable) and
- * stays on the device until pf_pool_destroy; a matrix is identified by its data pointer (the
- * model file's bytes, immutable while the model is loaded).
+ * stays on the device until pf_pool_destroy; a matrix is identified by its data pointer, so
+ * the matrices must stay mapped and unchanged while the pool lives (the engine destroys its
+ * pool before it frees the model, engine/src/pinfer.c:185-186).
  * Activations and the recurrent state stay where the engine keeps them, in host memory: the
  * engine's own code reads and writes them directly (pinfer_reset zeroes the state,
  * engine/src/pinfer.c:196; the state blob copies it, state.c:89-90). Every call therefore

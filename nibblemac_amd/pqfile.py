@@ -100,10 +100,18 @@ def nbytes(dtype: int, dims: list[int]) -> int:
 
 
 def write_model(path: str | os.PathLike, shape: Shape = QWEN35_08B, seed: int = 1,
-                random_norms: bool = False, mtp: bool = True) -> Path:
-    """Write a synthetic model; returns the path."""
+                random_norms: bool = False, mtp: bool = True,
+                overrides: dict[str, np.ndarray] | None = None) -> Path:
+    """Write a synthetic model; returns the path. `overrides` replaces the values of named F32
+    tensors (same element count)."""
     path = Path(path)
     ts = tensors(shape, seed, random_norms, mtp)
+    for name, value in (overrides or {}).items():
+        i = next((i for i, t in enumerate(ts) if t[0] == name), None)
+        if i is None or ts[i][1] != F32:
+            raise ValueError(f"override {name}: no F32 tensor of that name")
+        data = np.ascontiguousarray(value, np.float32).reshape(ts[i][2])
+        ts[i] = (name, F32, ts[i][2], lambda d=data: d)
     mask = sum(1 << i for i in range(shape.layers) if shape.is_full(i))
     dir_off = 4096
     data_off = -(-(dir_off + 128 * len(ts)) // 4096) * 4096

@@ -15,7 +15,6 @@ from __future__ import annotations
 
 import ctypes
 import os
-from dataclasses import replace
 
 import numpy as np
 import pytest
@@ -49,8 +48,11 @@ def bits_equal(a, b, what):
     assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[0]}"
 
 
-@pytest.fixture(scope="module")
+@pytest.fixture
 def plug():
+    """A fresh pool per test: a pool keys its device weights by host address, valid while the
+    matrices outlive it (as in the engine, engine/src/pinfer.c:185-186), and a test's arrays do
+    not outlive the test."""
     L = ctypes.CDLL(str(PLUG))
     L.pf_pool_create.restype, L.pf_pool_create.argtypes = _vp, [ctypes.c_int]
     L.pf_pool_destroy.restype, L.pf_pool_destroy.argtypes = None, [_vp]
@@ -152,11 +154,9 @@ def test_pf_lin_apply(plug):
 
 
 @pytest.fixture(scope="module")
-def models(tmp_path_factory):
-    d = tmp_path_factory.mktemp("pq")
-    tiny = replace(pqfile.SMALL, vocab=8, eos_id=7)
-    return {"small": pqfile.write_model(d / "small.pq", pqfile.SMALL, seed=3, random_norms=True),
-            "tiny": pqfile.write_model(d / "tiny.pq", tiny, seed=4, random_norms=True)}
+def small_pq(tmp_path_factory):
+    return pqfile.write_model(tmp_path_factory.mktemp("pq") / "small.pq", pqfile.SMALL, seed=3,
+                              random_norms=True)
 
 
 def engines(path):
@@ -168,8 +168,8 @@ def engines(path):
 
 
 @needs_plug
-def test_engine_eval_on_plug(models):
-    dev, ref = engines(models["small"])
+def test_engine_eval_on_plug(small_pq):
+    dev, ref = engines(small_pq)
     rng = np.random.default_rng(60)
     prompt = rng.integers(0, pqfile.SMALL.vocab, 40)
     bits_equal(dev.eval(prompt), ref.eval(prompt), "logits after prefill")
@@ -179,18 +179,18 @@ def test_engine_eval_on_plug(models):
 
 
 @needs_plug
-@pytest.mark.parametrize("name,k", [("small", 4), ("tiny", 4), ("tiny", 2)])
-def test_engine_generate_on_plug(models, name, k):
-    """Speculative generation through the reference's own loop; the tiny vocabulary makes drafts
-    get accepted (multi-token commits, deferred replays through pf_lin_rule's pend)."""
-    print(f"[case] plug generate {name} k={k}", flush=True)
-    dev, ref = engines(models[name])
-    vocab = pqfile.SMALL.vocab if name == "small" else 7
-    prompt = np.random.default_rng(61).integers(0, vocab, 23)
-    ta, sa = dev.generate(prompt, 48, k=k)
-    tb, sb = ref.generate(prompt, 48, k=k)
+@pytest.mark.parametrize("k", [2, 4])
+def test_engine_generate_on_plug(agree_model, k):
+    """Speculative generation through the reference's own loop with drafts accepted in many
+    rounds: multi-token commits and deferred replays through pf_lin_rule's pend / keep."""
+    path, prompt = agree_model
+    print(f"[case] plug generate agree k={k}", flush=True)
+    dev, ref = engines(path)
+    ta, sa = dev.generate(prompt, 64, k=k)
+    tb, sb = ref.generate(prompt, 64, k=k)
     assert ta == tb
     assert (sa.rounds, sa.drafted, sa.accepted) == (sb.rounds, sb.drafted, sb.accepted)
-    if name == "tiny":
-        assert sa.accepted > 0, "no draft accepted: the deferred-replay path did not run"
+    assert sa.accepted >= sa.drafted // 4
+    probe = [1, 2, 3]
+    bits_equal(dev.eval(probe), ref.eval(probe), "logits after the generation")
     dev.close(), ref.close()
