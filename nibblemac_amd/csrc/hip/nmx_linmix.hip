@@ -53,9 +53,11 @@ struct LinMix {
 };
 
 __host__ __device__ constexpr int mix_lds_floats(int n, int dk, int dv) {
-    /* q, k (rule layout [n][4][dk/4 + 4]), v, o [n][dv], pending rows [MIX_TB][4][dk/4 + 4],
+    /* q, k (rule layout [n][4][dk/4 + 4]), v, o [n][dv], pending keys [MIX_TB][4][dk/4 + 4],
+     * pending deltas [MIX_TB][dv], z of the first tokens [MIX_TB][dv], norm weight [dv],
      * beta, decay [n] */
-    return 2 * n * 4 * (dk / 4 + 4) + 2 * n * dv + MIX_TB * 4 * (dk / 4 + 4) + 2 * n;
+    return 2 * n * 4 * (dk / 4 + 4) + 2 * n * dv + MIX_TB * 4 * (dk / 4 + 4) + 2 * MIX_TB * dv +
+           dv + 2 * n;
 }
 
 template <int DK4>
@@ -70,10 +72,13 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
     const size_t logw = (size_t)DK + dv + 1;
     const bool logged = a.log != nullptr;
     float *sq = sm, *sk = sq + n * ROW, *sv = sk + n * ROW, *so = sv + n * dv;
-    float *sp = so + n * dv, *sbet = sp + MIX_TB * ROW, *sdec = sbet + n;
+    float *sp = so + n * dv, *spd = sp + MIX_TB * ROW, *sz = spd + MIX_TB * dv;
+    float *sw = sz + MIX_TB * dv, *sbet = sw + dv, *sdec = sbet + n;
     auto kidx = [](int i) { return (i / DK4) * PAD + i % DK4; }; /* rule layout of key i */
+    const int n0 = n < MIX_TB ? n : MIX_TB; /* tokens whose inputs are requested at entry */
 
-    /* ---- recurrence state of the quad's keys (loaded first) ---- */
+    /* ==== every input of the first batch is requested here, before any of it is used ==== */
+    /* recurrence state of the quad's keys */
     float *Sp = a.S + ((size_t)h * dv + j) * DK + c * DK4;
     float s[DK4];
 #pragma unroll
@@ -81,6 +86,66 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         const float4 x = *(const float4 *)(Sp + r);
         s[r] = x.x, s[r + 1] = x.y, s[r + 2] = x.z, s[r + 3] = x.w;
     }
+    /* pending rows of the first batch, up to the host's bound on keep: keys (x = e T + tid
+     * over [pb0][DK]), deltas (over [pb0][dv]), decays (tid < pb0) */
+    const int pb0 = a.keep < MIX_TB ? a.keep : MIX_TB;
+    float pkey[2], pdel[2], pdec = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv, jd = x - ud * dv;
+        pkey[e] = 0.0f, pdel[e] = 0.0f;
+        if (uk < pb0) pkey[e] = a.pend[((size_t)uk * heads + h) * logw + ik];
+        if (ud < pb0) pdel[e] = a.pend[((size_t)ud * heads + h) * logw + DK + jd];
+    }
+    if (tid < pb0) pdec = a.pend[((size_t)tid * heads + h) * logw + DK + dv];
+    /* conv: thread tid < nch / 2 owns channels 2 tid, 2 tid + 1 (K = 4: 3 state rows, taps as
+     * one float4 per channel) */
+    const int nch = 2 * DK + dv, ci = 2 * tid;
+    const bool conv_on = ci < nch;
+    const int gc = ci < DK ? kh * DK + ci : ci < 2 * DK ? kd + kh * DK + (ci - DK)
+                                                        : 2 * kd + h * dv + (ci - 2 * DK);
+    float2 cwin[3], cx[MIX_TB];
+    float4 cw0 = make_float4(0.f, 0.f, 0.f, 0.f), cw1 = cw0;
+    if (conv_on) {
+#pragma unroll
+        for (int r = 0; r < 3; r++) cwin[r] = *(const float2 *)(a.state + (size_t)r * a.C + gc);
+        cw0 = *(const float4 *)(a.conv_w + (size_t)gc * 4);
+        cw1 = *(const float4 *)(a.conv_w + (size_t)gc * 4 + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < MIX_TB; u++) {
+        cx[u] = make_float2(0.f, 0.f);
+        if (conv_on && u < n0) cx[u] = *(const float2 *)(a.raw + (size_t)u * a.raw_stride + gc);
+    }
+    /* gates of token T - 1 - tid (the last wave) */
+    const int gt = T - 1 - tid;
+    float gb = 0.0f, ga = 0.0f, gA = 0.0f, gdt = 0.0f;
+    if (gt < n) {
+        gb = a.b_in[(size_t)gt * a.g_stride + h];
+        ga = a.a_in[(size_t)gt * a.g_stride + h];
+        gA = a.A ? a.A[h] : a.A_log[h];
+        gdt = a.dt_bias[h];
+    }
+    /* z of the first tokens and the norm weight, as float4 (x4 = tid over [n0][dv / 4]) */
+    const bool z_on = 4 * tid < n0 * dv, w_on = 4 * tid < dv;
+    float4 zq = make_float4(0.f, 0.f, 0.f, 0.f), wq = zq;
+    if (z_on) {
+        const int t = (4 * tid) / dv, jj = 4 * tid - t * dv;
+        zq = *(const float4 *)(a.z + (size_t)t * a.z_stride + h * dv + jj);
+    }
+    if (w_on) wq = *(const float4 *)(a.w + 4 * tid);
+
+    /* ---- requested values that later phases read from LDS ---- */
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv;
+        if (uk < pb0) sp[uk * ROW + kidx(ik)] = pkey[e];
+        if (ud < pb0) spd[x] = pdel[e];
+    }
+    if (tid < pb0) red[tid] = pdec;
+    if (z_on) *(float4 *)(sz + 4 * tid) = zq;
+    if (w_on) *(float4 *)(sw + 4 * tid) = wq;
+    __syncthreads();
 
     /* ---- the deferred commit of the previous pass (matvec_ref.c:169-188 arithmetic) ---- */
     int keep = a.keep;
@@ -90,39 +155,34 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
     }
     for (int u0 = 0; u0 < keep; u0 += MIX_TB) {
         const int nb = keep - u0 < MIX_TB ? keep - u0 : MIX_TB;
-        float pdel[MIX_TB];
+        if (u0 > 0) { /* later batches (keep > MIX_TB) load here */
+            float kb[2], db[2], dc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < MIX_TB; u++)
-            pdel[u] = u < nb ? a.pend[((size_t)(u0 + u) * heads + h) * logw + DK + j] : 0.0f;
-        __syncthreads();
-        for (int x0 = 0; x0 < nb * DK; x0 += 8 * T) {
-            float kb[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int x = x0 + e * T + tid, xc = x < nb * DK ? x : nb * DK - 1;
-                const int u = xc / DK, i = xc - u * DK;
-                kb[e] = a.pend[((size_t)(u0 + u) * heads + h) * logw + i];
+            for (int e = 0; e < 2; e++) {
+                const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv, jd = x - ud * dv;
+                kb[e] = uk < nb ? a.pend[((size_t)(u0 + uk) * heads + h) * logw + ik] : 0.0f;
+                db[e] = ud < nb ? a.pend[((size_t)(u0 + ud) * heads + h) * logw + DK + jd] : 0.0f;
             }
+            if (tid < nb) dc = a.pend[((size_t)(u0 + tid) * heads + h) * logw + DK + dv];
+            __syncthreads(); /* the previous batch is applied */
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int x = x0 + e * T + tid;
-                if (x < nb * DK) {
-                    const int u = x / DK, i = x - u * DK;
-                    sp[u * ROW + kidx(i)] = kb[e];
-                }
+            for (int e = 0; e < 2; e++) {
+                const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv;
+                if (uk < nb) sp[uk * ROW + kidx(ik)] = kb[e];
+                if (ud < nb) spd[x] = db[e];
             }
+            if (tid < nb) red[tid] = dc;
+            __syncthreads();
         }
-        if (tid < nb) red[tid] = a.pend[((size_t)(u0 + tid) * heads + h) * logw + DK + dv];
-        __syncthreads();
 #pragma unroll
         for (int u = 0; u < MIX_TB; u++) {
             if (u < nb) {
-                const float pdec = red[u];
+                const float pdec_ = red[u], pdel_ = spd[u * dv + j];
                 const float *kk = sp + u * ROW + c * PAD;
 #pragma unroll
                 for (int r = 0; r < DK4; r++) {
-                    s[r] = s[r] * pdec;
-                    s[r] = s[r] + kk[r] * pdel[u];
+                    s[r] = s[r] * pdec_;
+                    s[r] = s[r] + kk[r] * pdel_;
                 }
             }
         }
@@ -133,65 +193,63 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
     }
 
-    /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv) ---- */
-    const int S1 = a.K - 1, nch = 2 * DK + dv;
-    for (int ci = tid; ci < nch; ci += T) {
-        const int gc = ci < DK ? kh * DK + ci : ci < 2 * DK ? kd + kh * DK + (ci - DK)
-                                                            : 2 * kd + h * dv + (ci - 2 * DK);
-        float win[8], wc[8];
+    /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv), two per thread ---- */
+    if (conv_on) {
+        float win0[3], win1[3];
+        const float wc0[4] = {cw0.x, cw0.y, cw0.z, cw0.w}, wc1[4] = {cw1.x, cw1.y, cw1.z, cw1.w};
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            win[r] = r < S1 ? a.state[(size_t)r * a.C + gc] : 0.0f;
-            wc[r] = r < a.K ? a.conv_w[(size_t)gc * a.K + r] : 0.0f;
-        }
+        for (int r = 0; r < 3; r++) win0[r] = cwin[r].x, win1[r] = cwin[r].y;
         for (int t0 = 0; t0 < n; t0 += MIX_TB) {
             const int nb = n - t0 < MIX_TB ? n - t0 : MIX_TB;
-            float xt[MIX_TB];
+            float2 xt[MIX_TB];
 #pragma unroll
-            for (int u = 0; u < MIX_TB; u++)
-                xt[u] = u < nb ? a.raw[(size_t)(t0 + u) * a.raw_stride + gc] : 0.0f;
+            for (int u = 0; u < MIX_TB; u++) xt[u] = cx[u];
+            if (t0 > 0) {
+#pragma unroll
+                for (int u = 0; u < MIX_TB; u++)
+                    xt[u] = u < nb ? *(const float2 *)(a.raw + (size_t)(t0 + u) * a.raw_stride + gc)
+                                   : make_float2(0.f, 0.f);
+            }
 #pragma unroll
             for (int u = 0; u < MIX_TB; u++) {
                 if (u >= nb) continue;
                 const int t = t0 + u;
                 /* taps in order over [state rows (oldest first), x_t] */
-                float acc = wc[0] * (S1 > 0 ? win[0] : xt[u]);
-#pragma unroll
-                for (int q = 1; q < 8; q++)
-                    if (q < a.K) acc = acc + wc[q] * (q < S1 ? win[q] : xt[u]);
-#pragma unroll
-                for (int q = 0; q < 7; q++)
-                    if (q + 1 < S1) win[q] = win[q + 1];
-#pragma unroll
-                for (int q = 0; q < 8; q++)
-                    if (q == S1 - 1) win[q] = xt[u];
+                float acc0 = wc0[0] * win0[0], acc1 = wc1[0] * win1[0];
+                acc0 = acc0 + wc0[1] * win0[1], acc1 = acc1 + wc1[1] * win1[1];
+                acc0 = acc0 + wc0[2] * win0[2], acc1 = acc1 + wc1[2] * win1[2];
+                acc0 = acc0 + wc0[3] * xt[u].x, acc1 = acc1 + wc1[3] * xt[u].y;
+                win0[0] = win0[1], win0[1] = win0[2], win0[2] = xt[u].x;
+                win1[0] = win1[1], win1[1] = win1[2], win1[2] = xt[u].y;
                 if (t == 0 && a.xin) { /* logged pass: token 0 is committed in place */
 #pragma unroll
-                    for (int q = 0; q < 8; q++)
-                        if (q < S1) a.state[(size_t)q * a.C + gc] = win[q];
+                    for (int q = 0; q < 3; q++)
+                        *(float2 *)(a.state + (size_t)q * a.C + gc) = make_float2(win0[q], win1[q]);
                 }
-                if (t > 0 && a.xin) a.xin[(size_t)t * a.C + gc] = xt[u];
-                const float yv = nmx_silu(acc);
-                if (ci < DK) sq[t * ROW + kidx(ci)] = yv;
-                else if (ci < 2 * DK) sk[t * ROW + kidx(ci - DK)] = yv;
-                else sv[t * dv + (ci - 2 * DK)] = yv;
+                if (t > 0 && a.xin) *(float2 *)(a.xin + (size_t)t * a.C + gc) = xt[u];
+                const float y0 = nmx_silu(acc0), y1 = nmx_silu(acc1);
+                if (ci < DK) {
+                    sq[t * ROW + kidx(ci)] = y0, sq[t * ROW + kidx(ci + 1)] = y1;
+                } else if (ci < 2 * DK) {
+                    sk[t * ROW + kidx(ci - DK)] = y0, sk[t * ROW + kidx(ci - DK + 1)] = y1;
+                } else {
+                    *(float2 *)(sv + t * dv + (ci - 2 * DK)) = make_float2(y0, y1);
+                }
             }
         }
         if (!a.xin) {
 #pragma unroll
-            for (int q = 0; q < 8; q++)
-                if (q < S1) a.state[(size_t)q * a.C + gc] = win[q];
+            for (int q = 0; q < 3; q++)
+                *(float2 *)(a.state + (size_t)q * a.C + gc) = make_float2(win0[q], win1[q]);
         }
     }
     /* gates: beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)), A = -exp(A_log) */
-    for (int t = tid; t < n; t += T) {
-        const float b = a.b_in[(size_t)t * a.g_stride + h];
-        const float av = a.a_in[(size_t)t * a.g_stride + h];
-        sbet[t] = 1.0f / (1.0f + nmx_gate_expf(-b));
-        const float A = a.A ? a.A[h] : -nmx_gate_expf(a.A_log[h]);
-        float sp_ = av + a.dt_bias[h];
+    if (gt < n) {
+        sbet[gt] = 1.0f / (1.0f + nmx_gate_expf(-gb));
+        const float A = a.A ? gA : -nmx_gate_expf(gA);
+        float sp_ = ga + gdt;
         sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf(sp_));
-        sdec[t] = nmx_gate_expf(A * sp_);
+        sdec[gt] = nmx_gate_expf(A * sp_);
     }
     __syncthreads();
 
@@ -274,8 +332,9 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
         const float r = 1.0f / sqrtf(ss / (float)dv + a.eps);
         const float ov = so[t * dv + jj];
-        float yv = (ov * r) * a.w[jj];
-        yv = yv * nmx_silu(a.z[(size_t)t * a.z_stride + h * dv + jj]);
+        const float zv = t < n0 ? sz[x] : a.z[(size_t)t * a.z_stride + h * dv + jj];
+        float yv = (ov * r) * sw[jj];
+        yv = yv * nmx_silu(zv);
         const int col = h * dv + jj;
         if (a.y) a.y[(size_t)t * a.y_stride + col] = yv;
         if (a.aq) {
@@ -315,8 +374,16 @@ int nmx_lin_mix(nmx_ctx *ctx, const nmx_lin_mix_args *a) {
     const size_t lds = (size_t)mix_lds_floats(n, dk, dv) * 4;
     /* one value head per key head: with shared key heads, a workgroup could read a shared
      * q / k channel's conv state after its owner committed token 0 into it */
+    /* the fused kernel reads the conv inputs as channel pairs (2 dk + dv <= 2 T), a batch of
+     * pending keys as two elements per thread (dk <= dv) and z / w / the taps as float4:
+     * K = 4, even channel strides, 16-byte aligned z, w and taps */
+    auto al = [](const void *q, unsigned m) { return ((uintptr_t)q & (m - 1)) == 0; };
+    const bool vec_ok = p.conv_k == 4 && p.C % 2 == 0 && p.raw_stride % 2 == 0 &&
+                        a->z_stride % 4 == 0 && al(p.raw, 8) && al(p.state, 8) &&
+                        (!p.xin || al(p.xin, 8)) && al(p.conv_w, 16) && al(a->z, 16) &&
+                        al(a->norm_w, 16);
     const bool fused = r.rep == 1 && (dk == 64 || dk == 128) && 4 * dv <= MIX_MAX_THREADS &&
-                       lds <= MIX_LDS && p.conv_k >= 1 && p.conv_k <= 8 && !(r.log0 && !r.log);
+                       dk <= dv && lds <= MIX_LDS && vec_ok && !(r.log0 && !r.log);
     if (!fused) { /* the separate kernels, through the intermediate buffers of the structs */
         if (nmx_lin_pre(ctx, &p) || nmx_lin_rule(ctx, &r)) return -1;
         return nmx_lin_post(ctx, r.o, r.o_stride, a->z, a->z_stride, a->norm_w, n, r.heads, dv,

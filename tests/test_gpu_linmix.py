@@ -28,7 +28,7 @@ def make_case(dev, rng, n, heads, rep, dk, dv, K=4, logged=True, keep=0, log0=Fa
     kh = heads // rep
     kd = kh * dk
     C = 2 * kd + heads * dv
-    cap = 9
+    cap = max(9, keep + 1)
     host = dict(
         raw=rng.standard_normal((n, C)).astype(np.float32),
         z=rng.standard_normal((n, heads * dv)).astype(np.float32),
@@ -92,6 +92,7 @@ CASES = [
     (5, 16, 1, 128, 128, True, 3, False),
     (1, 16, 1, 128, 128, True, 0, False),
     (8, 4, 1, 128, 128, True, 7, False),
+    (5, 4, 1, 128, 128, True, 12, False),  # two batches of pending rows
     (5, 4, 1, 128, 128, True, 2, True),
     (1, 4, 1, 128, 128, False, 0, False),
     (13, 4, 1, 128, 128, False, 4, False),
