@@ -55,9 +55,9 @@ struct LinMix {
 __host__ __device__ constexpr int mix_lds_floats(int n, int dk, int dv) {
     /* q, k (rule layout [n][4][dk/4 + 4]), v, o [n][dv], pending keys [MIX_TB][4][dk/4 + 4],
      * pending deltas [MIX_TB][dv], z of the first tokens [MIX_TB][dv], norm weight [dv],
-     * beta, decay [n] */
+     * beta, decay [n], norm factors [3 n] (q, k L2; o RMS) */
     return 2 * n * 4 * (dk / 4 + 4) + 2 * n * dv + MIX_TB * 4 * (dk / 4 + 4) + 2 * MIX_TB * dv +
-           dv + 2 * n;
+           dv + 5 * n;
 }
 
 template <int DK4>
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
     const bool logged = a.log != nullptr;
     float *sq = sm, *sk = sq + n * ROW, *sv = sk + n * ROW, *so = sv + n * dv;
     float *sp = so + n * dv, *spd = sp + MIX_TB * ROW, *sz = spd + MIX_TB * dv;
-    float *sw = sz + MIX_TB * dv, *sbet = sw + dv, *sdec = sbet + n;
+    float *sw = sz + MIX_TB * dv, *sbet = sw + dv, *sdec = sbet + n, *srn = sdec + n;
     auto kidx = [](int i) { return (i / DK4) * PAD + i % DK4; }; /* rule layout of key i */
     const int n0 = n < MIX_TB ? n : MIX_TB; /* tokens whose inputs are requested at entry */
 
@@ -98,33 +98,35 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         if (ud < pb0) pdel[e] = a.pend[((size_t)ud * heads + h) * logw + DK + jd];
     }
     if (tid < pb0) pdec = a.pend[((size_t)tid * heads + h) * logw + DK + dv];
-    /* conv: thread tid < nch / 2 owns channels 2 tid, 2 tid + 1 (K = 4: 3 state rows, taps as
-     * one float4 per channel) */
-    const int nch = 2 * DK + dv, ci = 2 * tid;
+    /* conv: thread tid < nch owns channel tid (K = 4: 3 state rows, the taps as one float4) */
+    const int nch = 2 * DK + dv, ci = tid;
     const bool conv_on = ci < nch;
     const int gc = ci < DK ? kh * DK + ci : ci < 2 * DK ? kd + kh * DK + (ci - DK)
                                                         : 2 * kd + h * dv + (ci - 2 * DK);
-    float2 cwin[3], cx[MIX_TB];
-    float4 cw0 = make_float4(0.f, 0.f, 0.f, 0.f), cw1 = cw0;
+    float cwin[3], cx[MIX_TB];
+    float4 cw = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 3; r++) cwin[r] = 0.0f;
     if (conv_on) {
 #pragma unroll
-        for (int r = 0; r < 3; r++) cwin[r] = *(const float2 *)(a.state + (size_t)r * a.C + gc);
-        cw0 = *(const float4 *)(a.conv_w + (size_t)gc * 4);
-        cw1 = *(const float4 *)(a.conv_w + (size_t)gc * 4 + 4);
+        for (int r = 0; r < 3; r++) cwin[r] = a.state[(size_t)r * a.C + gc];
+        cw = *(const float4 *)(a.conv_w + (size_t)gc * 4);
     }
 #pragma unroll
     for (int u = 0; u < MIX_TB; u++) {
-        cx[u] = make_float2(0.f, 0.f);
-        if (conv_on && u < n0) cx[u] = *(const float2 *)(a.raw + (size_t)u * a.raw_stride + gc);
+        cx[u] = 0.0f;
+        if (conv_on && u < n0) cx[u] = a.raw[(size_t)u * a.raw_stride + gc];
     }
-    /* gates of token T - 1 - tid (the last wave) */
-    const int gt = T - 1 - tid;
-    float gb = 0.0f, ga = 0.0f, gA = 0.0f, gdt = 0.0f;
-    if (gt < n) {
-        gb = a.b_in[(size_t)gt * a.g_stride + h];
-        ga = a.a_in[(size_t)gt * a.g_stride + h];
+    /* gate items of the last wave, which owns no channel (y = tid - (T - 64)): item y < n is the
+     * decay of token y, item n <= y < 2 n the beta of token y - n */
+    const int gy = tid - (T - 64);
+    float ga = 0.0f, gA = 0.0f, gdt = 0.0f;
+    if (gy >= 0 && gy < n) {
+        ga = a.a_in[(size_t)gy * a.g_stride + h];
         gA = a.A ? a.A[h] : a.A_log[h];
         gdt = a.dt_bias[h];
+    } else if (gy >= n && gy < 2 * n) {
+        ga = a.b_in[(size_t)(gy - n) * a.g_stride + h];
     }
     /* z of the first tokens and the norm weight, as float4 (x4 = tid over [n0][dv / 4]) */
     const bool z_on = 4 * tid < n0 * dv, w_on = 4 * tid < dv;
@@ -193,63 +195,66 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
     }
 
-    /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv), two per thread ---- */
+    /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv), one per thread ---- */
     if (conv_on) {
-        float win0[3], win1[3];
-        const float wc0[4] = {cw0.x, cw0.y, cw0.z, cw0.w}, wc1[4] = {cw1.x, cw1.y, cw1.z, cw1.w};
+        float win[3];
+        const float wc[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
-        for (int r = 0; r < 3; r++) win0[r] = cwin[r].x, win1[r] = cwin[r].y;
+        for (int r = 0; r < 3; r++) win[r] = cwin[r];
         for (int t0 = 0; t0 < n; t0 += MIX_TB) {
             const int nb = n - t0 < MIX_TB ? n - t0 : MIX_TB;
-            float2 xt[MIX_TB];
+            float xt[MIX_TB];
 #pragma unroll
             for (int u = 0; u < MIX_TB; u++) xt[u] = cx[u];
             if (t0 > 0) {
 #pragma unroll
                 for (int u = 0; u < MIX_TB; u++)
-                    xt[u] = u < nb ? *(const float2 *)(a.raw + (size_t)(t0 + u) * a.raw_stride + gc)
-                                   : make_float2(0.f, 0.f);
+                    xt[u] = u < nb ? a.raw[(size_t)(t0 + u) * a.raw_stride + gc] : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < MIX_TB; u++) {
                 if (u >= nb) continue;
                 const int t = t0 + u;
                 /* taps in order over [state rows (oldest first), x_t] */
-                float acc0 = wc0[0] * win0[0], acc1 = wc1[0] * win1[0];
-                acc0 = acc0 + wc0[1] * win0[1], acc1 = acc1 + wc1[1] * win1[1];
-                acc0 = acc0 + wc0[2] * win0[2], acc1 = acc1 + wc1[2] * win1[2];
-                acc0 = acc0 + wc0[3] * xt[u].x, acc1 = acc1 + wc1[3] * xt[u].y;
-                win0[0] = win0[1], win0[1] = win0[2], win0[2] = xt[u].x;
-                win1[0] = win1[1], win1[1] = win1[2], win1[2] = xt[u].y;
+                float acc = wc[0] * win[0];
+                acc = acc + wc[1] * win[1];
+                acc = acc + wc[2] * win[2];
+                acc = acc + wc[3] * xt[u];
+                win[0] = win[1], win[1] = win[2], win[2] = xt[u];
                 if (t == 0 && a.xin) { /* logged pass: token 0 is committed in place */
 #pragma unroll
-                    for (int q = 0; q < 3; q++)
-                        *(float2 *)(a.state + (size_t)q * a.C + gc) = make_float2(win0[q], win1[q]);
+                    for (int q = 0; q < 3; q++) a.state[(size_t)q * a.C + gc] = win[q];
                 }
-                if (t > 0 && a.xin) *(float2 *)(a.xin + (size_t)t * a.C + gc) = xt[u];
-                const float y0 = nmx_silu(acc0), y1 = nmx_silu(acc1);
-                if (ci < DK) {
-                    sq[t * ROW + kidx(ci)] = y0, sq[t * ROW + kidx(ci + 1)] = y1;
-                } else if (ci < 2 * DK) {
-                    sk[t * ROW + kidx(ci - DK)] = y0, sk[t * ROW + kidx(ci - DK + 1)] = y1;
-                } else {
-                    *(float2 *)(sv + t * dv + (ci - 2 * DK)) = make_float2(y0, y1);
-                }
+                if (t > 0 && a.xin) a.xin[(size_t)t * a.C + gc] = xt[u];
+                const float yv = nmx_silu(acc);
+                if (ci < DK) sq[t * ROW + kidx(ci)] = yv;
+                else if (ci < 2 * DK) sk[t * ROW + kidx(ci - DK)] = yv;
+                else sv[t * dv + (ci - 2 * DK)] = yv;
             }
         }
         if (!a.xin) {
 #pragma unroll
-            for (int q = 0; q < 3; q++)
-                *(float2 *)(a.state + (size_t)q * a.C + gc) = make_float2(win0[q], win1[q]);
+            for (int q = 0; q < 3; q++) a.state[(size_t)q * a.C + gc] = win[q];
         }
     }
-    /* gates: beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)), A = -exp(A_log) */
-    if (gt < n) {
-        sbet[gt] = 1.0f / (1.0f + nmx_gate_expf(-gb));
-        const float A = a.A ? gA : -nmx_gate_expf(gA);
-        float sp_ = ga + gdt;
-        sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf(sp_));
-        sdec[gt] = nmx_gate_expf(A * sp_);
+    /* meanwhile the last wave computes the gates, beta = sigmoid(b) and
+     * decay = exp(A softplus(a + dt_bias)) with A = -exp(A_log) */
+    if (gy >= 0) {
+        for (int x = gy; x < 2 * n; x += 64) {
+            const bool first = x == gy;
+            if (x < n) {
+                const float av = first ? ga : a.a_in[(size_t)x * a.g_stride + h];
+                const float Ai = first ? gA : a.A ? a.A[h] : a.A_log[h];
+                const float dt = first ? gdt : a.dt_bias[h];
+                const float A = a.A ? Ai : -nmx_gate_expf(Ai);
+                float sp_ = av + dt;
+                sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf(sp_));
+                sdec[x] = nmx_gate_expf(A * sp_);
+            } else {
+                const float b = first ? ga : a.b_in[(size_t)(x - n) * a.g_stride + h];
+                sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf(-b));
+            }
+        }
     }
     __syncthreads();
 
@@ -266,15 +271,18 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         red[x] = cs;
     }
     __syncthreads();
+    for (int x = tid; x < 2 * n; x += T) { /* x = 2 t + w */
+        const float *r4 = red + 4 * x;
+        const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
+        srn[x] = 1.0f / sqrtf(ss + a.l2eps);
+    }
+    __syncthreads();
     for (int x = tid; x < n * DK; x += T) {
         const int t = x / DK, i = x - t * DK;
 #pragma unroll
         for (int w = 0; w < 2; w++) {
-            const float *r4 = red + 8 * t + 4 * w;
-            const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
-            const float r = 1.0f / sqrtf(ss + a.l2eps);
             float *v = (w ? sk : sq) + t * ROW + kidx(i);
-            *v = (*v * r) * (w ? 1.0f : a.qscale);
+            *v = (*v * srn[2 * t + w]) * (w ? 1.0f : a.qscale);
         }
     }
     __syncthreads();
@@ -326,15 +334,18 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         red[x] = cs;
     }
     __syncthreads();
-    for (int x = tid; x < n * dv; x += T) { /* a 32-lane half-wave holds one A8 block */
-        const int t = x / dv, jj = x - t * dv;
+    for (int t = tid; t < n; t += T) {
         const float *r4 = red + 4 * t;
         const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
-        const float r = 1.0f / sqrtf(ss / (float)dv + a.eps);
+        srn[2 * n + t] = 1.0f / sqrtf(ss / (float)dv + a.eps);
+    }
+    __syncthreads();
+    for (int x = tid; x < n * dv; x += T) { /* a 32-lane half-wave holds one A8 block */
+        const int t = x / dv, jj = x - t * dv;
         const float ov = so[t * dv + jj];
-        const float zv = t < n0 ? sz[x] : a.z[(size_t)t * a.z_stride + h * dv + jj];
-        float yv = (ov * r) * sw[jj];
-        yv = yv * nmx_silu(zv);
+        const float gz = nmx_silu(t < n0 ? sz[x] : a.z[(size_t)t * a.z_stride + h * dv + jj]);
+        float yv = (ov * srn[2 * n + t]) * sw[jj];
+        yv = yv * gz;
         const int col = h * dv + jj;
         if (a.y) a.y[(size_t)t * a.y_stride + col] = yv;
         if (a.aq) {
@@ -374,16 +385,16 @@ int nmx_lin_mix(nmx_ctx *ctx, const nmx_lin_mix_args *a) {
     const size_t lds = (size_t)mix_lds_floats(n, dk, dv) * 4;
     /* one value head per key head: with shared key heads, a workgroup could read a shared
      * q / k channel's conv state after its owner committed token 0 into it */
-    /* the fused kernel reads the conv inputs as channel pairs (2 dk + dv <= 2 T), a batch of
-     * pending keys as two elements per thread (dk <= dv) and z / w / the taps as float4:
-     * K = 4, even channel strides, 16-byte aligned z, w and taps */
+    /* the fused kernel gives each thread of the first T - 64 one conv channel (the last wave
+     * computes the gates: 2 dk + dv <= T - 64), a batch of
+     * pending keys two elements per thread (dk <= dv), and reads z / w / the taps as float4:
+     * K = 4, 16-byte aligned z, w and taps */
     auto al = [](const void *q, unsigned m) { return ((uintptr_t)q & (m - 1)) == 0; };
-    const bool vec_ok = p.conv_k == 4 && p.C % 2 == 0 && p.raw_stride % 2 == 0 &&
-                        a->z_stride % 4 == 0 && al(p.raw, 8) && al(p.state, 8) &&
-                        (!p.xin || al(p.xin, 8)) && al(p.conv_w, 16) && al(a->z, 16) &&
-                        al(a->norm_w, 16);
+    const bool vec_ok = p.conv_k == 4 && a->z_stride % 4 == 0 && al(p.conv_w, 16) &&
+                        al(a->z, 16) && al(a->norm_w, 16);
     const bool fused = r.rep == 1 && (dk == 64 || dk == 128) && 4 * dv <= MIX_MAX_THREADS &&
-                       dk <= dv && lds <= MIX_LDS && vec_ok && !(r.log0 && !r.log);
+                       dk <= dv && 2 * dk + dv <= 4 * dv - 64 && lds <= MIX_LDS && vec_ok &&
+                       !(r.log0 && !r.log);
     if (!fused) { /* the separate kernels, through the intermediate buffers of the structs */
         if (nmx_lin_pre(ctx, &p) || nmx_lin_rule(ctx, &r)) return -1;
         return nmx_lin_post(ctx, r.o, r.o_stride, a->z, a->z_stride, a->norm_w, n, r.heads, dv,
