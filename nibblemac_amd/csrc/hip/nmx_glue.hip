@@ -469,19 +469,36 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
  * any order: only its value is used, and exp(x - (+-0)) agrees), e_p = exp(s_p - max) with
  * 4 partial sums + tail, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] accumulated in p
  * order from zero; o *= sigmoid(gate) (forward_attn.c:217-220); + A8 of o for o_proj.
- * Workgroup = (64 output dims, head h, token t): all four waves stage V tiles of PV_TP rows
- * (double-buffered, the next tile's loads in flight during the current tile's chain); wave 0
- * runs the 64 per-dimension chains. */
-constexpr int PV_TP = 32;
+ * Workgroup = (PV_DS output dims, head h, token t); one workgroup per CU (160 for the 0.8B
+ * verify shape). The first PV_PT value rows of the slice are requested at entry, before the
+ * softmax; each tile lands in LDS as w_p v_p[d] (the products the chain adds), and the next
+ * tile's loads are issued before the current tile's chain, so that the chain lanes (one per
+ * dimension) only add. */
+constexpr int PV_DS = 64;           /* output dims per workgroup: two A8 blocks */
+constexpr int PV_PT = 448;          /* positions per LDS tile */
+constexpr int PV_PER = PV_PT * (PV_DS / 4) / 256; /* float4 tile loads per thread */
 __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict__ sc) {
     extern __shared__ float4 smem4[];
     __shared__ float red[8];
-    const int tid = threadIdx.x, d0 = blockIdx.x * 64, h = blockIdx.y, t = blockIdx.z;
+    constexpr int F4 = PV_DS / 4;
+    const int tid = threadIdx.x, d0 = blockIdx.x * PV_DS, h = blockIdx.y, t = blockIdx.z;
     const int hd = a.hd, g = h / (a.nh / a.nkv);
     const int np = *a.pos + a.pos_off + t + 1;
     float *att = (float *)smem4;                    /* [max_ctx] */
-    float *vt = att + ((a.max_ctx + 3) & ~3);       /* [2][PV_TP][64] */
+    float *vt = att + ((a.max_ctx + 3) & ~3);       /* [PV_PT][PV_DS] */
     const float *srow = sc + ((size_t)t * a.nh + h) * a.max_ctx;
+    const float *V = a.vc + (size_t)g * a.max_ctx * hd + d0;
+    /* tile values: element f = u * 256 + tid is float4 (f % F4) of tile row f / F4 */
+    float4 vb[PV_PER];
+    auto load_tile = [&](int base, int rows) {
+#pragma unroll
+        for (int u = 0; u < PV_PER; u++) {
+            const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
+            vb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (r < rows) vb[u] = *(const float4 *)(V + (size_t)(base + r) * hd + 4 * c4);
+        }
+    };
+    load_tile(0, np < PV_PT ? np : PV_PT);
     for (int p0 = 0; p0 < np; p0 += 4 * 256) {
         float b[4];
 #pragma unroll
@@ -509,44 +526,36 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     const float inv = 1.0f / ordered_sum4(att, np, red);
     for (int p = tid; p < np; p += 256) att[p] = att[p] * inv;
 
-    /* V tiles: element (r, c4) of a tile = float4 c4 of dims d0.. of row p = tile base + r */
-    const float *V = a.vc + (size_t)g * a.max_ctx * hd + d0;
-    constexpr int PER = PV_TP * 16 / 256;
-    float4 nx[PER];
-#pragma unroll
-    for (int u = 0; u < PER; u++) {
-        const int f = u * 256 + tid, r = f >> 4, c4 = f & 15;
-        nx[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < np) nx[u] = *(const float4 *)(V + (size_t)r * hd + 4 * c4);
-    }
     float o = 0.0f;
-    for (int base = 0, buf = 0; base < np; base += PV_TP, buf ^= 1) {
-        float *tile = vt + buf * PV_TP * 64;
+    for (int base = 0; base < np; base += PV_PT) {
+        const int rows = np - base < PV_PT ? np - base : PV_PT;
+        __syncthreads(); /* att scaled; the previous tile's chain is done */
 #pragma unroll
-        for (int u = 0; u < PER; u++) { /* rows past np hold zeros and are never read */
-            const int f = u * 256 + tid, r = f >> 4, c4 = f & 15;
-            *(float4 *)(tile + r * 64 + 4 * c4) = nx[u];
-        }
-        __syncthreads(); /* tile staged and att scaled */
-        const int nb = base + PV_TP;
-#pragma unroll
-        for (int u = 0; u < PER; u++) {
-            const int f = u * 256 + tid, r = f >> 4, c4 = f & 15;
-            nx[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (nb + r < np) nx[u] = *(const float4 *)(V + (size_t)(nb + r) * hd + 4 * c4);
-        }
-        if (tid < 64) {
-            const int cnt = np - base < PV_TP ? np - base : PV_TP;
-            const float *ap = att + base;
-            if (cnt == PV_TP) {
-#pragma unroll
-                for (int r = 0; r < PV_TP; r++) o = o + ap[r] * tile[r * 64 + tid];
-            } else {
-                for (int r = 0; r < cnt; r++) o = o + ap[r] * tile[r * 64 + tid];
+        for (int u = 0; u < PV_PER; u++) {
+            const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
+            if (r < rows) {
+                const float w = att[base + r];
+                *(float4 *)(vt + r * PV_DS + 4 * c4) =
+                    make_float4(w * vb[u].x, w * vb[u].y, w * vb[u].z, w * vb[u].w);
             }
         }
+        __syncthreads();
+        const int next = base + PV_PT;
+        if (next < np) load_tile(next, np - next < PV_PT ? np - next : PV_PT);
+        if (tid < PV_DS) {
+            const float *pr = vt + tid;
+            int r = 0;
+            for (; r + 16 <= rows; r += 16) {
+                float b[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) b[u] = pr[(r + u) * PV_DS];
+#pragma unroll
+                for (int u = 0; u < 16; u++) o = o + b[u];
+            }
+            for (; r < rows; r++) o = o + pr[r * PV_DS];
+        }
     }
-    if (tid < 64) {
+    if (tid < PV_DS) {
         const int d = d0 + tid;
         const float *qrow = a.q + ((size_t)t * a.nh + h) * 2 * hd;
         o = o * nmx_sigmoid(qrow[hd + d]);
@@ -737,8 +746,15 @@ int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p) {
     if (cp == 32) attn_score_k<32><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
     else attn_score_k<16><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
     NMX_LAUNCHED(ctx, "attn_score");
-    dim3 pgrid((unsigned)(p->hd / 64), (unsigned)p->nh, (unsigned)p->n);
-    const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + 2 * PV_TP * 64) * 4;
+    dim3 pgrid((unsigned)(p->hd / PV_DS), (unsigned)p->nh, (unsigned)p->n);
+    const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + (size_t)PV_PT * PV_DS) * 4;
+    static bool pv_ready = false; /* idempotent */
+    if (!pv_ready) {
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_pv_k,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)((8192 + (size_t)PV_PT * PV_DS) * 4)));
+        pv_ready = true;
+    }
     attn_pv_k<<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
     NMX_LAUNCHED(ctx, "attn_pv");
     return 0;

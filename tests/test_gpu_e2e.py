@@ -123,6 +123,23 @@ def test_stop_inside_commit(agree_model):
 
 
 @needs_ref
+def test_long_context(models):
+    """A 1000-token context: the attention's value rows then span two LDS tiles (896 positions
+    each) in the prefill chunks and in the single-token steps after them."""
+    gpu, ref = pair(models["small"], max_ctx=1200)
+    rng = np.random.default_rng(13)
+    prompt = rng.integers(0, pqfile.SMALL.vocab, 1000)
+    print("[case] long context prefill 1000", flush=True)
+    assert np.array_equal(bits(gpu.eval(prompt)), bits(ref.eval(prompt))), "after 1000-token prefill"
+    for tok in rng.integers(0, pqfile.SMALL.vocab, 3):
+        assert np.array_equal(bits(gpu.eval([tok])), bits(ref.eval([tok]))), "single steps"
+    tg, sg = gpu.generate([int(tok)], 12, k=4, draft_vocab=1024, cont=True)
+    tr, sr = ref.generate([int(tok)], 12, k=4, draft_vocab=1024, cont=True)
+    assert tg == tr and (sg.rounds, sg.accepted) == (sr.rounds, sr.accepted)
+    gpu.close(), ref.close()
+
+
+@needs_ref
 def test_generate_continuation_and_stop_ids(models):
     gpu, ref = pair(models["small"])
     prompt = np.random.default_rng(3).integers(0, pqfile.SMALL.vocab, 20)
