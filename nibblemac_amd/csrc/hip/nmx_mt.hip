@@ -13,12 +13,13 @@
  *      line and the row's four 16-byte code chunks) is loaded first; meanwhile the pass's A8
  *      activations are staged into LDS (copied, or computed by the RMSNorm prologue);
  *   1. every unit decodes its sub-scales and computes its 4 blocks x NV exact int32 dots with
- *      v_dot4_i32_i8, storing ((float)dot, (D*s)*d_v) pairs and -(M*m) to LDS laid out
- *      [block][vector][row] (up to 160 KB of LDS per workgroup on gfx950);
+ *      v_dot4_i32_i8, storing one record ((float)dot, (D*s)*d_v, -(M*m), fsum_v) per (block,
+ *      vector, row) to LDS laid out [block][vector][row] (the 64-row SwiGLU launch stores
+ *      ((float)dot, (D*s)*d_v) pairs and -(M*m) separately, to fit in 160 KB);
  *   2. one lane per (row, vector) runs the fp32 chain over the blocks in column order, two
- *      FMAs per block from three conflict-free LDS reads, then stores the row (or, for
- *      SwiGLU, the workgroup combines its gate and up halves, silu(g) * u, and quantizes the
- *      result to A8).
+ *      FMAs per block from one 16-byte LDS read (three reads for SwiGLU), then stores the row
+ *      (or, for SwiGLU, the workgroup combines its gate and up halves, silu(g) * u, and
+ *      quantizes the result to A8).
  * The RMSNorm prologue restates engine/src/forward_ops.c:168-200 (sumsq as 4 interleaved
  * partial sums + tail, r = 1 / sqrtf(ss / cols + eps), y = (x * r) * w) and the A8 of
  * engine/src/kern_act.c:14-42, so the activations equal those of the separate kernels. */
@@ -81,8 +82,9 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     L.ad = (aq_off(nb, nv) + 15) & ~15;
     L.afs = L.ad + nb * nv * 4;
     L.work = (L.afs + nb * nv * 4 + 15) & ~15;
-    /* ((float)dot, (D*s)*d) [nb][nv][R] float2, then -(M*m) [nb][R] */
-    int work = nb * nv * R * 8 + nb * R * 4;
+    /* chain records: (dot, (D*s)*d, -(M*m), fsum) float4 [nb][nv][R]; the SwiGLU launch (64
+     * rows) keeps ((float)dot, (D*s)*d) float2 [nb][nv][R] and -(M*m) [nb][R] to fit */
+    int work = swiglu ? nb * nv * R * 8 + nb * R * 4 : nb * nv * R * 16;
     const int nwork = nv * (4 * cm_stride4(cols) + 4) * 4;
     if (norm && nwork > work) work = nwork;
     L.res = L.work + work;
@@ -102,6 +104,8 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
     const MtLayout L = mt_layout(cols, NV, R, NORM, SWI);
     int8_t *aq = (int8_t *)(smem + L.aq);
     float *ad = (float *)(smem + L.ad), *afs = (float *)(smem + L.afs);
+    constexpr bool REC = !SWI; /* one float4 record per (block, vector, row) */
+    float4 *rec = (float4 *)(smem + L.work);  /* [nb][NV][R] (dot, (D*s)*d, -(M*m), fsum) */
     float2 *lp = (float2 *)(smem + L.work);  /* [nb][NV][R] ((float)dot, (D*s)*d) */
     float *lof = (float *)(lp + nb * NV * R); /* [nb][R] -(M*m) */
 
@@ -295,7 +299,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
             const int blk = blk0 + k;
             const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
             const float of = M * (float)m6[k];
-            lof[blk * R + u_r] = -of;
+            if constexpr (!REC) lof[blk * R + u_r] = -of;
             const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
             const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
             const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
@@ -313,7 +317,10 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
                 dot = __builtin_amdgcn_sdot4(hi1, x1.y, dot, false);
                 dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
                 dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
-                lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * dv);
+                if constexpr (REC)
+                    rec[(blk * NV + v) * R + u_r] = make_float4((float)dot, sc * dv, -of, afs[blk * NV + v]);
+                else
+                    lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * dv);
             }
         }
     }
@@ -326,6 +333,25 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
     float acc = 0.0f;
     if (chain) {
         /* per block: acc = fma((float)dot, (D*s)*d_v, acc); acc = fma(-(M*m), fsum_v, acc) */
+        if constexpr (REC) {
+            const float4 *rp = rec + cv * R + cr;
+            int b = 0;
+            for (; b + 8 <= nb; b += 8) {
+                float4 r[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) r[u] = rp[(b + u) * NV * R];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    acc = __builtin_fmaf(r[u].x, r[u].y, acc);
+                    acc = __builtin_fmaf(r[u].z, r[u].w, acc);
+                }
+            }
+            for (; b < nb; b++) {
+                const float4 r = rp[b * NV * R];
+                acc = __builtin_fmaf(r.x, r.y, acc);
+                acc = __builtin_fmaf(r.z, r.w, acc);
+            }
+        } else {
         const float2 *pp = lp + cv * R + cr;
         const float *op = lof + cr;
         int b = 0;
@@ -349,6 +375,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
             const float ff = afs[b * NV + cv];
             acc = __builtin_fmaf(pv.x, pv.y, acc);
             acc = __builtin_fmaf(op[b * R], ff, acc);
+        }
         }
     }
     if constexpr (!SWI) {
@@ -374,11 +401,13 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : MT_MAX_THREADS) void q4k_m
     }
 }
 
-/* Rows per workgroup for a pass of nv vectors: the largest R (64, 32, ... 4) whose LDS and
- * thread counts fit; SwiGLU needs R = 64 (32 gate + 32 up rows = one A8 block). */
+/* Rows per workgroup for a pass of nv vectors. SwiGLU needs R = 64 (32 gate + 32 up rows = one
+ * A8 block). The other launches use chain records and R = 8 (else 4): measured on the verify
+ * shapes (1024 .. 3584 columns, 5 vectors) this beat every larger R, since a small workgroup's
+ * dot and chain phases are short and several workgroups share a CU. */
 int pick_rows(int cols, int nv, bool norm, bool swiglu, int *threads) {
     const int nsb = cols >> 8;
-    for (int R = 64; R >= 4; R >>= 1) {
+    for (int R = swiglu ? 64 : 8; R >= 4; R >>= 1) {
         if (swiglu && R != 64) break;
         const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
         if (t > (norm ? MT_NORM_THREADS : MT_MAX_THREADS)) continue;
