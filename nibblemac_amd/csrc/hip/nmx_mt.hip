@@ -30,7 +30,7 @@
 namespace {
 
 constexpr int MT_MAX_NV = 8;
-constexpr int MT_MAX_THREADS = 1024;
+constexpr int MT_MAX_THREADS = 512; /* the SwiGLU launch (64 rows; the dots' VGPR buffers) */
 constexpr int MT_LDS = 159 * 1024; /* dynamic LDS per workgroup (gfx950: 160 KB) */
 constexpr int MT_NORM_CPT = 8; /* columns per thread in the norm prologue */
 constexpr int MT_NORM_THREADS = 512; /* the prologue keeps NV x MT_NORM_CPT values in VGPRs */
@@ -295,75 +295,43 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
         decode6_half(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, u_h & 1, s6);
         decode6_half(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, u_h & 1, m6);
         const int blk0 = u_sb * 8 + u_k0;
-        if constexpr (REC) {
-            /* the unit's 4 blocks x NV scales d and fsum (4 NV consecutive floats each, read as
-             * NV float4), then the activations block by block, the next block's 2 NV reads
-             * issued before the current block's dots */
-            float sdv[4 * NV], sfv[4 * NV];
+        /* the unit's 4 blocks x NV scales d and fsum (4 NV consecutive floats each, read as NV
+         * float4), then the activations block by block, the next block's 2 NV reads issued
+         * before the current block's dots */
+        float sdv[4 * NV], sfv[4 * NV];
 #pragma unroll
-            for (int i = 0; i < NV; i++) {
-                const float4 x = *(const float4 *)(ad + blk0 * NV + 4 * i);
-                const float4 y = *(const float4 *)(afs + blk0 * NV + 4 * i);
-                sdv[4 * i] = x.x, sdv[4 * i + 1] = x.y, sdv[4 * i + 2] = x.z, sdv[4 * i + 3] = x.w;
-                sfv[4 * i] = y.x, sfv[4 * i + 1] = y.y, sfv[4 * i + 2] = y.z, sfv[4 * i + 3] = y.w;
-            }
-            int4 xa[NV][2], xn[NV][2];
+        for (int i = 0; i < NV; i++) {
+            const float4 x = *(const float4 *)(ad + blk0 * NV + 4 * i);
+            const float4 y = *(const float4 *)(afs + blk0 * NV + 4 * i);
+            sdv[4 * i] = x.x, sdv[4 * i + 1] = x.y, sdv[4 * i + 2] = x.z, sdv[4 * i + 3] = x.w;
+            sfv[4 * i] = y.x, sfv[4 * i + 1] = y.y, sfv[4 * i + 2] = y.z, sfv[4 * i + 3] = y.w;
+        }
+        int4 xa[NV][2], xn[NV][2];
 #pragma unroll
-            for (int v = 0; v < NV; v++) {
-                const int8_t *xb = aq + aq_off(blk0, NV) + v * 32;
-                xa[v][0] = *(const int4 *)xb, xa[v][1] = *(const int4 *)(xb + 16);
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int blk = blk0 + k;
-                if (k < 3) {
-#pragma unroll
-                    for (int v = 0; v < NV; v++) {
-                        const int8_t *xb = aq + aq_off(blk + 1, NV) + v * 32;
-                        xn[v][0] = *(const int4 *)xb, xn[v][1] = *(const int4 *)(xb + 16);
-                    }
-                }
-                const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
-                const float of = M * (float)m6[k];
-                const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
-                const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
-                const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
-                const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
-#pragma unroll
-                for (int v = 0; v < NV; v++) {
-                    const int4 x0 = xa[v][0], x1 = xa[v][1];
-                    int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
-                    dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
-                    dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
-                    dot = __builtin_amdgcn_sdot4(lo3, x0.w, dot, false);
-                    dot = __builtin_amdgcn_sdot4(hi0, x1.x, dot, false);
-                    dot = __builtin_amdgcn_sdot4(hi1, x1.y, dot, false);
-                    dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
-                    dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
-                    rec[(blk * NV + v) * R + u_r] =
-                        make_float4((float)dot, sc * sdv[k * NV + v], -of, sfv[k * NV + v]);
-                }
-                if (k < 3) {
-#pragma unroll
-                    for (int v = 0; v < NV; v++) xa[v][0] = xn[v][0], xa[v][1] = xn[v][1];
-                }
-            }
-        } else {
+        for (int v = 0; v < NV; v++) {
+            const int8_t *xb = aq + aq_off(blk0, NV) + v * 32;
+            xa[v][0] = *(const int4 *)xb, xa[v][1] = *(const int4 *)(xb + 16);
+        }
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int blk = blk0 + k;
+            if (k < 3) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const int8_t *xb = aq + aq_off(blk + 1, NV) + v * 32;
+                    xn[v][0] = *(const int4 *)xb, xn[v][1] = *(const int4 *)(xb + 16);
+                }
+            }
             const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
             const float of = M * (float)m6[k];
-            lof[blk * R + u_r] = -of;
+            if constexpr (!REC) lof[blk * R + u_r] = -of;
             const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
             const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
             const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
             const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
 #pragma unroll
             for (int v = 0; v < NV; v++) {
-                const int8_t *xb = aq + aq_off(blk, NV) + v * 32;
-                const int4 x0 = *(const int4 *)xb, x1 = *(const int4 *)(xb + 16);
-                const float dv = ad[blk * NV + v];
+                const int4 x0 = xa[v][0], x1 = xa[v][1];
                 int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
                 dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
                 dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
@@ -372,9 +340,16 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
                 dot = __builtin_amdgcn_sdot4(hi1, x1.y, dot, false);
                 dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
                 dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
-                lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * dv);
+                if constexpr (REC)
+                    rec[(blk * NV + v) * R + u_r] =
+                        make_float4((float)dot, sc * sdv[k * NV + v], -of, sfv[k * NV + v]);
+                else
+                    lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * sdv[k * NV + v]);
             }
-        }
+            if (k < 3) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) xa[v][0] = xn[v][0], xa[v][1] = xn[v][1];
+            }
         }
     }
     __syncthreads();
