@@ -168,6 +168,87 @@ __global__ __launch_bounds__(256) void rmsnorm_k(const float *x, int x_stride,
     }
 }
 
+/* The same RMSNorm with each thread owning 4 consecutive columns (float4 loads and stores,
+ * cols % 4 == 0, 16-byte aligned rows): element 4 j + l is term j of partial sum l, so the squares
+ * go to LDS chain-major directly; a 32-column A8 block is 8 consecutive lanes (its amax and the
+ * code sum reduced over them by DPP, exact in any order). */
+__device__ __forceinline__ void a8_block4(float4 x, int b, int v, int n, int8_t *q, float *d,
+                                          float *fs) {
+    const size_t u = (size_t)b * n + v;
+    const int l8 = threadIdx.x & 7;
+    float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    m = fmaxf(m, __int_as_float(nmx_dpp<NMX_DPP_XOR1>(__float_as_int(m))));
+    m = fmaxf(m, __int_as_float(nmx_dpp<NMX_DPP_XOR2>(__float_as_int(m))));
+    m = fmaxf(m, __int_as_float(nmx_dpp<NMX_DPP_HALF_MIRROR>(__float_as_int(m))));
+    const float id = m > 0.0f ? 127.0f / m : 0.0f;
+    const int c0 = (int)rintf(x.x * id), c1 = (int)rintf(x.y * id);
+    const int c2 = (int)rintf(x.z * id), c3 = (int)rintf(x.w * id);
+    int sum = (c0 + c1) + (c2 + c3);
+    sum += nmx_dpp<NMX_DPP_XOR1>(sum);
+    sum += nmx_dpp<NMX_DPP_XOR2>(sum);
+    sum += nmx_dpp<NMX_DPP_HALF_MIRROR>(sum);
+    auto cl = [](int c) { return (uint32_t)(uint8_t)(int8_t)(c > 127 ? 127 : c < -128 ? -128 : c); };
+    ((uint32_t *)(q + u * 32))[l8] = cl(c0) | cl(c1) << 8 | cl(c2) << 16 | cl(c3) << 24;
+    if (l8 == 0) {
+        const float dd = m / 127.0f;
+        d[u] = dd;
+        fs[u] = dd * (float)sum;
+    }
+}
+
+template <int P4>
+__global__ __launch_bounds__(256) void rmsnorm4_k(const float *x, int x_stride,
+                                                  const float *add, int add_stride,
+                                                  float *xo, int xo_stride,
+                                                  const float *__restrict__ w, int cols, float eps,
+                                                  float *__restrict__ y, int y_stride,
+                                                  int8_t *__restrict__ q, float *__restrict__ d,
+                                                  float *__restrict__ fs, int n) {
+    extern __shared__ float sq[]; /* chain-major squares */
+    __shared__ float red[8];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int c4 = cols >> 2, s4 = cm_stride(cols);
+    const float4 *xr = (const float4 *)(x + (size_t)row * x_stride);
+    float4 v[P4], wv[P4];
+#pragma unroll
+    for (int u = 0; u < P4; u++) { /* clamped (always in-bounds) loads */
+        const int j = tid + 256 * u, jc = j < c4 ? j : c4 - 1;
+        v[u] = xr[jc];
+        wv[u] = ((const float4 *)w)[jc];
+    }
+    if (add) {
+        const float4 *ar = (const float4 *)(add + (size_t)row * add_stride);
+#pragma unroll
+        for (int u = 0; u < P4; u++) {
+            const int j = tid + 256 * u;
+            const float4 a4 = ar[j < c4 ? j : c4 - 1];
+            v[u] = make_float4(v[u].x + a4.x, v[u].y + a4.y, v[u].z + a4.z, v[u].w + a4.w);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < P4; u++) {
+        const int j = tid + 256 * u;
+        if (j >= c4) continue;
+        if (xo) ((float4 *)(xo + (size_t)row * xo_stride))[j] = v[u];
+        sq[j] = v[u].x * v[u].x;
+        sq[s4 + j] = v[u].y * v[u].y;
+        sq[2 * s4 + j] = v[u].z * v[u].z;
+        sq[3 * s4 + j] = v[u].w * v[u].w;
+    }
+    __syncthreads();
+    const float ss = ordered_sum4_cm(sq, cols, s4, red);
+    const float r = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+    for (int u = 0; u < P4; u++) {
+        const int j = tid + 256 * u;
+        if (256 * u + (tid & ~7) >= c4) continue; /* whole 8-lane group past the row */
+        const float4 o = make_float4((v[u].x * r) * wv[u].x, (v[u].y * r) * wv[u].y,
+                                     (v[u].z * r) * wv[u].z, (v[u].w * r) * wv[u].w);
+        if (y) ((float4 *)(y + (size_t)row * y_stride))[j] = o;
+        if (q) a8_block4(o, j >> 3, row, n, q, d, fs);
+    }
+}
+
 /* ---- Gated DeltaNet pre (engine/src/forward_lin.c:36-67): per channel the causal conv over
  * [state rows, tokens] in tap order, SiLU (forward_ops.c:237-260); q / k heads L2-normalised
  * (eps 1e-6) with q scaled by 1/sqrt(dk) (forward_ops.c:204-212). Logged pass: the live
@@ -649,6 +730,21 @@ int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
         return nmx_fail(ctx, "nmx_rmsnorm: bad arguments n=%d cols=%d", n, cols);
     if (a8.q && (cols % 32 || !a8.d || !a8.fs)) return nmx_fail(ctx, "nmx_rmsnorm: bad A8 output");
     const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (cols % 32 == 0 && cols <= 4096 && x_stride % 4 == 0 && al16(x) && al16(w) &&
+        (!add || (add_stride % 4 == 0 && al16(add))) && (!xo || (xo_stride % 4 == 0 && al16(xo))) &&
+        (!y || (y_stride % 4 == 0 && al16(y)))) {
+#define NMX_RMS4(P)                                                                             \
+    rmsnorm4_k<P><<<(unsigned)n, 256, lds, ctx->stream>>>(x, x_stride, add, add_stride, xo,     \
+                                                          xo_stride, w, cols, eps, y, y_stride, \
+                                                          a8.q, a8.d, a8.fs, n)
+        if (cols <= 1024) NMX_RMS4(1);
+        else if (cols <= 2048) NMX_RMS4(2);
+        else NMX_RMS4(4);
+#undef NMX_RMS4
+        NMX_LAUNCHED(ctx, "rmsnorm");
+        return 0;
+    }
 #define NMX_RMS(P)                                                                              \
     rmsnorm_k<P><<<(unsigned)n, 256, lds, ctx->stream>>>(x, x_stride, add, add_stride, xo,      \
                                                          xo_stride, w, cols, eps, y, y_stride,  \

@@ -78,6 +78,31 @@ def test_matmul_norm_equals_separate(dev, cols, shapes, n):
     q, d, fs = oracle.quant_a8(rmsnorm_restated(x + add, w, EPS))
     assert_bits_equal(a8[0].numpy(), q, "A8 codes of the norm")
     assert_bits_equal(a8[1].numpy(), d, "A8 scales of the norm")
+    assert_bits_equal(a8[2].numpy(), fs, "A8 fsum of the norm")
+
+
+@pytest.mark.parametrize("cols", [64, 1024, 2048, 3584, 4096, 4100, 8192])
+@pytest.mark.parametrize("n", [1, 5])
+def test_rmsnorm_outputs(dev, cols, n):
+    """The RMSNorm alone (float4 rows up to 4096 columns, the per-column kernel otherwise or
+    for widths that are not a multiple of 32): residual sum, y and A8 against the restated
+    summation order and the oracle's A8."""
+    print(f"[case] rmsnorm cols={cols} n={n}", flush=True)
+    rng = np.random.default_rng(7 * cols + n)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    add = rng.standard_normal((n, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    dx, dadd, dw = dev.to_device(x), dev.to_device(add), dev.to_device(w)
+    xo, y = dev.zeros((n, cols), np.float32), dev.zeros((n, cols), np.float32)
+    a8 = a8_bufs(dev, n, cols) if cols % 32 == 0 else (None, None, None)
+    dev.rmsnorm(dx, n, cols, dw, EPS, add=dadd, xo=xo, y=y, a8=a8)
+    dev.sync()
+    want = rmsnorm_restated(x + add, w, EPS)
+    assert_bits_equal(xo.numpy(), x + add, "residual sum")
+    assert_bits_equal(y.numpy(), want, "y")
+    if cols % 32 == 0:
+        for got, ref, what in zip(a8, oracle.quant_a8(want), ("codes", "scales", "fsum")):
+            assert_bits_equal(got.numpy(), ref, f"A8 {what}")
 
 
 @pytest.mark.parametrize("n", [1, 2, 5, 6, 8, 13])
