@@ -550,48 +550,101 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
  * any order: only its value is used, and exp(x - (+-0)) agrees), e_p = exp(s_p - max) with
  * 4 partial sums + tail, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] accumulated in p
  * order from zero; o *= sigmoid(gate) (forward_attn.c:217-220); + A8 of o for o_proj.
- * Workgroup = (PV_DS output dims, head h, token t); one workgroup per CU (160 for the 0.8B
- * verify shape). The first PV_PT value rows of the slice are requested at entry, before the
- * softmax; each tile lands in LDS as w_p v_p[d] (the products the chain adds), and the next
- * tile's loads are issued before the current tile's chain, so that the chain lanes (one per
- * dimension) only add. */
+ * Workgroup = (PV_DS output dims, head h, token t). Linear workgroup i takes value slice
+ * (dims, KV group) i mod S and (query head of the group, token) i / S, S = hd / PV_DS x nkv:
+ * consecutive workgroups go to different XCDs (round-robin), so the workgroups reading one
+ * slice share one XCD's L2. The scores row and the first PV_PT value rows are requested at
+ * entry; each tile lands in LDS as w_p v_p[d] (the products the chain adds). Wave 0's lanes
+ * run the chains (one per dimension), reading 3 batches of 8 positions ahead of the adds; while
+ * wave 0 runs a tile's chains, waves 1-3 load the next PV_PT2 rows. */
 constexpr int PV_DS = 64;           /* output dims per workgroup: two A8 blocks */
-constexpr int PV_PT = 448;          /* positions per LDS tile */
-constexpr int PV_PER = PV_PT * (PV_DS / 4) / 256; /* float4 tile loads per thread */
+constexpr int PV_PT = 448;          /* positions of the first tile */
+constexpr int PV_PT2 = 192;         /* positions of each later tile (loaded by waves 1-3) */
+constexpr int PV_PER = PV_PT * (PV_DS / 4) / 256;    /* float4 loads per thread, first tile */
+constexpr int PV_PER2 = PV_PT2 * (PV_DS / 4) / 192;  /* per thread of waves 1-3, later tiles */
+
+/* acc += x[0] + ... + x[n-1] in order, x[i] = p[i * stride] in LDS, with the reads of 3
+ * batches of 8 in flight ahead of the adds (at most 12 LDS reads outstanding). The scheduling
+ * barriers keep each batch's reads where they are issued: left alone, the scheduler sinks
+ * them to just before their adds, and every batch then waits the full LDS latency. */
+__device__ __forceinline__ float pv_chain(float acc, const float *p, int stride, int n) {
+    int r = 0;
+    if (n >= 24) {
+        float A[8], B[8], C[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) A[u] = p[u * stride], B[u] = p[(8 + u) * stride];
+        for (; r + 24 <= n; r += 24) {
+            /* A = r .. r+7, B = r+8 .. r+15 loaded; reads past n are clamped (not used) */
+            const int c0 = r + 16, a0 = r + 24 + 8 <= n ? r + 24 : r, b0 = r + 32 + 8 <= n ? r + 32 : r;
+#pragma unroll
+            for (int u = 0; u < 8; u++) C[u] = p[(c0 + u) * stride];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = acc + A[u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) A[u] = p[(a0 + u) * stride];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = acc + B[u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) B[u] = p[(b0 + u) * stride];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = acc + C[u];
+        }
+        /* A holds r .. r+7 and B r+8 .. r+15 when those are in range */
+        if (r + 8 <= n) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = acc + A[u];
+            r += 8;
+            if (r + 8 <= n) {
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc = acc + B[u];
+                r += 8;
+            }
+        }
+    }
+    for (; r < n; r++) acc = acc + p[r * stride];
+    return acc;
+}
+
 __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict__ sc) {
     extern __shared__ float4 smem4[];
     __shared__ float red[8];
     constexpr int F4 = PV_DS / 4;
-    const int tid = threadIdx.x, d0 = blockIdx.x * PV_DS, h = blockIdx.y, t = blockIdx.z;
-    const int hd = a.hd, g = h / (a.nh / a.nkv);
+    const int hd = a.hd, rep = a.nh / a.nkv, S = (hd / PV_DS) * a.nkv;
+    const int tid = threadIdx.x, sl = blockIdx.x % S, k = blockIdx.x / S;
+    const int d0 = (sl % (hd / PV_DS)) * PV_DS, g = sl / (hd / PV_DS);
+    const int h = g * rep + k % rep, t = k / rep;
     const int np = *a.pos + a.pos_off + t + 1;
     float *att = (float *)smem4;                    /* [max_ctx] */
     float *vt = att + ((a.max_ctx + 3) & ~3);       /* [PV_PT][PV_DS] */
     const float *srow = sc + ((size_t)t * a.nh + h) * a.max_ctx;
     const float *V = a.vc + (size_t)g * a.max_ctx * hd + d0;
-    /* tile values: element f = u * 256 + tid is float4 (f % F4) of tile row f / F4 */
+    /* the scores row, then the first tile's values (element f = u 256 + tid: float4 f % F4 of
+     * row f / F4) */
+    float bs[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int p = u * 256 + tid;
+        bs[u] = p < np ? srow[p] : 0.0f;
+    }
+    const int rows0 = np < PV_PT ? np : PV_PT;
     float4 vb[PV_PER];
-    auto load_tile = [&](int base, int rows) {
 #pragma unroll
-        for (int u = 0; u < PV_PER; u++) {
-            const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
-            vb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (r < rows) vb[u] = *(const float4 *)(V + (size_t)(base + r) * hd + 4 * c4);
-        }
-    };
-    load_tile(0, np < PV_PT ? np : PV_PT);
-    for (int p0 = 0; p0 < np; p0 += 4 * 256) {
-        float b[4];
+    for (int u = 0; u < PV_PER; u++) {
+        const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
+        vb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < rows0) vb[u] = *(const float4 *)(V + (size_t)r * hd + 4 * c4);
+    }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int p = p0 + u * 256 + tid;
-            b[u] = p < np ? srow[p] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int p = p0 + u * 256 + tid;
-            if (p < np) att[p] = b[u];
-        }
+    for (int u = 0; u < 4; u++) {
+        const int p = u * 256 + tid;
+        if (p < np) att[p] = bs[u];
+    }
+    for (int p0 = 4 * 256; p0 < np; p0 += 256) { /* contexts beyond 1024 positions */
+        const int p = p0 + tid;
+        if (p < np) att[p] = srow[p];
     }
     __syncthreads();
     float mx = -INFINITY;
@@ -604,37 +657,61 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     __syncthreads();
     for (int p = tid; p < np; p += 256) att[p] = nmx_expf_cephes(att[p] - mx);
     __syncthreads();
-    const float inv = 1.0f / ordered_sum4(att, np, red);
+    /* 4 partial sums over e[4m + l] (m ascending) + the tail, in the reference's order */
+    {
+        const int m4 = np >> 2;
+        if (tid < 4) red[tid] = pv_chain(0.0f, att + tid, 4, m4);
+        else if (tid == 4) {
+            float tl = 0.0f;
+            for (int i = 4 * m4; i < np; i++) tl = tl + att[i];
+            red[4] = tl;
+        }
+    }
+    __syncthreads();
+    const float inv = 1.0f / (((red[0] + red[1]) + (red[2] + red[3])) + red[4]);
     for (int p = tid; p < np; p += 256) att[p] = att[p] * inv;
 
     float o = 0.0f;
-    for (int base = 0; base < np; base += PV_PT) {
-        const int rows = np - base < PV_PT ? np - base : PV_PT;
-        __syncthreads(); /* att scaled; the previous tile's chain is done */
+    __syncthreads(); /* att scaled */
 #pragma unroll
-        for (int u = 0; u < PV_PER; u++) {
-            const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
-            if (r < rows) {
-                const float w = att[base + r];
-                *(float4 *)(vt + r * PV_DS + 4 * c4) =
-                    make_float4(w * vb[u].x, w * vb[u].y, w * vb[u].z, w * vb[u].w);
+    for (int u = 0; u < PV_PER; u++) {
+        const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
+        if (r < rows0) {
+            const float w = att[r];
+            *(float4 *)(vt + r * PV_DS + 4 * c4) =
+                make_float4(w * vb[u].x, w * vb[u].y, w * vb[u].z, w * vb[u].w);
+        }
+    }
+    __syncthreads();
+    for (int base = 0, rows = rows0; base < np;) {
+        const int next = base + rows, rows2 = np - next < PV_PT2 ? np - next : PV_PT2;
+        float4 nb[PV_PER2];
+        if (tid >= 64 && next < np) { /* waves 1-3: the next tile, during wave 0's chains */
+            const int f0 = tid - 64;
+#pragma unroll
+            for (int u = 0; u < PV_PER2; u++) {
+                const int f = u * 192 + f0, r = f / F4, c4 = f - r * F4;
+                nb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (r < rows2) nb[u] = *(const float4 *)(V + (size_t)(next + r) * hd + 4 * c4);
+            }
+        }
+        if (tid < PV_DS) o = pv_chain(o, vt + tid, PV_DS, rows);
+        __syncthreads(); /* the chains of this tile are done */
+        if (next >= np) break;
+        if (tid >= 64) {
+            const int f0 = tid - 64;
+#pragma unroll
+            for (int u = 0; u < PV_PER2; u++) {
+                const int f = u * 192 + f0, r = f / F4, c4 = f - r * F4;
+                if (r < rows2) {
+                    const float w = att[next + r];
+                    *(float4 *)(vt + r * PV_DS + 4 * c4) =
+                        make_float4(w * nb[u].x, w * nb[u].y, w * nb[u].z, w * nb[u].w);
+                }
             }
         }
         __syncthreads();
-        const int next = base + PV_PT;
-        if (next < np) load_tile(next, np - next < PV_PT ? np - next : PV_PT);
-        if (tid < PV_DS) {
-            const float *pr = vt + tid;
-            int r = 0;
-            for (; r + 16 <= rows; r += 16) {
-                float b[16];
-#pragma unroll
-                for (int u = 0; u < 16; u++) b[u] = pr[(r + u) * PV_DS];
-#pragma unroll
-                for (int u = 0; u < 16; u++) o = o + b[u];
-            }
-            for (; r < rows; r++) o = o + pr[r * PV_DS];
-        }
+        base = next, rows = rows2;
     }
     if (tid < PV_DS) {
         const int d = d0 + tid;
@@ -842,7 +919,7 @@ int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p) {
     if (cp == 32) attn_score_k<32><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
     else attn_score_k<16><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
     NMX_LAUNCHED(ctx, "attn_score");
-    dim3 pgrid((unsigned)(p->hd / PV_DS), (unsigned)p->nh, (unsigned)p->n);
+    const unsigned pgrid = (unsigned)((p->hd / PV_DS) * p->nh * p->n);
     const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + (size_t)PV_PT * PV_DS) * 4;
     static bool pv_ready = false; /* idempotent */
     if (!pv_ready) {
