@@ -76,7 +76,8 @@ static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *
 }
 
 /* post norm + SwiGLU MLP (engine/src/forward.c:49-58): x += mix out; xn = norm(x);
- * out = down(silu(gate xn) * up xn); the norm and the SwiGLU fused into the gate/up launch. */
+ * out = down(silu(gate xn) * up xn); silu(g) * u and its A8 fused into the gate/up launch (the
+ * norm as that launch's prologue measured slower: 13.3 us against 3.9 + 7.5 us). */
 static int mlp_block(pinfer_ctx *c, const e_layer *L, int n, e_resid *r) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
