@@ -334,6 +334,175 @@ __global__ __launch_bounds__(1024) void q4k_mv_ks_k(SegTable tab, int cols, int 
     }
 }
 
+/* Prefill chunks (more than 8 vectors): the int32 block dots on the matrix cores, one
+ * v_mfma_i32_16x16x32_i8 per (16 rows, 16 vectors, 32-column block), then the reference's
+ * ordered per-block FMA pair on the 16 x 16 result in registers.
+ *
+ * A wave owns 16 rows (four 4-row tiles) and NT tiles of 16 vectors; a workgroup of WAVES waves
+ * shares the activations of its vectors, staged in LDS one superblock at a time; the weights and
+ * activations of superblock sb + DIST are loaded into registers while sb is used (DIST = 2 for
+ * single-wave workgroups, whose latency nothing else on the CU hides; 1 where VGPRs are
+ * short).
+ * MFMA operand layout (16x16x32 i8, checked on gfx950): lane l supplies row (A) / column (B)
+ * l % 16 and the 8 K values of group g = l / 16; the result C[4 (l / 16) + j][l % 16] lands in
+ * the lane's element j. The 32 columns of a block may be dealt to the K positions in any order
+ * that is the same for both operands, since the int32 sum is exact: group g takes the low
+ * nibbles of code bytes 4g..4g+3 (columns 4g..4g+3) and their high nibbles (columns
+ * 16+4g..16+4g+3), and the staged activations are permuted to the same order. The lane's four
+ * result rows are the four rows of tile l / 16, whose 6-bit scales and mins for block k are
+ * decoded four at a time (one byte per row). Per (row, vector) the lane then runs
+ * acc = fma((float)dot, (D*s)*d, acc); acc = fma(-(M*m), fsum, acc) block by block. */
+template <int NT, int WAVES, int DIST>
+__global__ __launch_bounds__(64 * WAVES) void q4k_mm_k(SegTable tab, int cols, int n,
+                                                       const int8_t *__restrict__ q,
+                                                       const float *__restrict__ d,
+                                                       const float *__restrict__ fs) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    constexpr int NV16 = NT * 16, T = 64 * WAVES;
+    constexpr int SE = (8 * NV16 + T - 1) / T; /* staged (block, vector) entries per thread */
+    __shared__ __align__(16) uint8_t xs[8 * NV16 * 32]; /* [block][vector][g][8 B] */
+    __shared__ float2 xdf[8 * NV16];                    /* (d, fsum) per [block][vector] */
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int grp_raw = blockIdx.x * WAVES + w; /* 16-row group over all segments */
+    const bool live = grp_raw < tab.total_waves;
+    const int grp = live ? grp_raw : tab.total_waves - 1;
+    const uint8_t *W = tab.s[0].W;
+    float *Y = tab.s[0].Y;
+    int rows = tab.s[0].rows, ystride = tab.s[0].ystride, grp0 = tab.s[0].wave0;
+#pragma unroll
+    for (int t = 1; t < NMX_MAX_SEGS; t++)
+        if (t < tab.count && grp >= tab.s[t].wave0) {
+            W = tab.s[t].W;
+            Y = tab.s[t].Y;
+            rows = tab.s[t].rows;
+            ystride = tab.s[t].ystride;
+            grp0 = tab.s[t].wave0;
+        }
+    const int nsb = cols >> 8;
+    const int row0 = (grp - grp0) * 16;
+    const int vt0 = blockIdx.y * NV16, nvw = n - vt0 < NV16 ? n - vt0 : NV16;
+    const int g = lane >> 4, c16 = lane & 15;
+    /* operand A: row row0 + c16 (clamped into the matrix), code dword g of each block */
+    const int arow = row0 + c16 < rows ? row0 + c16 : rows - 1;
+    const uint8_t *ap = W + (size_t)(arow >> 2) * nsb * SB_BYTES + 64 + 16 * (arow & 3) + 4 * g;
+    /* result rows: tile g of the group (clamped), vector vt0 + 16 t + c16 */
+    const int erow0 = row0 + 4 * g < rows ? row0 + 4 * g : rows - 4;
+    const uint4 *hp = (const uint4 *)(W + (size_t)(erow0 >> 2) * nsb * SB_BYTES);
+
+    /* one superblock's inputs; DIST sets, loaded DIST superblocks ahead of their use */
+    struct Buf {
+        uint32_t cw[8];
+        uint4 h[4], x0[SE], x1[SE];
+        float2 df[SE];
+    };
+    auto fetch = [&](Buf &B, int sb) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) B.cw[k] = *(const uint32_t *)(ap + (size_t)sb * SB_BYTES + 64 * k);
+#pragma unroll
+        for (int u = 0; u < 4; u++) B.h[u] = hp[sb * 36 + u];
+#pragma unroll
+        for (int u = 0; u < SE; u++) {
+            const int e = u * T + tid, k = e / NV16, v = e - k * NV16;
+            B.x0[u] = B.x1[u] = make_uint4(0, 0, 0, 0);
+            B.df[u] = make_float2(0.0f, 0.0f);
+            if (e < 8 * NV16 && v < nvw) {
+                const size_t ai = (size_t)(sb * 8 + k) * n + vt0 + v;
+                B.x0[u] = *(const uint4 *)(q + ai * 32);
+                B.x1[u] = *(const uint4 *)(q + ai * 32 + 16);
+                B.df[u] = make_float2(d[ai], fs[ai]);
+            }
+        }
+    };
+
+    float acc[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[t][j] = 0.0f;
+    const v4i zero = {0, 0, 0, 0};
+
+    /* superblock sb from buffer B, whose set is then refilled with superblock sb + DIST */
+    auto step = [&](Buf &B, int sb) {
+        uint32_t cw[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) cw[k] = B.cw[k];
+        const uint4 h0 = B.h[0], h1 = B.h[1], h2 = B.h[2], h3 = B.h[3];
+        __syncthreads(); /* the previous superblock's activations are consumed */
+#pragma unroll
+        for (int u = 0; u < SE; u++) {
+            const int e = u * T + tid;
+            if (e < 8 * NV16) {
+                uint2 *dst = (uint2 *)(xs + (size_t)e * 32);
+                dst[0] = make_uint2(B.x0[u].x, B.x1[u].x);
+                dst[1] = make_uint2(B.x0[u].y, B.x1[u].y);
+                dst[2] = make_uint2(B.x0[u].z, B.x1[u].z);
+                dst[3] = make_uint2(B.x0[u].w, B.x1[u].w);
+                xdf[e] = B.df[u];
+            }
+        }
+        if (sb + DIST < nsb) fetch(B, sb + DIST);
+        __syncthreads();
+        float Dj[4], Mj[4];
+        Dj[0] = half_bits_to_float(h0.x), Dj[1] = half_bits_to_float(h0.x >> 16);
+        Dj[2] = half_bits_to_float(h0.y), Dj[3] = half_bits_to_float(h0.y >> 16);
+        Mj[0] = half_bits_to_float(h0.z), Mj[1] = half_bits_to_float(h0.z >> 16);
+        Mj[2] = half_bits_to_float(h0.w), Mj[3] = half_bits_to_float(h0.w >> 16);
+        const uint32_t SL[4] = {h1.x, h1.y, h1.z, h1.w}, SH[2] = {h2.x, h2.y};
+        const uint32_t ML[4] = {h2.z, h2.w, h3.x, h3.y}, MH[2] = {h3.z, h3.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t c = cw[k];
+            const long a = (long)(c & 0x0f0f0f0fu) | ((long)((c >> 4) & 0x0f0f0f0fu) << 32);
+            /* 6-bit scale / min of block k for the tile's rows 0..3, one byte each */
+            const int sl = 4 * (k >> 2), sh = 2 * (k >> 1);
+            const uint32_t s4 = ((SL[k & 3] >> sl) & 0x0f0f0f0fu) | (((SH[k & 1] >> sh) & 0x03030303u) << 4);
+            const uint32_t m4 = ((ML[k & 3] >> sl) & 0x0f0f0f0fu) | (((MH[k & 1] >> sh) & 0x03030303u) << 4);
+            float sc[4], of[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sc[j] = Dj[j] * (float)((s4 >> (8 * j)) & 0xffu); /* exact: 6-bit x 11-bit */
+                of[j] = Mj[j] * (float)((m4 >> (8 * j)) & 0xffu);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const int e = k * NV16 + 16 * t + c16;
+                const long b = *(const long *)(xs + (size_t)e * 32 + 8 * g);
+                const v4i dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+                const float2 df = xdf[e];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc[t][j] = __builtin_fmaf((float)dot[j], sc[j] * df.x, acc[t][j]);
+                    acc[t][j] = __builtin_fmaf(-of[j], df.y, acc[t][j]);
+                }
+            }
+        }
+    };
+
+    if constexpr (DIST == 2) {
+        Buf A, B;
+        fetch(A, 0);
+        if (nsb > 1) fetch(B, 1);
+        for (int sb = 0; sb < nsb; sb += 2) {
+            step(A, sb);
+            if (sb + 1 < nsb) step(B, sb + 1);
+        }
+    } else {
+        Buf A;
+        fetch(A, 0);
+        for (int sb = 0; sb < nsb; sb++) step(A, sb);
+    }
+    if (!live) return;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int v = vt0 + 16 * t + c16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = row0 + 4 * g + j;
+            if (v < n && row < rows) Y[(size_t)v * ystride + row] = acc[t][j];
+        }
+    }
+}
+
 /* A8 quantization, one 32-lane half-wave per (block b, vector v) unit; unit index = b * n + v,
  * which is the block-major output index (engine/src/kern.h:19-27). Cross-lane max of |x| and
  * the int sum are exact in any order; 127 / amax and amax / 127 are IEEE divides; the code is
@@ -380,10 +549,40 @@ int launch_ksplit(nmx_ctx *ctx, const SegTable &tab, int total_rows_groups, int 
     return 0;
 }
 
+/* More than 8 vectors (prefill chunks): the MFMA kernel. Its segment table counts 16-row
+ * groups. A wave takes all vector tiles when there are enough row groups to fill the chip,
+ * else one tile (four times the waves, the scale decode repeated per tile). */
+int launch_mm(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *q,
+              const float *d, const float *fs) {
+    SegTable t16 = tab;
+    int groups = 0;
+    for (int s = 0; s < tab.count; s++) {
+        t16.s[s].wave0 = groups;
+        groups += (tab.s[s].rows + 15) / 16;
+    }
+    t16.total_waves = groups;
+    const int vtiles = (n + 15) / 16;
+    if (groups < 512) { /* few rows: one vector tile per single-wave workgroup */
+        const dim3 grid((unsigned)groups, (unsigned)vtiles);
+        q4k_mm_k<1, 1, 2><<<grid, 64, 0, ctx->stream>>>(t16, cols, n, q, d, fs);
+    } else {
+        const dim3 grid((unsigned)((groups + 3) / 4));
+        switch (vtiles) {
+        case 4: q4k_mm_k<4, 4, 1><<<grid, 256, 0, ctx->stream>>>(t16, cols, n, q, d, fs); break;
+        case 3: q4k_mm_k<3, 4, 1><<<grid, 256, 0, ctx->stream>>>(t16, cols, n, q, d, fs); break;
+        case 2: q4k_mm_k<2, 4, 1><<<grid, 256, 0, ctx->stream>>>(t16, cols, n, q, d, fs); break;
+        default: q4k_mm_k<1, 4, 1><<<grid, 256, 0, ctx->stream>>>(t16, cols, n, q, d, fs); break;
+        }
+    }
+    NMX_LAUNCHED(ctx, "q4k_mm");
+    return 0;
+}
+
 int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *q,
                   const float *d, const float *fs, int32_t *dots, unsigned long long *am = nullptr) {
     int total_rows = 0;
     for (int s = 0; s < tab.count; s++) total_rows += tab.s[s].rows;
+    if (!am && !dots && n > MAX_NV) return launch_mm(ctx, tab, cols, n, q, d, fs);
     if (!am && !dots && total_rows < KSPLIT_MAX_ROWS) {
         nmx_mt_seg segs[NMX_MAX_SEGS];
         for (int s = 0; s < tab.count; s++)

@@ -127,10 +127,13 @@ def test_q4k_batch_equals_single(dev):
         assert_bits_equal(one[0], full[v], f"vector {v}")
 
 
-def test_q4k_multi_segment(dev):
-    """The fused launch of several matrices gives each matrix's own result."""
+@pytest.mark.parametrize("n", [5, 64])
+def test_q4k_multi_segment(dev, n):
+    """The fused launch of several matrices gives each matrix's own result (n = 64: the prefill
+    kernel, whose 16-row groups straddle no segment)."""
+    print(f"[case] multi-segment n={n}", flush=True)
     rng = np.random.default_rng(4)
-    cols, n = 1024, 5
+    cols = 1024
     shapes = [6144, 2048, 16, 16]
     Ws = [gaussian_q4k(rng, r, cols) for r in shapes]
     X = rng.standard_normal((n, cols)).astype(np.float32)
@@ -145,6 +148,19 @@ def test_q4k_multi_segment(dev):
         ref = oracle.q4k_matmul(W, r, cols, q, d, fs, n)
         assert_bits_equal(dY.numpy()[:, :r], ref, f"segment rows={r}")
         assert not dY.numpy()[:, r:].any(), "padding columns written"
+
+
+@pytest.mark.parametrize("n", [9, 16, 17, 40, 64])
+def test_q4k_prefill_chunk(dev, n):
+    """More than 8 vectors (prefill chunks, the MFMA kernel): ragged vector tiles, a matrix whose
+    rows are not a multiple of 16, one wave per vector tile (1024 rows) and every tile in one
+    wave (8224 rows)."""
+    rng = np.random.default_rng(5000 + n)
+    for rows, cols in [(20, 256), (1024, 3584), (8224, 1024)]:
+        print(f"[case] prefill chunk rows={rows} cols={cols} n={n}", flush=True)
+        W = gaussian_q4k(rng, rows, cols)
+        X = rng.standard_normal((n, cols)).astype(np.float32)
+        check_case(dev, W, rows, cols, X, dots=False)
 
 
 def test_q4k_invalid_calls_rejected(dev):
