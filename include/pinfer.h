@@ -76,7 +76,8 @@ typedef struct {
     int k;           /* drafts per verification pass, 0..PINFER_SPEC_MAX_K; 0 = plain */
     int draft_vocab; /* drafts are the argmax over ids [0, draft_vocab); <= 0: full vocabulary */
     int adaptive;    /* accepted for the ABI; this engine always uses the fixed k */
-    int ngram;       /* accepted for the ABI; prompt-lookup drafts are not used */
+    int ngram;       /* prompt-lookup drafts of up to ngram tokens (0..PINFER_SPEC_MAX_K), tried
+                      * before the MTP drafts each round (engine/src/spec.c:133-151) */
 } pinfer_spec_params;
 
 typedef struct {

@@ -124,6 +124,7 @@ static int alloc_state(pinfer_ctx *c) {
     s->a_f = a8_alloc(c, c->ffn, B, &ok);
     s->a_1 = a8_alloc(c, H, 1, &ok);
     c->hbuf = dalloc(c, (size_t)B * H * 4, &ok);
+    c->pbuf = dalloc(c, (size_t)B * H * 4, &ok);
     c->mbuf = dalloc(c, (size_t)3 * H * 4, &ok);
     c->ctl = dalloc(c, 16 * 4, &ok);
     c->vt = dalloc(c, (E_MAX_K + 2) * 4, &ok);
@@ -132,7 +133,7 @@ static int alloc_state(pinfer_ctx *c) {
     c->hout2 = dalloc(c, 4 * 4, &ok);
     c->hwork = dalloc(c, nmx_head_work_bytes(c->vocab, E_MAX_K + 1), &ok);
     c->logits = dalloc(c, (size_t)c->vocab * 4, &ok);
-    if (!ok) return PINFER_E_NOMEM;
+    if (!ok || e_ngram_init(&c->ng, c->max_ctx + 1)) return PINFER_E_NOMEM;
     return rope_tables(c, &ok);
 }
 
@@ -187,6 +188,7 @@ void pinfer_free(pinfer_ctx *c) {
         for (int i = 0; i < c->n_allocs; i++) nmx_free(c->dev, c->allocs[i]);
         nmx_destroy(c->dev);
     }
+    e_ngram_free(&c->ng);
     free(c->layers);
     free(c);
 }
@@ -282,14 +284,14 @@ int pinfer_generate_greedy_ex(pinfer_ctx *c, const int32_t *prompt, int n_prompt
                               const pinfer_gen_opts *opts, pinfer_spec_stats *stats,
                               int *status) {
     if (c) pinfer_reset(c);
-    return e_generate(c, prompt, n_prompt, out, n_max, sp, opts, stats, status);
+    return e_generate(c, prompt, n_prompt, out, n_max, sp, opts, stats, status, 0);
 }
 
 int pinfer_generate_greedy_cont(pinfer_ctx *c, const int32_t *prompt, int n_prompt,
                                 int32_t *out, int n_max, const pinfer_spec_params *sp,
                                 const pinfer_gen_opts *opts, pinfer_spec_stats *stats,
                                 int *status) {
-    return e_generate(c, prompt, n_prompt, out, n_max, sp, opts, stats, status);
+    return e_generate(c, prompt, n_prompt, out, n_max, sp, opts, stats, status, 1);
 }
 
 int pinfer_generate_greedy(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
@@ -309,6 +311,6 @@ int pinfer_bench_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, in
     int status;
     if (c) pinfer_reset(c);
     const int n = e_generate_timed(c, prompt, n_prompt, out, n_gen, sp, NULL, stats, &status, 1,
-                                   prefill_s, decode_s);
+                                   0, prefill_s, decode_s);
     return status != PINFER_OK ? status : n;
 }

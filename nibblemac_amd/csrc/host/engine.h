@@ -47,6 +47,35 @@ typedef struct {
     float *row1;       /* [hidden] */
 } e_scratch;
 
+/* Prompt-lookup drafts (engine/src/ngram.h:13-47, spec.h:40-47): n-gram lengths looked up,
+ * the backward extension of a match, and the draft rule (a match of at least E_NG_TRUST tokens
+ * drafts in full; E_NG_ASK.. tokens only when its first token equals the MTP head's draft, then
+ * at most E_NG_SHORT tokens; without the MTP head, shorter matches draft E_NG_SHORT tokens). */
+#define E_NG_MIN 2
+#define E_NG_MAX 4
+#define E_NG_EXT 32
+#define E_NG_TRUST 16
+#define E_NG_ASK 4
+#define E_NG_SHORT 3
+
+typedef struct {
+    int32_t *tok;  /* [cap] token history, oldest first */
+    int32_t *tab;  /* [E_NG_MAX - E_NG_MIN + 1][1 << bits] end position + 1, 0 = empty */
+    int cap, n;    /* capacity, tokens in the history */
+    int indexed;   /* n-grams ending before this position are in tab */
+    int bits;
+} e_ngram;
+
+int e_ngram_init(e_ngram *g, int cap);
+void e_ngram_free(e_ngram *g);
+void e_ngram_reset(e_ngram *g);
+void e_ngram_push(e_ngram *g, const int32_t *t, int m);
+void e_ngram_pop(e_ngram *g);
+/* Up to max tokens that followed the most recent earlier occurrence of the history's longest
+ * matching tail n-gram; returns the count (0: no match) and, if match != NULL, how many
+ * tokens the two occurrences share backwards. */
+int e_ngram_draft(e_ngram *g, int32_t *out, int max, int *match);
+
 struct pinfer_ctx {
     nmx_ctx *dev;
     /* dimensions (engine/src/pinfer.c:45-63) */
@@ -81,6 +110,8 @@ struct pinfer_ctx {
 
     e_scratch s;
     float *hbuf;              /* [E_MAX_BATCH][H] final-normed rows kept for the MTP pass */
+    float *pbuf;              /* [E_MAX_BATCH][H] committed rows waiting for the MTP pass
+                               * (plain steps, n-gram rounds) */
     float *mbuf;              /* [3][H]: MTP hidden of the current draft + chain ping-pong */
     int32_t *ctl;             /* [16] control block (see nmx.h) */
     int32_t *vt;              /* [E_MAX_K + 2] verify tokens */
@@ -94,6 +125,9 @@ struct pinfer_ctx {
     int n_past, mtp_rows, keep;
     /* captured rounds: verify graph and commit graph per draft count */
     nmx_graph *g_verify[E_MAX_K + 1], *g_commit[E_MAX_K + 1];
+    /* n-gram rounds: verify without the MTP chain, commit without the MTP pass */
+    nmx_graph *g_verify_ng[E_MAX_K + 1], *g_commit_ng;
+    e_ngram ng;               /* token history of the prompt-lookup drafts */
     int graph_nv;             /* draft vocabulary the graphs were captured with */
     int use_graphs;
     void *allocs[E_MAX_ALLOCS]; /* every device allocation besides the weight blob */
@@ -112,13 +146,15 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
 int e_set_pos(pinfer_ctx *c, int pos);
 
 /* spec.c */
+/* append: a continuation of the context (pinfer_generate_greedy_cont), which keeps the
+ * n-gram history when the prompt leads with the last emitted token */
 int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out, int n_max,
                const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
-               pinfer_spec_stats *stats, int *status);
+               pinfer_spec_stats *stats, int *status, int append);
 int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
                      int n_max, const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
-                     pinfer_spec_stats *stats, int *status, int no_eos, double *t_prefill,
-                     double *t_decode);
+                     pinfer_spec_stats *stats, int *status, int no_eos, int append,
+                     double *t_prefill, double *t_decode);
 void e_drop_graphs(pinfer_ctx *c);
 
 /* model.c */

@@ -9,7 +9,11 @@
  *       the committed rows (next d1 and its hidden), n_past += e.
  *
  * Both graphs are captured once per draft count and replayed at any position (the kernels read
- * n_past, e and keep from the device control block). Tokens emitted equal plain greedy
+ * n_past, e and keep from the device control block). With pinfer_spec_params.ngram a round may
+ * instead draft by prompt lookup (ngram.c, engine/src/spec.c:133-151): its verify graph has no
+ * MTP chain (the host uploads the drafts) and its commit graph no MTP pass (the committed rows
+ * wait, with those of plain steps, for one batched MTP pass before the next MTP round,
+ * engine/src/spec.c:110-131). Tokens emitted equal plain greedy
  * decoding whatever the drafts are. */
 #define _POSIX_C_SOURCE 200809L
 #include <stdio.h>
@@ -36,8 +40,11 @@ void e_drop_graphs(pinfer_ctx *c) {
     for (int i = 0; i <= E_MAX_K; i++) {
         nmx_graph_destroy(c->g_verify[i]);
         nmx_graph_destroy(c->g_commit[i]);
-        c->g_verify[i] = c->g_commit[i] = NULL;
+        nmx_graph_destroy(c->g_verify_ng[i]);
+        c->g_verify[i] = c->g_commit[i] = c->g_verify_ng[i] = NULL;
     }
+    nmx_graph_destroy(c->g_commit_ng);
+    c->g_commit_ng = NULL;
 }
 
 static int draft_vocab(const pinfer_ctx *c, const pinfer_spec_params *sp) {
@@ -75,15 +82,49 @@ static int seq_commit(pinfer_ctx *c, int ke, int nv) {
     return PINFER_OK;
 }
 
-static int graph_for(pinfer_ctx *c, int ke, int nv, int commit, nmx_graph **out) {
-    nmx_graph **slot = commit ? &c->g_commit[ke] : &c->g_verify[ke];
+/* The n-gram round's verify: [cur, drafts] (the drafts uploaded into vt[1..ke] by the host)
+ * through the logged main pass, the head with acceptance. */
+static int seq_verify_ng(pinfer_ctx *c, int ke) {
+    TRY(e_forward(c, c->vt, ke + 1, 1));
+    e_scratch *sc = &c->s;
+    CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
+                       NULL, c->vt + 1, c->hwork, c->hout));
+    CK(nmx_accept_commit(c->dev, c->hout, c->vt, c->ctl));
+    return PINFER_OK;
+}
+
+/* The n-gram round's commit: cur <- vt[e], the rollback commit, n_past += e. The committed
+ * rows stay in s.xn for the host to queue for the MTP pass. */
+static int seq_commit_ng(pinfer_ctx *c) {
+    CK(nmx_copy_token(c->dev, c->vt, c->ctl));
+    nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
+                         c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl};
+    if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
+    CK(nmx_ctl_advance(c->dev, c->ctl));
+    return PINFER_OK;
+}
+
+enum { SEQ_VERIFY, SEQ_COMMIT, SEQ_VERIFY_NG, SEQ_COMMIT_NG };
+
+static int seq_run(pinfer_ctx *c, int ke, int nv, int kind) {
+    switch (kind) {
+    case SEQ_VERIFY: return seq_verify(c, ke, nv);
+    case SEQ_COMMIT: return seq_commit(c, ke, nv);
+    case SEQ_VERIFY_NG: return seq_verify_ng(c, ke);
+    default: return seq_commit_ng(c);
+    }
+}
+
+static int graph_for(pinfer_ctx *c, int ke, int nv, int kind, nmx_graph **out) {
+    nmx_graph **slot = kind == SEQ_VERIFY ? &c->g_verify[ke] : kind == SEQ_COMMIT ? &c->g_commit[ke]
+                     : kind == SEQ_VERIFY_NG ? &c->g_verify_ng[ke] : &c->g_commit_ng;
     if (c->graph_nv != nv) {
         e_drop_graphs(c);
         c->graph_nv = nv;
     }
     if (!*slot) {
         CK(nmx_graph_begin(c->dev));
-        int rc = commit ? seq_commit(c, ke, nv) : seq_verify(c, ke, nv);
+        int rc = seq_run(c, ke, nv, kind);
         nmx_graph *g = nmx_graph_end(c->dev);
         if (rc != PINFER_OK) {
             nmx_graph_destroy(g);
@@ -99,10 +140,10 @@ static int graph_for(pinfer_ctx *c, int ke, int nv, int commit, nmx_graph **out)
     return PINFER_OK;
 }
 
-static int run_seq(pinfer_ctx *c, int ke, int nv, int commit) {
-    if (!c->use_graphs) return commit ? seq_commit(c, ke, nv) : seq_verify(c, ke, nv);
+static int run_seq(pinfer_ctx *c, int ke, int nv, int kind) {
+    if (!c->use_graphs) return seq_run(c, ke, nv, kind);
     nmx_graph *g;
-    TRY(graph_for(c, ke, nv, commit, &g));
+    TRY(graph_for(c, ke, nv, kind, &g));
     CK(nmx_graph_launch(c->dev, g));
     return PINFER_OK;
 }
@@ -177,37 +218,73 @@ static int lin_flush(pinfer_ctx *c) {
     return PINFER_OK;
 }
 
+/* Committed rows waiting for the MTP pass (plain steps, n-gram rounds), in c->pbuf:
+ * rows [0, n) hold the final-normed hiddens of positions pos.., tok the tokens after them
+ * (engine/src/spec.c:110-131). */
+typedef struct {
+    int n, pos;
+    int32_t tok[E_MAX_BATCH];
+} e_pending;
+
+/* The MTP pass over the pending rows (leaves d1 in vt[1], its hidden in m_cur). */
+static int flush_pending(pinfer_ctx *c, e_pending *pd, int nv) {
+    if (pd->n == 0) return PINFER_OK;
+    CK(nmx_upload(c->dev, c->tok, pd->tok, (size_t)pd->n * sizeof(int32_t)));
+    TRY(e_set_pos(c, pd->pos));
+    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c)));
+    c->mtp_rows = pd->pos + pd->n;
+    pd->n = 0;
+    TRY(e_set_pos(c, c->n_past));
+    return PINFER_OK;
+}
+
+/* Queue the first m rows of s.xn (positions pos..) with the tokens that follow them. */
+static int defer_rows(pinfer_ctx *c, e_pending *pd, const int32_t *tok, int m, int pos) {
+    if (pd->n == 0) pd->pos = pos;
+    CK(nmx_copy_d2d(c->dev, c->pbuf + (size_t)pd->n * c->H, c->s.xn,
+                    (size_t)m * c->H * sizeof(float)));
+    memcpy(pd->tok + pd->n, tok, (size_t)m * sizeof(int32_t));
+    pd->n += m;
+    return PINFER_OK;
+}
+
 /* One plain step (engine/src/spec.c:238-262): cur through the model at n_past, argmax; with
- * the MTP head the final-normed row is kept for a later MTP pass. */
-static int plain_step(pinfer_ctx *c, int use_mtp, int *pend_n, int *pend_pos, int32_t *pend_tok,
-                      int32_t *next) {
+ * the MTP head the final-normed row is queued for a later MTP pass. */
+static int plain_step(pinfer_ctx *c, int use_mtp, e_pending *pd, int nv, int32_t *next) {
     const int P = c->n_past;
+    if (use_mtp && pd->n == E_MAX_BATCH) TRY(flush_pending(c, pd, nv));
     TRY(e_set_pos(c, P));
     TRY(e_forward(c, c->vt, 1, 0));
     c->keep = 0;
     TRY(e_head_last(c, 1, c->vt, 0));
-    if (use_mtp) {
-        if (*pend_n == 0) *pend_pos = P;
-        CK(nmx_copy_d2d(c->dev, c->hbuf + (size_t)(E_MAX_BATCH - E_MAX_K - 2 + *pend_n) * c->H,
-                        c->s.xn, (size_t)c->H * sizeof(float)));
-    }
     CK(nmx_download(c->dev, next, c->vt, sizeof(int32_t)));
-    if (use_mtp) pend_tok[(*pend_n)++] = *next;
+    if (use_mtp) TRY(defer_rows(c, pd, next, 1, P));
+    e_ngram_push(&c->ng, next, 1);
     c->n_past = P + 1;
     TRY(e_set_pos(c, c->n_past));
     return PINFER_OK;
 }
 
-static int flush_pending(pinfer_ctx *c, int *pend_n, int pend_pos, const int32_t *pend_tok, int nv) {
-    if (*pend_n == 0) return PINFER_OK;
-    CK(nmx_upload(c->dev, c->tok, pend_tok, (size_t)*pend_n * sizeof(int32_t)));
-    TRY(e_set_pos(c, pend_pos));
-    TRY(e_mtp_forward(c, c->hbuf + (size_t)(E_MAX_BATCH - E_MAX_K - 2) * c->H, c->tok, *pend_n, 0,
-                      0, nv, c->vt + 1, m_cur(c)));
-    c->mtp_rows = pend_pos + *pend_n;
-    *pend_n = 0;
-    TRY(e_set_pos(c, c->n_past));
-    return PINFER_OK;
+/* The n-gram draft of the coming round (engine/src/spec.c:133-151): its length, or 0 for MTP
+ * drafts / a plain step. A match of E_NG_ASK..E_NG_TRUST-1 tokens must start with the MTP
+ * head's d1, which may need the pending rows' MTP pass first. */
+static int ngram_pick(pinfer_ctx *c, const pinfer_spec_params *sp, int left, int32_t *d,
+                      e_pending *pd, int nv, int *rc) {
+    int match = 0;
+    const int max = sp->ngram < left ? sp->ngram : left;
+    const int n = max > 0 ? e_ngram_draft(&c->ng, d, max, &match) : 0;
+    if (n == 0) return 0;
+    if (match >= E_NG_TRUST) return n;
+    if (sp->k == 0) return n < E_NG_SHORT ? n : E_NG_SHORT; /* no MTP head to ask */
+    if (match < E_NG_ASK) return 0;
+    if (pd->n > 0 && (*rc = flush_pending(c, pd, nv)) != PINFER_OK) return 0;
+    int32_t d1;
+    if (nmx_download(c->dev, &d1, c->vt + 1, sizeof d1)) {
+        *rc = PINFER_E_ARG;
+        return 0;
+    }
+    if (d[0] != d1) return 0;
+    return n < E_NG_SHORT ? n : E_NG_SHORT;
 }
 
 static double now_sec(void) {
@@ -218,8 +295,8 @@ static double now_sec(void) {
 
 int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out,
                      int n_max, const pinfer_spec_params *sp_in, const pinfer_gen_opts *opts,
-                     pinfer_spec_stats *st, int *status, int no_eos, double *t_prefill,
-                     double *t_decode) {
+                     pinfer_spec_stats *st, int *status, int no_eos, int append,
+                     double *t_prefill, double *t_decode) {
     pinfer_spec_params plain = {0, 0, 0, 0};
     const pinfer_spec_params *sp = sp_in ? sp_in : &plain;
     int dummy;
@@ -234,18 +311,25 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
         if (prompt[i] < 0 || prompt[i] >= c->vocab) return *status = PINFER_E_ARG;
     if (n_prompt > c->max_ctx - c->n_past) return *status = PINFER_E_CTX_FULL;
     const int use_mtp = sp->k > 0, nv = draft_vocab(c, sp);
+    const int drafting = sp->k > 0 || sp->ngram > 0;
     e_stop stop = {no_eos ? -1 : c->eos, opts ? opts->stop_ids : NULL, opts ? opts->n_stop : 0,
                    opts ? opts->on_token : NULL, opts ? opts->user : NULL};
+    /* the n-gram history is the fed tokens plus the last emitted one, with which a continuation
+     * prompt leads; any other context starts a new history (engine/src/spec.c:165-170) */
+    if (append && c->ng.n == c->n_past + 1) e_ngram_pop(&c->ng);
+    else e_ngram_reset(&c->ng);
+    e_ngram_push(&c->ng, prompt, n_prompt);
     const double t0 = now_sec();
     int rc = prefill(c, prompt, n_prompt, use_mtp, nv);
     if (rc != PINFER_OK) return *status = rc;
     int32_t cur;
     if (nmx_download(c->dev, &cur, c->vt, sizeof cur)) return *status = PINFER_E_ARG;
+    e_ngram_push(&c->ng, &cur, 1);
     const double t1 = now_sec();
     if (t_prefill) *t_prefill = t1 - t0;
     int count = 0, done = emit(out, &count, n_max, cur, &stop);
-    int pend_n = 0, pend_pos = 0;
-    int32_t pend_tok[E_MAX_K + 2];
+    e_pending pd;
+    pd.n = pd.pos = 0;
     int32_t host[2 + E_MAX_BATCH], vt[E_MAX_K + 2];
     while (!done) {
         const int P = c->n_past;
@@ -255,14 +339,31 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             rc = PINFER_E_CTX_FULL;
             break;
         }
-        const int ke = sp->k < left ? sp->k : left;
+        /* prompt lookup first, else MTP drafts, else a plain step */
+        int ke = 0, use_ng = 0;
+        if (sp->ngram > 0 && left > 0) ke = ngram_pick(c, sp, left, vt + 1, &pd, nv, &rc);
+        if (rc != PINFER_OK) break;
+        use_ng = ke > 0;
+        if (!use_ng) ke = sp->k < left ? sp->k : left;
         if (ke == 0) {
-            if (st && use_mtp) st->rounds++;
-            if ((rc = plain_step(c, use_mtp, &pend_n, &pend_pos, pend_tok, &cur)) != PINFER_OK) break;
+            if (st && drafting) st->rounds++;
+            if ((rc = plain_step(c, use_mtp, &pd, nv, &cur)) != PINFER_OK) break;
             done = emit(out, &count, n_max, cur, &stop);
             continue;
         }
-        if ((rc = run_seq(c, ke, nv, 0)) != PINFER_OK) break;
+        if (use_ng) {
+            /* room for this round's rows among the pending ones */
+            if (use_mtp && pd.n + ke + 1 > E_MAX_BATCH && (rc = flush_pending(c, &pd, nv)) != PINFER_OK)
+                break;
+            if (nmx_upload(c->dev, c->vt + 1, vt + 1, (size_t)ke * sizeof(int32_t))) {
+                rc = PINFER_E_ARG;
+                break;
+            }
+            if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
+        } else {
+            if ((rc = flush_pending(c, &pd, nv)) != PINFER_OK) break; /* d1 current */
+            if ((rc = run_seq(c, ke, nv, SEQ_VERIFY)) != PINFER_OK) break;
+        }
         if (nmx_download(c->dev, host, c->hout, 2 * sizeof(int32_t)) ||
             nmx_download(c->dev, vt, c->vt, (size_t)(ke + 2) * sizeof(int32_t))) {
             rc = PINFER_E_ARG;
@@ -275,18 +376,28 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             rc = PINFER_E_ARG;
             break;
         }
-        if ((rc = run_seq(c, ke, nv, 1)) != PINFER_OK) break;
+        if ((rc = run_seq(c, ke, nv, use_ng ? SEQ_COMMIT_NG : SEQ_COMMIT)) != PINFER_OK) break;
+        if (use_ng) {
+            if (use_mtp && (rc = defer_rows(c, &pd, vt + 1, e, P)) != PINFER_OK) break;
+        } else {
+            c->mtp_rows = P + e;
+        }
         c->n_past = P + e;
         c->keep = e - 1;
-        c->mtp_rows = P + e;
         cur = vt[e];
+        e_ngram_push(&c->ng, vt + 1, e);
         if (st) {
             st->rounds++;
             st->drafted += ke;
             st->accepted += a;
+            if (use_ng) {
+                st->ngram_rounds++;
+                st->ngram_drafted += ke;
+                st->ngram_accepted += a;
+            }
         }
     }
-    if (rc == PINFER_OK && use_mtp) rc = flush_pending(c, &pend_n, pend_pos, pend_tok, nv);
+    if (rc == PINFER_OK && use_mtp) rc = flush_pending(c, &pd, nv);
     int frc = lin_flush(c);
     if (rc == PINFER_OK) rc = frc;
     if (nmx_sync(c->dev) && rc == PINFER_OK) rc = PINFER_E_ARG;
@@ -297,6 +408,7 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
 
 int e_generate(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t *out, int n_max,
                const pinfer_spec_params *sp, const pinfer_gen_opts *opts,
-               pinfer_spec_stats *st, int *status) {
-    return e_generate_timed(c, prompt, n_prompt, out, n_max, sp, opts, st, status, 0, NULL, NULL);
+               pinfer_spec_stats *st, int *status, int append) {
+    return e_generate_timed(c, prompt, n_prompt, out, n_max, sp, opts, st, status, 0, append,
+                            NULL, NULL);
 }

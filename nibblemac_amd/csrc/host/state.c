@@ -176,6 +176,7 @@ int pinfer_state_load(pinfer_ctx *c, const void *buf, size_t len) {
     c->mtp_rows = n_mtp;
     c->keep = 0;
     c->ck_valid = 0; /* the KV rows below the checkpoint were replaced */
+    e_ngram_reset(&c->ng); /* a loaded context is not described by the history (state.c:210) */
     if (nmx_ctl_set(c->dev, c->ctl, 0, n_past) || nmx_ctl_set(c->dev, c->ctl, 2, 0) ||
         nmx_sync(c->dev))
         return PINFER_E_ARG;

@@ -64,10 +64,14 @@ class Model:
         return out
 
     def generate(self, prompt, n_max: int, k: int = 0, draft_vocab: int = 32768,
-                 cont: bool = False, stop_ids=()) -> tuple[list[int], SpecStats]:
+                 cont: bool = False, stop_ids=(), adaptive: int = 0,
+                 ngram: int = 0) -> tuple[list[int], SpecStats]:
+        """Greedy generation (pinfer_generate_greedy_ex, or _cont with cont=True): k MTP drafts
+        per verify pass (0 = plain), prompt-lookup drafts of up to `ngram` tokens, the adaptive
+        policy flag; returns the tokens and the speculative statistics."""
         t = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(n_max, np.int32)
-        sp = SpecParams(k, draft_vocab, 0, 0)
+        sp = SpecParams(k, draft_vocab, adaptive, ngram)
         st = SpecStats()
         status = ctypes.c_int(0)
         stops = np.ascontiguousarray(stop_ids, np.int32)

@@ -106,6 +106,40 @@ def test_accepting_drafts(agree_model, k):
     gpu.close(), ref.close()
 
 
+def counters(s):
+    return (s.rounds, s.drafted, s.accepted, s.ngram_rounds, s.ngram_drafted, s.ngram_accepted)
+
+
+@needs_ref
+@pytest.mark.parametrize("which,k,ngram", [("agree", 0, 4), ("agree", 4, 7), ("agree", 2, 8),
+                                           ("small", 4, 7)])
+def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
+    """Prompt-lookup drafts (pinfer_spec_params.ngram, engine/src/spec.c:133-151): a prompt
+    that repeats a span, so the history holds matches of every class (trusted, checked against
+    the MTP draft, short; with k = 0 the no-MTP rule). Tokens and all six speculative counters
+    equal the reference engine's; the output equals plain greedy; the states agree."""
+    path, base = agree_model if which == "agree" else (models["small"], np.random.default_rng(
+        9).integers(0, pqfile.SMALL.vocab, 24))
+    prompt = np.concatenate([base, base[:20], base])
+    gpu, ref = pair(path)
+    print(f"[case] ngram {which} k={k} ngram={ngram}", flush=True)
+    tg, sg = gpu.generate(prompt, 64, k=k, ngram=ngram)
+    tr, sr = ref.generate(prompt, 64, k=k, ngram=ngram)
+    assert tg == tr
+    assert counters(sg) == counters(sr)
+    if which == "agree":  # its output repeats itself; the random model's rarely does
+        assert sg.ngram_rounds > 0 and sg.ngram_accepted > 0, "no accepted n-gram round"
+    assert gpu.state_save() == ref.state_save(), "state after an n-gram generation"
+    assert gpu.generate(prompt, 64, k=0)[0] == tg  # plain greedy: the same tokens and state
+    # a continuation leading with the last emitted token keeps the history (both engines)
+    tg2, sg2 = gpu.generate([tg[-1]] + list(base[:6]), 24, k=k, ngram=ngram, cont=True)
+    tr2, sr2 = ref.generate([tr[-1]] + list(base[:6]), 24, k=k, ngram=ngram, cont=True)
+    assert tg2 == tr2 and counters(sg2) == counters(sr2)
+    probe = [1, 2, 3]
+    assert np.array_equal(bits(gpu.eval(probe)), bits(ref.eval(probe)))
+    gpu.close(), ref.close()
+
+
 @needs_ref
 def test_stop_inside_commit(agree_model):
     """A stop id that is reached among accepted drafts ends the generation inside the round's
