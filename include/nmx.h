@@ -239,7 +239,13 @@ int nmx_silu_mul(nmx_ctx *ctx, const float *gate, const float *up, int stride, i
 /* Gated full attention (engine/src/forward_attn.c:231-266). prep: k rows normed + RoPE and
  * stored with the v rows at position *pos + pos_off + t; query heads normed + RoPE in place.
  * attn: causal GQA softmax attention over rows [0, position], o *= sigmoid(gate), + A8; two
- * launches (scores into the caller's workspace, then softmax + P.V). */
+ * launches (scores into the caller's workspace, then softmax + P.V).
+ * KV caches (engine/src/forward_kv.c:1-14, pinfer.h PINFER_KV_*): kv_dtype 0 = fp32 rows
+ * [nkv][max_ctx][hd]; 1 = IEEE binary16 rows (round to nearest even); 2 = int8 rows
+ * q = rint(x * 127 / amax) followed by [nkv][max_ctx] fp32 scales amax / 127. Rows are stored
+ * rounded and read widened (binary16 exactly, int8 as q * scale); nmx_kv_bytes gives the size
+ * of one cache. */
+size_t nmx_kv_bytes(int kv_dtype, int nkv, int max_ctx, int hd);
 typedef struct {
     int n, nh, nkv, hd, rot, max_ctx;
     float *q;                    /* [n][nh][2 hd] query | gate */
@@ -247,12 +253,13 @@ typedef struct {
     const float *q_norm, *k_norm;
     float eps, scale;
     const float *rope_cos, *rope_sin; /* [max_ctx][rot/2] */
-    float *kc, *vc;              /* [nkv][max_ctx][hd] */
+    void *kc, *vc;               /* caches of kv_dtype, nmx_kv_bytes each */
     const int32_t *pos;
     int pos_off;
     float *o;                    /* [n][nh hd] */
     nmx_a8 a8;
     float *scores;               /* attn workspace: [n][nh][max_ctx] floats */
+    int kv_dtype;                /* 0 fp32, 1 binary16, 2 int8 + row scales */
 } nmx_attn_args;
 int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p);
 int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p);

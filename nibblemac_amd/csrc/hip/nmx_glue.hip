@@ -422,7 +422,7 @@ struct Attn {
     const float *q_norm, *k_norm;
     float eps, scale;
     const float *rcos, *rsin;  /* [max_ctx][rot/2] */
-    float *kc, *vc;      /* [nkv][max_ctx][hd] */
+    void *kc, *vc;       /* KV caches of the launch's format (nmx_kv_bytes each) */
     const int32_t *pos;  /* device: position of token 0 is *pos + pos_off */
     int pos_off;
     float *o;            /* [n][nh hd] */
@@ -430,6 +430,89 @@ struct Attn {
     float *ad, *afs;
 };
 
+/* ---- KV cache formats (engine/src/forward_kv.c:28-188): row R = g max_ctx + p of a cache
+ * holds hd values as fp32, binary16, or int8 with an fp32 scale in a [nkv][max_ctx] array
+ * after the rows. */
+enum { KV_F32 = 0, KV_F16 = 1, KV_I8 = 2 };
+
+/* binary16 bits of x rounded to nearest even, subnormals kept (v_cvt_f16_f32); a NaN becomes
+ * the quiet NaN with x's sign and top 10 payload bits (forward_kv.c:28-48 f32_to_f16) */
+__device__ __forceinline__ uint32_t kv_half_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu))
+        return ((u >> 16) & 0x8000u) | 0x7e00u | ((u & 0x7fffffu) >> 13);
+    const _Float16 h = (_Float16)x;
+    unsigned short b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ float kv_half_value(uint32_t bits16) { /* exact widening */
+    const unsigned short b = (unsigned short)bits16;
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+/* the int8 code of x at inv = 127 / amax (or 0): round half even, clamped to +-127, NaN to 0
+ * (forward_kv.c:101-124) */
+__device__ __forceinline__ uint32_t kv_i8_code(float x, float inv) {
+    const float y = rintf(x * inv);
+    const int q = y > 127.0f ? 127 : y < -127.0f ? -127 : y == y ? (int)y : 0;
+    return (uint32_t)(uint8_t)(int8_t)q;
+}
+
+/* fp32 values of columns col .. col + 3 of cache row R (col % 4 == 0) */
+template <int KVT>
+__device__ __forceinline__ float4 kv_load4(const void *cache, size_t R, int hd, int col,
+                                           const float *scales) {
+    if constexpr (KVT == KV_F32) {
+        return *(const float4 *)((const float *)cache + R * hd + col);
+    } else if constexpr (KVT == KV_F16) {
+        const uint2 h = *(const uint2 *)((const unsigned short *)cache + R * hd + col);
+        return make_float4(kv_half_value(h.x), kv_half_value(h.x >> 16), kv_half_value(h.y),
+                           kv_half_value(h.y >> 16));
+    } else {
+        const uint32_t w = *(const uint32_t *)((const int8_t *)cache + R * hd + col);
+        const float sc = scales[R];
+        return make_float4((float)(int8_t)w * sc, (float)(int8_t)(w >> 8) * sc,
+                           (float)(int8_t)(w >> 16) * sc, (float)(int8_t)(w >> 24) * sc);
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ const float *kv_scales(const void *cache, const Attn &a) {
+    return KVT == KV_I8 ? (const float *)((const int8_t *)cache + (size_t)a.nkv * a.max_ctx * a.hd)
+                        : nullptr;
+}
+
+/* Store one row element per thread (thread i of the row's hd); the int8 format first reduces
+ * the row's max |x| over the workgroup (hd threads, exact in any order). */
+template <int KVT>
+__device__ __forceinline__ void kv_store(void *cache, const Attn &a, size_t R, int i, float x,
+                                         float *red) {
+    const int hd = a.hd;
+    if constexpr (KVT == KV_F32) {
+        ((float *)cache)[R * hd + i] = x;
+    } else if constexpr (KVT == KV_F16) {
+        ((unsigned short *)cache)[R * hd + i] = (unsigned short)kv_half_bits(x);
+    } else {
+        float m = fabsf(x);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        __syncthreads(); /* red free */
+        if ((i & 63) == 0) red[i >> 6] = m;
+        __syncthreads();
+        float amax = 0.0f;
+        for (int w = 0; w < (hd >> 6); w++) amax = fmaxf(amax, red[w]);
+        /* inv stays finite: a row of subnormals codes to zeros like a zero row */
+        const float inv = amax > 127.0f / 3.40282347e+38f ? 127.0f / amax : 0.0f;
+        ((int8_t *)cache)[R * hd + i] = (int8_t)kv_i8_code(x, inv);
+        if (i == 0) ((float *)((int8_t *)cache + (size_t)a.nkv * a.max_ctx * hd))[R] = amax / 127.0f;
+    }
+}
+
+template <int KVT>
 __global__ __launch_bounds__(512) void attn_prep_k(Attn a) {
     extern __shared__ float sq[];
     __shared__ float buf[1024];
@@ -456,9 +539,10 @@ __global__ __launch_bounds__(512) void attn_prep_k(Attn a) {
         const float x0 = buf[i - h2], x1 = buf[i];
         v = x1 * c + x0 * s;
     }
-    if (is_k) {
-        a.kc[((size_t)u * a.max_ctx + p) * hd + i] = v;
-        a.vc[((size_t)u * a.max_ctx + p) * hd + i] = a.v_in[(size_t)t * a.nkv * hd + u * hd + i];
+    if (is_k) { /* uniform per workgroup */
+        const size_t R = (size_t)u * a.max_ctx + p;
+        kv_store<KVT>(a.kc, a, R, i, v, red);
+        kv_store<KVT>(a.vc, a, R, i, a.v_in[(size_t)t * a.nkv * hd + u * hd + i], red);
     } else {
         a.q[((size_t)t * a.nh + (u - a.nkv)) * 2 * hd + i] = v;
     }
@@ -473,7 +557,7 @@ __global__ __launch_bounds__(512) void attn_prep_k(Attn a) {
  * hit different banks); lane = position (lane % CP) x part (lane / CP) of the 16 partial
  * sums, the parts combined in the tree order by two cross-lane exchanges; wave w takes the
  * group's query heads w, w + 4, ... */
-template <int CP>
+template <int CP, int KVT>
 __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ sc) {
     constexpr int LP = 64 / CP, CPL = 16 / LP; /* lanes per position, partial sums per lane */
     extern __shared__ float4 smem4[];
@@ -485,14 +569,15 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
     float *ks = (float *)smem4;   /* [CP][rs] */
     float *qs = ks + CP * rs;     /* [4][hd] */
     const int f4 = hd >> 2;
-    const float *K = a.kc + ((size_t)g * a.max_ctx + p0) * hd;
+    const size_t R0 = (size_t)g * a.max_ctx + p0;
+    const float *ksc = kv_scales<KVT>(a.kc, a);
     for (int f0 = 0; f0 < rows * f4; f0 += 4 * 256) {
         float4 b[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int f = f0 + u * 256 + threadIdx.x;
             b[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (f < rows * f4) b[u] = ((const float4 *)K)[f];
+            if (f < rows * f4) b[u] = kv_load4<KVT>(a.kc, R0 + f / f4, hd, 4 * (f % f4), ksc);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -608,6 +693,7 @@ __device__ __forceinline__ float pv_chain(float acc, const float *p, int stride,
     return acc;
 }
 
+template <int KVT>
 __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict__ sc) {
     extern __shared__ float4 smem4[];
     __shared__ float red[8];
@@ -620,7 +706,8 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     float *att = (float *)smem4;                    /* [max_ctx] */
     float *vt = att + ((a.max_ctx + 3) & ~3);       /* [PV_PT][PV_DS] */
     const float *srow = sc + ((size_t)t * a.nh + h) * a.max_ctx;
-    const float *V = a.vc + (size_t)g * a.max_ctx * hd + d0;
+    const size_t R0 = (size_t)g * a.max_ctx;
+    const float *vsc = kv_scales<KVT>(a.vc, a);
     /* the scores row, then the first tile's values (element f = u 256 + tid: float4 f % F4 of
      * row f / F4) */
     float bs[4];
@@ -635,7 +722,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     for (int u = 0; u < PV_PER; u++) {
         const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
         vb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < rows0) vb[u] = *(const float4 *)(V + (size_t)r * hd + 4 * c4);
+        if (r < rows0) vb[u] = kv_load4<KVT>(a.vc, R0 + r, hd, d0 + 4 * c4, vsc);
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -692,7 +779,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
             for (int u = 0; u < PV_PER2; u++) {
                 const int f = u * 192 + f0, r = f / F4, c4 = f - r * F4;
                 nb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (r < rows2) nb[u] = *(const float4 *)(V + (size_t)(next + r) * hd + 4 * c4);
+                if (r < rows2) nb[u] = kv_load4<KVT>(a.vc, R0 + next + r, hd, d0 + 4 * c4, vsc);
             }
         }
         if (tid < PV_DS) o = pv_chain(o, vt + tid, PV_DS, rows);
@@ -892,18 +979,57 @@ static int attn_args(nmx_ctx *ctx, const nmx_attn_args *p, Attn *a) {
         p->max_ctx < 1 || p->max_ctx > 8192 || !p->q || !p->k_in || !p->v_in || !p->q_norm ||
         !p->k_norm || !p->rope_cos || !p->rope_sin || !p->kc || !p->vc || !p->pos || !p->o)
         return nmx_fail(ctx, "nmx_attn: bad arguments");
+    if (p->kv_dtype < KV_F32 || p->kv_dtype > KV_I8)
+        return nmx_fail(ctx, "nmx_attn: kv_dtype %d", p->kv_dtype);
     *a = Attn{p->n, p->nh, p->nkv, p->hd, p->rot, p->max_ctx, p->q, p->k_in, p->v_in, p->q_norm,
               p->k_norm, p->eps, p->scale, p->rope_cos, p->rope_sin, p->kc, p->vc, p->pos,
               p->pos_off, p->o, p->a8.q, p->a8.d, p->a8.fs};
     return 0;
 }
 
+} /* extern "C" */
+
+namespace {
+
+template <int KVT>
+void launch_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
+    dim3 grid((unsigned)(p->nkv + p->nh), (unsigned)p->n);
+    attn_prep_k<KVT><<<grid, (unsigned)p->hd, (size_t)p->hd * 4, ctx->stream>>>(a);
+}
+
+template <int KVT>
+int launch_attn(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
+    const int cp = p->hd <= 256 ? 32 : 16;
+    dim3 sgrid((unsigned)((p->max_ctx + cp - 1) / cp), (unsigned)p->n, (unsigned)p->nkv);
+    const size_t slds = ((size_t)cp * (p->hd + 4) + 4 * (size_t)p->hd) * 4;
+    if (cp == 32) attn_score_k<32, KVT><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
+    else attn_score_k<16, KVT><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
+    NMX_LAUNCHED(ctx, "attn_score");
+    const unsigned pgrid = (unsigned)((p->hd / PV_DS) * p->nh * p->n);
+    const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + (size_t)PV_PT * PV_DS) * 4;
+    static bool pv_ready = false; /* idempotent */
+    if (!pv_ready) {
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_pv_k<KVT>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)((8192 + (size_t)PV_PT * PV_DS) * 4)));
+        pv_ready = true;
+    }
+    attn_pv_k<KVT><<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
+    NMX_LAUNCHED(ctx, "attn_pv");
+    return 0;
+}
+
+} // namespace
+
+extern "C" {
+
 int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p) {
     if (!ctx) return -1;
     Attn a;
     if (attn_args(ctx, p, &a)) return -1;
-    dim3 grid((unsigned)(p->nkv + p->nh), (unsigned)p->n);
-    attn_prep_k<<<grid, (unsigned)p->hd, (size_t)p->hd * 4, ctx->stream>>>(a);
+    if (p->kv_dtype == KV_F16) launch_attn_prep<KV_F16>(ctx, p, a);
+    else if (p->kv_dtype == KV_I8) launch_attn_prep<KV_I8>(ctx, p, a);
+    else launch_attn_prep<KV_F32>(ctx, p, a);
     NMX_LAUNCHED(ctx, "attn_prep");
     return 0;
 }
@@ -913,24 +1039,16 @@ int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p) {
     Attn a;
     if (attn_args(ctx, p, &a)) return -1;
     if (!p->scores) return nmx_fail(ctx, "nmx_attn: NULL scores workspace");
-    const int cp = p->hd <= 256 ? 32 : 16;
-    dim3 sgrid((unsigned)((p->max_ctx + cp - 1) / cp), (unsigned)p->n, (unsigned)p->nkv);
-    const size_t slds = ((size_t)cp * (p->hd + 4) + 4 * (size_t)p->hd) * 4;
-    if (cp == 32) attn_score_k<32><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
-    else attn_score_k<16><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
-    NMX_LAUNCHED(ctx, "attn_score");
-    const unsigned pgrid = (unsigned)((p->hd / PV_DS) * p->nh * p->n);
-    const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + (size_t)PV_PT * PV_DS) * 4;
-    static bool pv_ready = false; /* idempotent */
-    if (!pv_ready) {
-        NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_pv_k,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)((8192 + (size_t)PV_PT * PV_DS) * 4)));
-        pv_ready = true;
-    }
-    attn_pv_k<<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
-    NMX_LAUNCHED(ctx, "attn_pv");
-    return 0;
+    if (p->kv_dtype == KV_F16) return launch_attn<KV_F16>(ctx, p, a);
+    if (p->kv_dtype == KV_I8) return launch_attn<KV_I8>(ctx, p, a);
+    return launch_attn<KV_F32>(ctx, p, a);
+}
+
+size_t nmx_kv_bytes(int kv_dtype, int nkv, int max_ctx, int hd) {
+    if (kv_dtype < KV_F32 || kv_dtype > KV_I8 || nkv < 1 || max_ctx < 1 || hd < 1) return 0;
+    const size_t rows = (size_t)nkv * (size_t)max_ctx;
+    const size_t es = kv_dtype == KV_F32 ? 4 : kv_dtype == KV_F16 ? 2 : 1;
+    return rows * hd * es + (kv_dtype == KV_I8 ? rows * 4 : 0);
 }
 
 int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p) {

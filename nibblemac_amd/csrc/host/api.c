@@ -85,15 +85,16 @@ static int rope_tables(pinfer_ctx *c, int *ok) {
 static int alloc_state(pinfer_ctx *c) {
     int ok = 1;
     const int B = E_MAX_BATCH, H = c->H, S = c->conv_k - 1;
-    const size_t kv = (size_t)c->n_kv * c->max_ctx * c->hd;
     const size_t logw = (size_t)c->lk_dim + c->lv_dim + 1;
     c->cap = E_MAX_K + 1;
     c->conv_state = dalloc(c, (size_t)imax(c->n_lin, 1) * (S ? S : 1) * c->conv_dim * 4, &ok);
     c->rec = dalloc(c, (size_t)imax(c->n_lin, 1) * c->lv_heads * c->lk_dim * c->lv_dim * 4, &ok);
-    c->kc = dalloc(c, (size_t)imax(c->n_full, 1) * kv * 4, &ok);
-    c->vc = dalloc(c, (size_t)imax(c->n_full, 1) * kv * 4, &ok);
-    c->mkc = dalloc(c, kv * 4, &ok);
-    c->mvc = dalloc(c, kv * 4, &ok);
+    c->kv_bytes = nmx_kv_bytes(c->kv_dtype, c->n_kv, c->max_ctx, c->hd);
+    if (!c->kv_bytes) return PINFER_E_ARG;
+    c->kc = dalloc(c, (size_t)imax(c->n_full, 1) * c->kv_bytes, &ok);
+    c->vc = dalloc(c, (size_t)imax(c->n_full, 1) * c->kv_bytes, &ok);
+    c->mkc = dalloc(c, c->kv_bytes, &ok);
+    c->mvc = dalloc(c, c->kv_bytes, &ok);
     c->xin = dalloc(c, (size_t)imax(c->n_lin, 1) * c->cap * c->conv_dim * 4, &ok);
     c->log = dalloc(c, (size_t)imax(c->n_lin, 1) * c->cap * c->lv_heads * logw * 4, &ok);
     c->pend = dalloc(c, (size_t)imax(c->n_lin, 1) * c->cap * c->lv_heads * logw * 4, &ok);
@@ -144,11 +145,10 @@ pinfer_ctx *pinfer_load(const char *path, const pinfer_params *params, int *err)
     pinfer_ctx *c = NULL;
     if (!path) rc = PINFER_E_ARG;
     else if (!isfinite(p.gpu_split) || p.gpu_split < 0.0f || p.gpu_split > 1.0f) rc = PINFER_E_ARG;
-    else if (p.kv_dtype != PINFER_KV_F32) {
-        fprintf(stderr, "pinfer: kv_dtype %d not supported by the MI355X engine (fp32 only)\n",
-                p.kv_dtype);
+    else if (p.kv_dtype != PINFER_KV_F32 && p.kv_dtype != PINFER_KV_F16 &&
+             p.kv_dtype != PINFER_KV_I8)
         rc = PINFER_E_ARG;
-    } else if (p.max_ctx > 8192) {
+    else if (p.max_ctx > 8192) {
         fprintf(stderr, "pinfer: max_ctx %d above the attention kernel's 8192\n", p.max_ctx);
         rc = PINFER_E_ARG;
     } else if (!(c = calloc(1, sizeof *c))) rc = PINFER_E_NOMEM;
@@ -162,6 +162,7 @@ pinfer_ctx *pinfer_load(const char *path, const pinfer_params *params, int *err)
     }
     if (rc == PINFER_OK) {
         c->max_ctx = p.max_ctx;
+        c->kv_dtype = p.kv_dtype;
         rc = e_model_load(c, path);
     }
     if (rc == PINFER_OK) rc = alloc_state(c);

@@ -101,8 +101,10 @@ struct pinfer_ctx {
     /* state in HBM */
     float *conv_state;        /* [n_lin][conv_k-1][conv_dim] */
     float *rec;               /* [n_lin][lv_heads][lv_dim][lk_dim] */
-    float *kc, *vc;           /* [n_full][n_kv][max_ctx][hd] */
-    float *mkc, *mvc;         /* MTP cache [n_kv][max_ctx][hd] */
+    int kv_dtype;             /* PINFER_KV_*: storage of every KV cache (nmx.h nmx_kv_bytes) */
+    size_t kv_bytes;          /* bytes of one cache: [n_kv][max_ctx] rows (+ int8 scales) */
+    void *kc, *vc;            /* [n_full] caches of kv_bytes each */
+    void *mkc, *mvc;          /* MTP caches */
     float *xin;               /* [n_lin][cap][conv_dim] raw conv inputs of a logged pass */
     float *log, *pend;        /* [n_lin][cap][lv_heads][lk_dim + lv_dim + 1] */
     int cap;                  /* rows per log = E_MAX_K + 1 */
@@ -156,6 +158,10 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
                      pinfer_spec_stats *stats, int *status, int no_eos, int append,
                      double *t_prefill, double *t_decode);
 void e_drop_graphs(pinfer_ctx *c);
+
+/* state.c: KV rows of the context's format */
+size_t e_kv_row_bytes(const pinfer_ctx *c);
+int e_kv_zero_rows(pinfer_ctx *c, void *cache, int p0, int p1);
 
 /* model.c */
 int e_model_load(pinfer_ctx *c, const char *path);

@@ -30,7 +30,8 @@ int e_set_pos(pinfer_ctx *c, int pos) {
     return PINFER_OK;
 }
 
-static size_t kv_layer(const pinfer_ctx *c) { return (size_t)c->n_kv * c->max_ctx * c->hd; }
+/* the KV caches of full-attention layer f (c->kv_bytes each) */
+static void *kv_of(void *base, const pinfer_ctx *c, int f) { return (char *)base + (size_t)f * c->kv_bytes; }
 
 /* The residual stream: rows in one of two buffers; a fused norm reads the current one (plus
  * the pending residual add) and writes the sum to the other, which becomes current. */
@@ -57,7 +58,7 @@ static int norm_a8(pinfer_ctx *c, e_resid *r, const float *w, int n, nmx_a8 a) {
 /* Gated full attention (engine/src/forward_attn.c:231-266) on the normed rows (A8 in s->a_h):
  * q (query | gate per head), k, v in one launch; kc / vc: the block's caches; pos_off:
  * position of row 0 relative to ctl[0]. Output (o_proj) to s->out. */
-static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *vc, int pos_off) {
+static int attn_block(pinfer_ctx *c, const e_layer *L, int n, void *kc, void *vc, int pos_off) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H, hd = c->hd, qw = 2 * c->n_heads * hd, kvw = c->n_kv * hd;
@@ -67,7 +68,7 @@ static int attn_block(pinfer_ctx *c, const e_layer *L, int n, float *kc, float *
     CK(nmx_q4k_matmul_multi(D, 3, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
     nmx_attn_args a = {n, c->n_heads, c->n_kv, hd, c->rot, c->max_ctx, s->ta, s->tb, s->tc,
                        L->q_norm, L->k_norm, c->rms_eps, 1.0f / sqrtf((float)hd), c->rope_cos,
-                       c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w, s->sc};
+                       c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w, s->sc, c->kv_dtype};
     CK(nmx_attn_prep(D, &a));
     CK(nmx_attn(D, &a));
     CK(nmx_q4k_matmul(D, L->o.w, H, c->n_heads * hd, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->out,
@@ -131,8 +132,8 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
     for (int l = 0; l < c->n_layers; l++) {
         const e_layer *L = &c->layers[l];
         TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
-        int rc = L->is_full ? attn_block(c, L, n, c->kc + (size_t)L->full * kv_layer(c),
-                                         c->vc + (size_t)L->full * kv_layer(c), 0)
+        int rc = L->is_full ? attn_block(c, L, n, kv_of(c->kc, c, L->full),
+                                         kv_of(c->vc, c, L->full), 0)
                             : lin_block(c, L, n, logged);
         if (rc) return rc;
         if ((rc = mlp_block(c, L, n, &r))) return rc;

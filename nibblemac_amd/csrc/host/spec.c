@@ -168,13 +168,8 @@ static int emit(int32_t *out, int *count, int n_max, int32_t tok, const e_stop *
 }
 
 static int zero_mtp_rows(pinfer_ctx *c, int p0, int p1) {
-    if (p1 <= p0) return PINFER_OK;
-    for (int g = 0; g < c->n_kv; g++) {
-        const size_t off = ((size_t)g * c->max_ctx + p0) * c->hd, len = (size_t)(p1 - p0) * c->hd * 4;
-        CK(nmx_fill_zero(c->dev, c->mkc + off, len));
-        CK(nmx_fill_zero(c->dev, c->mvc + off, len));
-    }
-    return PINFER_OK;
+    TRY(e_kv_zero_rows(c, c->mkc, p0, p1));
+    return e_kv_zero_rows(c, c->mvc, p0, p1);
 }
 
 /* engine/src/spec.c:153-202: the prompt in chunks through the main model (final-normed rows

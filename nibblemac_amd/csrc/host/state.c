@@ -35,8 +35,32 @@ static size_t conv_bytes(const pinfer_ctx *c) {
 static size_t rec_bytes(const pinfer_ctx *c) {
     return (size_t)c->lv_heads * c->lk_dim * c->lv_dim * sizeof(float);
 }
+/* bytes of one cache row in the context's format, and of rows [0, n) of every group with
+ * their int8 scales (engine/src/state.c:40-44) */
+size_t e_kv_row_bytes(const pinfer_ctx *c) {
+    return (size_t)c->hd * (c->kv_dtype == PINFER_KV_F32 ? 4 : c->kv_dtype == PINFER_KV_F16 ? 2 : 1);
+}
 static size_t rows_bytes(const pinfer_ctx *c, int n) {
-    return (size_t)c->n_kv * (size_t)n * c->hd * sizeof(float);
+    return (size_t)c->n_kv * (size_t)n *
+           (e_kv_row_bytes(c) + (c->kv_dtype == PINFER_KV_I8 ? sizeof(float) : 0));
+}
+static float *kv_scales(const pinfer_ctx *c, void *cache) {
+    return (float *)(void *)((char *)cache + (size_t)c->n_kv * c->max_ctx * e_kv_row_bytes(c));
+}
+
+/* Zero rows [p0, p1) of every group of a cache (and their int8 scales): positions whose values
+ * were never computed must not reach an attention pass (forward_kv.c:128-139). */
+int e_kv_zero_rows(pinfer_ctx *c, void *cache, int p0, int p1) {
+    if (p1 <= p0) return PINFER_OK;
+    const size_t rb = e_kv_row_bytes(c);
+    for (int g = 0; g < c->n_kv; g++) {
+        const size_t r0 = (size_t)g * c->max_ctx + p0;
+        if (nmx_fill_zero(c->dev, (char *)cache + r0 * rb, (size_t)(p1 - p0) * rb) ||
+            (c->kv_dtype == PINFER_KV_I8 &&
+             nmx_fill_zero(c->dev, kv_scales(c, cache) + r0, (size_t)(p1 - p0) * sizeof(float))))
+            return PINFER_E_ARG;
+    }
+    return PINFER_OK;
 }
 static int mtp_rows(const pinfer_ctx *c) {
     return c->has_mtp && c->mtp_rows > 0 ? (c->mtp_rows < c->n_past ? c->mtp_rows : c->n_past) : 0;
@@ -56,14 +80,21 @@ size_t pinfer_state_size(const pinfer_ctx *c) {
     return c ? state_bytes(c, c->n_past, mtp_rows(c)) : 0;
 }
 
-/* rows [0, n) of every KV group of one cache [n_kv][max_ctx][hd] <-> the blob cursor */
-static int copy_rows(pinfer_ctx *c, float *cache, int n, char *cur, int to_blob, char **next) {
-    const size_t len = (size_t)n * c->hd * sizeof(float);
+/* rows [0, n) of every KV group of one cache <-> the blob cursor: per group the rows, then
+ * (int8) their scales (engine/src/state.c:64-83) */
+static int copy_rows(pinfer_ctx *c, void *cache, int n, char *cur, int to_blob, char **next) {
+    const size_t rb = e_kv_row_bytes(c), len = (size_t)n * rb, sl = (size_t)n * sizeof(float);
     for (int g = 0; g < c->n_kv; g++) {
-        float *rows = cache + (size_t)g * c->max_ctx * c->hd;
+        char *rows = (char *)cache + (size_t)g * c->max_ctx * rb;
         if (len && (to_blob ? nmx_download(c->dev, cur, rows, len) : nmx_upload(c->dev, rows, cur, len)))
             return PINFER_E_ARG;
         cur += len;
+        if (c->kv_dtype == PINFER_KV_I8) {
+            float *sc = kv_scales(c, cache) + (size_t)g * c->max_ctx;
+            if (sl && (to_blob ? nmx_download(c->dev, cur, sc, sl) : nmx_upload(c->dev, sc, cur, sl)))
+                return PINFER_E_ARG;
+            cur += sl;
+        }
     }
     *next = cur;
     return PINFER_OK;
@@ -98,7 +129,7 @@ int pinfer_state_save(const pinfer_ctx *cc, void *buf, size_t cap) {
     if (!c || !buf) return PINFER_E_ARG;
     const int n_mtp = mtp_rows(c);
     if (cap < state_bytes(c, c->n_past, n_mtp)) return PINFER_E_ARG;
-    state_hdr hdr = {STATE_MAGIC, STATE_VERSION, (uint32_t)c->n_past, PINFER_KV_F32,
+    state_hdr hdr = {STATE_MAGIC, STATE_VERSION, (uint32_t)c->n_past, (uint32_t)c->kv_dtype,
                      (uint32_t)n_mtp, (uint32_t)c->n_layers, (uint32_t)c->H, (uint32_t)c->n_kv,
                      (uint32_t)c->hd, (uint32_t)c->lk_heads, (uint32_t)c->lv_heads,
                      (uint32_t)c->lk_dim, (uint32_t)c->lv_dim, (uint32_t)c->conv_k,
@@ -114,9 +145,9 @@ int pinfer_state_save(const pinfer_ctx *cc, void *buf, size_t cap) {
     free(tmp);
     for (int l = 0; rc == PINFER_OK && l < c->n_layers; l++)
         if (c->layers[l].is_full) {
-            const size_t off = (size_t)c->layers[l].full * c->n_kv * c->max_ctx * c->hd;
-            rc = copy_rows(c, c->kc + off, c->n_past, cur, 1, &cur);
-            if (rc == PINFER_OK) rc = copy_rows(c, c->vc + off, c->n_past, cur, 1, &cur);
+            const size_t off = (size_t)c->layers[l].full * c->kv_bytes;
+            rc = copy_rows(c, (char *)c->kc + off, c->n_past, cur, 1, &cur);
+            if (rc == PINFER_OK) rc = copy_rows(c, (char *)c->vc + off, c->n_past, cur, 1, &cur);
         }
     if (rc == PINFER_OK && n_mtp > 0) {
         rc = copy_rows(c, c->mkc, n_mtp, cur, 1, &cur);
@@ -136,7 +167,7 @@ int pinfer_state_load(pinfer_ctx *c, const void *buf, size_t len) {
         hdr.lk_heads != (uint32_t)c->lk_heads || hdr.lv_heads != (uint32_t)c->lv_heads ||
         hdr.lk_dim != (uint32_t)c->lk_dim || hdr.lv_dim != (uint32_t)c->lv_dim ||
         hdr.conv_k != (uint32_t)c->conv_k || hdr.full_mask != full_mask(c) ||
-        hdr.kv_dtype != PINFER_KV_F32 || hdr.model_fp != c->model_fp)
+        hdr.kv_dtype != (uint32_t)c->kv_dtype || hdr.model_fp != c->model_fp)
         return PINFER_E_FORMAT; /* another model file, or another KV storage format */
     if (hdr.n_past > (uint32_t)c->max_ctx) return PINFER_E_CTX_FULL;
     if (hdr.mtp_rows > hdr.n_past || len < state_bytes(c, (int)hdr.n_past, (int)hdr.mtp_rows))
@@ -151,22 +182,17 @@ int pinfer_state_load(pinfer_ctx *c, const void *buf, size_t len) {
     free(tmp);
     for (int l = 0; rc == PINFER_OK && l < c->n_layers; l++)
         if (c->layers[l].is_full) {
-            const size_t off = (size_t)c->layers[l].full * c->n_kv * c->max_ctx * c->hd;
-            rc = copy_rows(c, c->kc + off, n_past, cur, 0, &cur);
-            if (rc == PINFER_OK) rc = copy_rows(c, c->vc + off, n_past, cur, 0, &cur);
+            const size_t off = (size_t)c->layers[l].full * c->kv_bytes;
+            rc = copy_rows(c, (char *)c->kc + off, n_past, cur, 0, &cur);
+            if (rc == PINFER_OK) rc = copy_rows(c, (char *)c->vc + off, n_past, cur, 0, &cur);
         }
     if (rc == PINFER_OK && n_mtp > 0) {
         rc = copy_rows(c, c->mkc, n_mtp, cur, 0, &cur);
         if (rc == PINFER_OK) rc = copy_rows(c, c->mvc, n_mtp, cur, 0, &cur);
     }
     if (rc == PINFER_OK && c->has_mtp && n_past > n_mtp) { /* rows without saved values */
-        const size_t row = (size_t)c->hd * sizeof(float);
-        for (int g = 0; rc == PINFER_OK && g < c->n_kv; g++) {
-            const size_t off = ((size_t)g * c->max_ctx + n_mtp) * c->hd;
-            if (nmx_fill_zero(c->dev, c->mkc + off, (size_t)(n_past - n_mtp) * row) ||
-                nmx_fill_zero(c->dev, c->mvc + off, (size_t)(n_past - n_mtp) * row))
-                rc = PINFER_E_ARG;
-        }
+        rc = e_kv_zero_rows(c, c->mkc, n_mtp, n_past);
+        if (rc == PINFER_OK) rc = e_kv_zero_rows(c, c->mvc, n_mtp, n_past);
     }
     if (rc != PINFER_OK) {
         pinfer_reset(c); /* a partial restore must not pass for a state */

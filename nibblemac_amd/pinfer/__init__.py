@@ -23,10 +23,11 @@ class Model:
     """A loaded .pq model on the MI355X."""
 
     def __init__(self, path: str, max_ctx: int = 4096, lib: Lib | None = None,
-                 lib_path: str | None = None, n_threads: int | None = None):
+                 lib_path: str | None = None, n_threads: int | None = None, kv_dtype: int = 0):
         self.lib = lib or load_library(lib_path)
         p = self.lib.pinfer_default_params()
         p.max_ctx = max_ctx
+        p.kv_dtype = kv_dtype  # PINFER_KV_F32 / F16 / I8
         if n_threads is not None:
             p.n_threads = n_threads
         err = ctypes.c_int(0)

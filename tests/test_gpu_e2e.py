@@ -35,13 +35,13 @@ def models(tmp_path_factory):
     return {"small": pqfile.write_model(d / "small.pq", pqfile.SMALL, seed=3, random_norms=True)}
 
 
-def pair(path, max_ctx=512):
+def pair(path, max_ctx=512, kv_dtype=0):
     from nibblemac_amd.pinfer import load_library
 
     ref_lib = load_library(str(REF))
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    return (Model(str(path), max_ctx=max_ctx),
-            Model(str(path), max_ctx=max_ctx, lib=ref_lib, n_threads=threads))
+    return (Model(str(path), max_ctx=max_ctx, kv_dtype=kv_dtype),
+            Model(str(path), max_ctx=max_ctx, lib=ref_lib, n_threads=threads, kv_dtype=kv_dtype))
 
 
 def bits(a):
@@ -136,6 +136,38 @@ def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
     tr2, sr2 = ref.generate([tr[-1]] + list(base[:6]), 24, k=k, ngram=ngram, cont=True)
     assert tg2 == tr2 and counters(sg2) == counters(sr2)
     probe = [1, 2, 3]
+    assert np.array_equal(bits(gpu.eval(probe)), bits(ref.eval(probe)))
+    gpu.close(), ref.close()
+
+
+@needs_ref
+@pytest.mark.parametrize("kv_dtype", [1, 2])
+def test_kv_dtypes_match_reference(models, agree_model, kv_dtype):
+    """KV caches stored as binary16 (1) or int8 with row scales (2) (pinfer_params.kv_dtype,
+    engine/src/forward_kv.c): prefill logits over two chunks, single-token steps, a speculative
+    generation with accepted drafts (MTP cache included) and the state blob (rows in the cache
+    format, int8 scales after each group's rows) equal the reference engine's bit for bit; the
+    blob loads into the other engine."""
+    gpu, ref = pair(models["small"], kv_dtype=kv_dtype)
+    rng = np.random.default_rng(20 + kv_dtype)
+    prompt = rng.integers(0, pqfile.SMALL.vocab, 70)
+    print(f"[case] kv_dtype={kv_dtype} eval", flush=True)
+    assert np.array_equal(bits(gpu.eval(prompt)), bits(ref.eval(prompt)))
+    for tok in prompt[:3]:
+        assert np.array_equal(bits(gpu.eval([tok])), bits(ref.eval([tok])))
+    assert gpu.state_save() == ref.state_save(), "state blob after eval"
+    gpu.close(), ref.close()
+    path, p2 = agree_model
+    gpu, ref = pair(path, kv_dtype=kv_dtype)
+    print(f"[case] kv_dtype={kv_dtype} generate", flush=True)
+    tg, sg = gpu.generate(p2, 48, k=4)
+    tr, sr = ref.generate(p2, 48, k=4)
+    assert tg == tr and (sg.rounds, sg.drafted, sg.accepted) == (sr.rounds, sr.drafted, sr.accepted)
+    assert sg.accepted > 0
+    blob = ref.state_save()
+    assert gpu.state_save() == blob, "state blob after generation"
+    gpu.state_load(blob)
+    probe = [7, 8]
     assert np.array_equal(bits(gpu.eval(probe)), bits(ref.eval(probe)))
     gpu.close(), ref.close()
 
