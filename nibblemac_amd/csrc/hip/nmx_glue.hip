@@ -810,6 +810,80 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     }
 }
 
+/* The same softmax and P.V for caches longer than the scores row that fits in LDS (max_ctx
+ * above PV_ATT_MAX): the max over the row from the scores workspace, then the exponentials
+ * segment by segment (SEG positions in LDS) with the four ordered partial sums and the tail
+ * carried across segments, then the value rows in tiles, each weight recomputed as
+ * e_p * (1 / sum) with e_p = exp(s_p - max) (the same operations as the in-LDS kernel, so the
+ * results are identical). */
+constexpr int PV_ATT_MAX = 8192; /* scores kept in LDS by attn_pv_k */
+constexpr int PV_SEG = 4096;     /* positions per exponential segment of attn_pv_long_k */
+
+template <int KVT>
+__global__ __launch_bounds__(256) void attn_pv_long_k(Attn a, const float *__restrict__ sc) {
+    extern __shared__ float4 smem4[];
+    __shared__ float red[8];
+    constexpr int F4 = PV_DS / 4;
+    const int hd = a.hd, rep = a.nh / a.nkv, S = (hd / PV_DS) * a.nkv;
+    const int tid = threadIdx.x, sl = blockIdx.x % S, k = blockIdx.x / S;
+    const int d0 = (sl % (hd / PV_DS)) * PV_DS, g = sl / (hd / PV_DS);
+    const int h = g * rep + k % rep, t = k / rep;
+    const int np = *a.pos + a.pos_off + t + 1;
+    float *seg = (float *)smem4;     /* [PV_SEG] */
+    float *vt = seg + PV_SEG;        /* [PV_PT2][PV_DS] */
+    const float *srow = sc + ((size_t)t * a.nh + h) * a.max_ctx;
+    const size_t R0 = (size_t)g * a.max_ctx;
+    const float *vsc = kv_scales<KVT>(a.vc, a);
+
+    float mx = -INFINITY;
+    for (int p = tid; p < np; p += 256) mx = fmaxf(mx, srow[p]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+
+    /* partial sum l over e[4m + l], m ascending (m < np / 4), and the tail, in order */
+    const int q4 = 4 * (np >> 2);
+    float chain = 0.0f; /* lane tid < 4: partial sum tid; lane 4: the tail */
+    for (int s0 = 0; s0 < np; s0 += PV_SEG) {
+        const int len = np - s0 < PV_SEG ? np - s0 : PV_SEG;
+        for (int p = tid; p < len; p += 256) seg[p] = nmx_expf_cephes(srow[s0 + p] - mx);
+        __syncthreads();
+        const int full = q4 - s0 < len ? (q4 - s0 > 0 ? q4 - s0 : 0) : len; /* in quads' range */
+        if (tid < 4) chain = pv_chain(chain, seg + tid, 4, full >> 2);
+        else if (tid == 4)
+            for (int i = full; i < len; i++) chain = chain + seg[i];
+        __syncthreads();
+    }
+    if (tid < 5) red[tid] = chain;
+    __syncthreads();
+    const float inv = 1.0f / (((red[0] + red[1]) + (red[2] + red[3])) + red[4]);
+
+    float o = 0.0f;
+    for (int base = 0; base < np; base += PV_PT2) {
+        const int rows = np - base < PV_PT2 ? np - base : PV_PT2;
+        for (int f = tid; f < rows * F4; f += 256) {
+            const int r = f / F4, c4 = f - r * F4;
+            const float4 v = kv_load4<KVT>(a.vc, R0 + base + r, hd, d0 + 4 * c4, vsc);
+            const float w = nmx_expf_cephes(srow[base + r] - mx) * inv;
+            *(float4 *)(vt + r * PV_DS + 4 * c4) = make_float4(w * v.x, w * v.y, w * v.z, w * v.w);
+        }
+        __syncthreads();
+        if (tid < PV_DS) o = pv_chain(o, vt + tid, PV_DS, rows);
+        __syncthreads();
+    }
+    if (tid < PV_DS) {
+        const int d = d0 + tid;
+        const float *qrow = a.q + ((size_t)t * a.nh + h) * 2 * hd;
+        o = o * nmx_sigmoid(qrow[hd + d]);
+        const int col = h * hd + d;
+        a.o[(size_t)t * a.nh * hd + col] = o;
+        if (a.aq) a8_block(o, col >> 5, t, a.n, a.aq, a.ad, a.afs);
+    }
+}
+
 /* ---- rollback commit over every linear layer (engine/src/forward_lin.c:185-204): with
  * E = e - 1 (e = ctl[1]), conv state <- last K-1 rows of [state after token 0, raw inputs
  * 1..E]; pending replay rows <- log rows 1..E; ctl[2] = E (keep). */
@@ -976,7 +1050,7 @@ int nmx_silu_mul(nmx_ctx *ctx, const float *gate, const float *up, int stride, i
 static int attn_args(nmx_ctx *ctx, const nmx_attn_args *p, Attn *a) {
     if (!p || p->n < 1 || p->n > 64 || p->nkv < 1 || p->nh < p->nkv || p->nh % p->nkv ||
         p->hd < 64 || p->hd > 512 || p->hd % 64 || p->rot % 2 || p->rot > p->hd ||
-        p->max_ctx < 1 || p->max_ctx > 8192 || !p->q || !p->k_in || !p->v_in || !p->q_norm ||
+        p->max_ctx < 1 || p->max_ctx > (1 << 20) || !p->q || !p->k_in || !p->v_in || !p->q_norm ||
         !p->k_norm || !p->rope_cos || !p->rope_sin || !p->kc || !p->vc || !p->pos || !p->o)
         return nmx_fail(ctx, "nmx_attn: bad arguments");
     if (p->kv_dtype < KV_F32 || p->kv_dtype > KV_I8)
@@ -1011,10 +1085,15 @@ int launch_attn(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
     if (!pv_ready) {
         NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_pv_k<KVT>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)((8192 + (size_t)PV_PT * PV_DS) * 4)));
+                                         (int)((PV_ATT_MAX + (size_t)PV_PT * PV_DS) * 4)));
         pv_ready = true;
     }
-    attn_pv_k<KVT><<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
+    if (p->max_ctx > PV_ATT_MAX) {
+        const size_t llds = ((size_t)PV_SEG + (size_t)PV_PT2 * PV_DS) * 4;
+        attn_pv_long_k<KVT><<<pgrid, 256, llds, ctx->stream>>>(a, p->scores);
+    } else {
+        attn_pv_k<KVT><<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
+    }
     NMX_LAUNCHED(ctx, "attn_pv");
     return 0;
 }

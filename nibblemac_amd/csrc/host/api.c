@@ -148,8 +148,8 @@ pinfer_ctx *pinfer_load(const char *path, const pinfer_params *params, int *err)
     else if (p.kv_dtype != PINFER_KV_F32 && p.kv_dtype != PINFER_KV_F16 &&
              p.kv_dtype != PINFER_KV_I8)
         rc = PINFER_E_ARG;
-    else if (p.max_ctx > 8192) {
-        fprintf(stderr, "pinfer: max_ctx %d above the attention kernel's 8192\n", p.max_ctx);
+    else if (p.max_ctx > (1 << 20)) {
+        fprintf(stderr, "pinfer: max_ctx %d above the attention kernels' 1048576\n", p.max_ctx);
         rc = PINFER_E_ARG;
     } else if (!(c = calloc(1, sizeof *c))) rc = PINFER_E_NOMEM;
     if (rc == PINFER_OK) {

@@ -190,8 +190,8 @@ def test_stop_inside_commit(agree_model):
 
 @needs_ref
 def test_long_context(models):
-    """A 1000-token context: the attention's value rows then span two LDS tiles (896 positions
-    each) in the prefill chunks and in the single-token steps after them."""
+    """A 1000-token context: the attention's value rows then span several LDS tiles (448
+    positions, then 192 each) in the prefill chunks and in the single-token steps after them."""
     gpu, ref = pair(models["small"], max_ctx=1200)
     rng = np.random.default_rng(13)
     prompt = rng.integers(0, pqfile.SMALL.vocab, 1000)
@@ -201,6 +201,26 @@ def test_long_context(models):
         assert np.array_equal(bits(gpu.eval([tok])), bits(ref.eval([tok]))), "single steps"
     tg, sg = gpu.generate([int(tok)], 12, k=4, draft_vocab=1024, cont=True)
     tr, sr = ref.generate([int(tok)], 12, k=4, draft_vocab=1024, cont=True)
+    assert tg == tr and (sg.rounds, sg.accepted) == (sr.rounds, sr.accepted)
+    gpu.close(), ref.close()
+
+
+@needs_ref
+@pytest.mark.parametrize("kv_dtype", [0, 2])
+def test_context_past_lds_scores(models, kv_dtype):
+    """max_ctx 9216, above the 8192 scores that the in-LDS softmax holds: the attention runs the
+    segmented kernel (exponentials 4096 at a time, the ordered partial sums carried across
+    segments, weights recomputed per value tile). An 8400-token prefill, single steps and a
+    speculative continuation equal the reference engine's."""
+    gpu, ref = pair(models["small"], max_ctx=9216, kv_dtype=kv_dtype)
+    rng = np.random.default_rng(14)
+    prompt = rng.integers(0, pqfile.SMALL.vocab, 8400)
+    print(f"[case] context 8400 of 9216 kv_dtype={kv_dtype}", flush=True)
+    assert np.array_equal(bits(gpu.eval(prompt)), bits(ref.eval(prompt))), "after the prefill"
+    for tok in rng.integers(0, pqfile.SMALL.vocab, 2):
+        assert np.array_equal(bits(gpu.eval([tok])), bits(ref.eval([tok]))), "single steps"
+    tg, sg = gpu.generate([int(tok)], 10, k=4, draft_vocab=1024, cont=True)
+    tr, sr = ref.generate([int(tok)], 10, k=4, draft_vocab=1024, cont=True)
     assert tg == tr and (sg.rounds, sg.accepted) == (sr.rounds, sr.accepted)
     gpu.close(), ref.close()
 
