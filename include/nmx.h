@@ -264,6 +264,13 @@ typedef struct {
 int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p);
 int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p);
 
+/* flag[0] = (top-1 probability of logits[0, n) >= tau): with mx = max (pf_softmax_max) and
+ * s = sum of pf_expf(l_i - mx) in the reference's order (4 interleaved partial sums, tail,
+ * pf_softmax_exp engine/src/forward_ops.c:294-353), p = s > 0 ? 1 / s : 0 (spec.c:93-97
+ * top1_prob). One workgroup; the decision is exact (an fp64 sum decides unless p is within the
+ * fp32 sum's error bound of tau, where the ordered fp32 sum itself is formed). */
+int nmx_top1_gate(nmx_ctx *ctx, const float *logits, int n, float tau, int32_t *flag);
+
 /* Rollback commit of every linear layer (pf_lin_commit, engine/src/forward_lin.c:185-204)
  * with e = ctl[1]: conv state <- last conv_k - 1 rows of [state after token 0, raw inputs
  * 1..e-1]; pend <- log rows 1..e-1; ctl[2] = e - 1. Arrays are [layers][...] contiguous. */

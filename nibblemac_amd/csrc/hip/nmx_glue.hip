@@ -884,6 +884,62 @@ __global__ __launch_bounds__(256) void attn_pv_long_k(Attn a, const float *__res
     }
 }
 
+/* ---- confidence gate of a draft (engine/src/spec.c:93-97, forward_ops.c:294-353) -------
+ * p = 1 / s, s = sum of e_i = pf_expf(l_i - max) in the reference's order; flag = p >= tau.
+ * The e_i are summed in fp64 first (error ~ n 2^-53, negligible); the ordered fp32 sum differs
+ * from the exact one by at most (n / 4 + n % 4 + 3) 2^-24 relative (positive terms), so unless
+ * 1 / s64 is within twice n 2^-24 of tau the comparison is decided. Otherwise the fp32 sum is
+ * formed as the reference forms it, the exponentials PV_SEG at a time in LDS, the four partial
+ * sums and the tail carried across segments. */
+__global__ __launch_bounds__(1024) void top1_gate_k(const float *__restrict__ l, int n, float tau,
+                                                    int32_t *__restrict__ flag) {
+    __shared__ float seg[PV_SEG];
+    __shared__ float redf[16];
+    __shared__ double redd[16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += 1024) mx = fmaxf(mx, l[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) redf[w] = mx;
+    __syncthreads();
+    mx = redf[0];
+    for (int j = 1; j < 16; j++) mx = fmaxf(mx, redf[j]);
+    double s64 = 0.0;
+    for (int i = tid; i < n; i += 1024) s64 += (double)nmx_expf_cephes(l[i] - mx);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s64 += __shfl_xor(s64, off);
+    if (lane == 0) redd[w] = s64;
+    __syncthreads();
+    s64 = 0.0;
+    for (int j = 0; j < 16; j++) s64 += redd[j];
+    const double p64 = s64 > 0.0 ? 1.0 / s64 : 0.0, m = 2.0 * (double)(n + 16) * 0x1p-24;
+    if (p64 * (1.0 - m) >= (double)tau || p64 * (1.0 + m) < (double)tau) {
+        if (tid == 0) flag[0] = p64 >= (double)tau;
+        return; /* uniform: every thread took the same branch */
+    }
+    const int q4 = 4 * (n >> 2);
+    float chain = 0.0f; /* lane tid < 4: partial sum tid; lane 4: the tail */
+    for (int s0 = 0; s0 < n; s0 += PV_SEG) {
+        const int len = n - s0 < PV_SEG ? n - s0 : PV_SEG;
+        __syncthreads(); /* the previous segment is consumed */
+        for (int i = tid; i < len; i += 1024) seg[i] = nmx_expf_cephes(l[s0 + i] - mx);
+        __syncthreads();
+        const int full = q4 - s0 < len ? (q4 - s0 > 0 ? q4 - s0 : 0) : len;
+        if (tid < 4) chain = pv_chain(chain, seg + tid, 4, full >> 2);
+        else if (tid == 4)
+            for (int i = full; i < len; i++) chain = chain + seg[i];
+    }
+    __syncthreads();
+    if (tid < 5) redf[tid] = chain;
+    __syncthreads();
+    if (tid == 0) {
+        const float sum = ((redf[0] + redf[1]) + (redf[2] + redf[3])) + redf[4];
+        const float p = sum > 0.0f ? 1.0f / sum : 0.0f;
+        flag[0] = p >= tau;
+    }
+}
+
 /* ---- rollback commit over every linear layer (engine/src/forward_lin.c:185-204): with
  * E = e - 1 (e = ctl[1]), conv state <- last K-1 rows of [state after token 0, raw inputs
  * 1..E]; pending replay rows <- log rows 1..E; ctl[2] = E (keep). */
@@ -1121,6 +1177,15 @@ int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p) {
     if (p->kv_dtype == KV_F16) return launch_attn<KV_F16>(ctx, p, a);
     if (p->kv_dtype == KV_I8) return launch_attn<KV_I8>(ctx, p, a);
     return launch_attn<KV_F32>(ctx, p, a);
+}
+
+int nmx_top1_gate(nmx_ctx *ctx, const float *logits, int n, float tau, int32_t *flag) {
+    if (!ctx) return -1;
+    if (!logits || !flag || n < 1 || n > (1 << 24))
+        return nmx_fail(ctx, "nmx_top1_gate: bad arguments");
+    top1_gate_k<<<1, 1024, 0, ctx->stream>>>(logits, n, tau, flag);
+    NMX_LAUNCHED(ctx, "top1_gate");
+    return 0;
 }
 
 size_t nmx_kv_bytes(int kv_dtype, int nkv, int max_ctx, int hd) {

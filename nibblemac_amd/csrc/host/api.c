@@ -129,6 +129,7 @@ static int alloc_state(pinfer_ctx *c) {
     c->mbuf = dalloc(c, (size_t)3 * H * 4, &ok);
     c->ctl = dalloc(c, 16 * 4, &ok);
     c->vt = dalloc(c, (E_MAX_K + 2) * 4, &ok);
+    c->gate = dalloc(c, (E_MAX_K + 2) * 4, &ok);
     c->tok = dalloc(c, B * 4, &ok);
     c->hout = dalloc(c, (2 + B) * 4, &ok);
     c->hout2 = dalloc(c, 4 * 4, &ok);

@@ -76,6 +76,24 @@ void e_ngram_pop(e_ngram *g);
  * tokens the two occurrences share backwards. */
 int e_ngram_draft(e_ngram *g, int32_t *out, int max, int *match);
 
+/* The adaptive speculation policy (adapt.c, engine/src/spec.h:49-57, spec_adapt.c) */
+#define E_AD_W (PINFER_SPEC_MAX_K + 2) /* verify widths 1..PINFER_SPEC_MAX_K + 1 */
+#define E_AD_TAU 0.6f                  /* chain on while the newest draft's top-1 p >= this */
+typedef struct {
+    double tv[E_AD_W];    /* running seconds of a verify pass of n tokens, 0 = not measured */
+    double t_plain;       /* running seconds of the plain steps taken, 0 = none yet */
+    double r_tok, r_sec;  /* decayed tokens emitted and seconds spent by speculative rounds */
+    int n_spec;           /* speculative rounds since speculation (or a probe) started */
+    int plain_mode;       /* plain steps; speculation is probed after probe_after of them */
+    int plain_run, probe_after;
+    int probing;          /* plain mode: the current speculative rounds are a probe */
+} e_adapt;
+
+void e_adapt_init(e_adapt *a);
+int e_adapt_plain_now(e_adapt *a);
+void e_adapt_plain(e_adapt *a, double sec);
+void e_adapt_round(e_adapt *a, int n, int emitted, double sec, double t_verify);
+
 struct pinfer_ctx {
     nmx_ctx *dev;
     /* dimensions (engine/src/pinfer.c:45-63) */
@@ -129,6 +147,11 @@ struct pinfer_ctx {
     nmx_graph *g_verify[E_MAX_K + 1], *g_commit[E_MAX_K + 1];
     /* n-gram rounds: verify without the MTP chain, commit without the MTP pass */
     nmx_graph *g_verify_ng[E_MAX_K + 1], *g_commit_ng;
+    /* adaptive rounds: one MTP chain step per graph (draft s + 1 and its confidence gate) */
+    nmx_graph *g_chain[E_MAX_K + 1];
+    int gate_on;              /* this generation computes the confidence gates (adaptive) */
+    int graph_gate;           /* gate_on when the graphs were captured */
+    int32_t *gate;            /* [E_MAX_K + 2] device: top-1 p of draft s >= E_AD_TAU (0: d1) */
     e_ngram ng;               /* token history of the prompt-lookup drafts */
     int graph_nv;             /* draft vocabulary the graphs were captured with */
     int use_graphs;
@@ -144,7 +167,8 @@ struct pinfer_ctx {
 int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged);
 int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits);
 int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst);
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst,
+                  int32_t *gate_dst);
 int e_set_pos(pinfer_ctx *c, int pos);
 
 /* spec.c */

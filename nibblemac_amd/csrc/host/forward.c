@@ -164,9 +164,12 @@ int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits) {
 /* The MTP draft head (engine/src/mtp.c:60-100) over n rows: h_dev [n][H] final-normed
  * hiddens, tok_dev [n] the tokens that follow them, positions ctl[0] + pos_off + i. The
  * selected row (n - 1, or ctl[1] - 1 when head_row_dynamic) gives the draft (argmax over the
- * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL). */
+ * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL); with
+ * gate_dst, also whether the draft's top-1 probability over those rows is >= E_AD_TAU
+ * (engine/src/spec.c:93-97 top1_prob, spec_adapt.c pf_adapt_chain_more). */
 int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst) {
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst,
+                  int32_t *gate_dst) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H;
@@ -189,6 +192,8 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
     const int off = head_row_dynamic ? -1 : n - 1;
     if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));
-    if (draft_dst) return head_row(c, idx, off, nv, draft_dst, 0);
+    if (!draft_dst) return PINFER_OK;
+    TRY(head_row(c, idx, off, nv, draft_dst, gate_dst != NULL));
+    if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
     return PINFER_OK;
 }

@@ -41,7 +41,8 @@ void e_drop_graphs(pinfer_ctx *c) {
         nmx_graph_destroy(c->g_verify[i]);
         nmx_graph_destroy(c->g_commit[i]);
         nmx_graph_destroy(c->g_verify_ng[i]);
-        c->g_verify[i] = c->g_commit[i] = c->g_verify_ng[i] = NULL;
+        nmx_graph_destroy(c->g_chain[i]);
+        c->g_verify[i] = c->g_commit[i] = c->g_verify_ng[i] = c->g_chain[i] = NULL;
     }
     nmx_graph_destroy(c->g_commit_ng);
     c->g_commit_ng = NULL;
@@ -60,7 +61,7 @@ static float *m_ping(pinfer_ctx *c, int i) { return c->mbuf + (size_t)(1 + (i & 
 static int seq_verify(pinfer_ctx *c, int ke, int nv) {
     for (int s = 1; s < ke; s++) {
         const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
-        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s)));
+        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), NULL));
     }
     TRY(e_forward(c, c->vt, ke + 1, 1));
     e_scratch *sc = &c->s;
@@ -77,7 +78,8 @@ static int seq_commit(pinfer_ctx *c, int ke, int nv) {
                          c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl};
     if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
     CK(nmx_copy_d2d(c->dev, c->hbuf, c->s.xn, (size_t)(ke + 1) * c->H * sizeof(float)));
-    TRY(e_mtp_forward(c, c->hbuf, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c)));
+    TRY(e_mtp_forward(c, c->hbuf, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c),
+                      c->gate_on ? c->gate : NULL));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
 }
@@ -104,23 +106,33 @@ static int seq_commit_ng(pinfer_ctx *c) {
     return PINFER_OK;
 }
 
-enum { SEQ_VERIFY, SEQ_COMMIT, SEQ_VERIFY_NG, SEQ_COMMIT_NG };
+/* Adaptive rounds: chain step s drafts vt[s + 1] from (m of draft s, vt[s]) at position
+ * n_past - 1 + s and gates it (gate[s]) (engine/src/spec.c:369-383). */
+static int seq_chain(pinfer_ctx *c, int s, int nv) {
+    const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
+    return e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), c->gate + s);
+}
+
+enum { SEQ_VERIFY, SEQ_COMMIT, SEQ_VERIFY_NG, SEQ_COMMIT_NG, SEQ_CHAIN };
 
 static int seq_run(pinfer_ctx *c, int ke, int nv, int kind) {
     switch (kind) {
     case SEQ_VERIFY: return seq_verify(c, ke, nv);
     case SEQ_COMMIT: return seq_commit(c, ke, nv);
     case SEQ_VERIFY_NG: return seq_verify_ng(c, ke);
+    case SEQ_CHAIN: return seq_chain(c, ke, nv);
     default: return seq_commit_ng(c);
     }
 }
 
 static int graph_for(pinfer_ctx *c, int ke, int nv, int kind, nmx_graph **out) {
     nmx_graph **slot = kind == SEQ_VERIFY ? &c->g_verify[ke] : kind == SEQ_COMMIT ? &c->g_commit[ke]
-                     : kind == SEQ_VERIFY_NG ? &c->g_verify_ng[ke] : &c->g_commit_ng;
-    if (c->graph_nv != nv) {
+                     : kind == SEQ_VERIFY_NG ? &c->g_verify_ng[ke]
+                     : kind == SEQ_CHAIN ? &c->g_chain[ke] : &c->g_commit_ng;
+    if (c->graph_nv != nv || c->graph_gate != c->gate_on) {
         e_drop_graphs(c);
         c->graph_nv = nv;
+        c->graph_gate = c->gate_on;
     }
     if (!*slot) {
         CK(nmx_graph_begin(c->dev));
@@ -191,7 +203,7 @@ static int prefill(pinfer_ctx *c, const int32_t *prompt, int n, int use_mtp, int
             CK(nmx_upload(c->dev, c->tok, next, (size_t)nb * sizeof(int32_t)));
             if (last) CK(nmx_copy_d2d(c->dev, c->tok + nb - 1, c->vt, sizeof(int32_t)));
             TRY(e_mtp_forward(c, c->hbuf, c->tok, nb, 0, 0, nv, last ? c->vt + 1 : NULL,
-                              last ? m_cur(c) : NULL));
+                              last ? m_cur(c) : NULL, last && c->gate_on ? c->gate : NULL));
         }
         c->n_past += nb;
     }
@@ -226,7 +238,8 @@ static int flush_pending(pinfer_ctx *c, e_pending *pd, int nv) {
     if (pd->n == 0) return PINFER_OK;
     CK(nmx_upload(c->dev, c->tok, pd->tok, (size_t)pd->n * sizeof(int32_t)));
     TRY(e_set_pos(c, pd->pos));
-    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c)));
+    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c),
+                      c->gate_on ? c->gate : NULL));
     c->mtp_rows = pd->pos + pd->n;
     pd->n = 0;
     TRY(e_set_pos(c, c->n_past));
@@ -307,6 +320,8 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
     if (n_prompt > c->max_ctx - c->n_past) return *status = PINFER_E_CTX_FULL;
     const int use_mtp = sp->k > 0, nv = draft_vocab(c, sp);
     const int drafting = sp->k > 0 || sp->ngram > 0;
+    const int adaptive = sp->adaptive && drafting;
+    c->gate_on = adaptive && use_mtp; /* the MTP passes also gate their drafts */
     e_stop stop = {no_eos ? -1 : c->eos, opts ? opts->stop_ids : NULL, opts ? opts->n_stop : 0,
                    opts ? opts->on_token : NULL, opts ? opts->user : NULL};
     /* the n-gram history is the fed tokens plus the last emitted one, with which a continuation
@@ -325,6 +340,8 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
     int count = 0, done = emit(out, &count, n_max, cur, &stop);
     e_pending pd;
     pd.n = pd.pos = 0;
+    e_adapt ad;
+    e_adapt_init(&ad);
     int32_t host[2 + E_MAX_BATCH], vt[E_MAX_K + 2];
     while (!done) {
         const int P = c->n_past;
@@ -334,18 +351,24 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             rc = PINFER_E_CTX_FULL;
             break;
         }
-        /* prompt lookup first, else MTP drafts, else a plain step */
+        const double r0 = now_sec();
+        /* prompt lookup first, else MTP drafts, else a plain step (the adaptive policy may
+         * take plain steps instead, engine/src/spec.c:300-312) */
         int ke = 0, use_ng = 0;
-        if (sp->ngram > 0 && left > 0) ke = ngram_pick(c, sp, left, vt + 1, &pd, nv, &rc);
-        if (rc != PINFER_OK) break;
-        use_ng = ke > 0;
-        if (!use_ng) ke = sp->k < left ? sp->k : left;
+        if (!(adaptive && e_adapt_plain_now(&ad))) {
+            if (sp->ngram > 0 && left > 0) ke = ngram_pick(c, sp, left, vt + 1, &pd, nv, &rc);
+            if (rc != PINFER_OK) break;
+            use_ng = ke > 0;
+            if (!use_ng) ke = sp->k < left ? sp->k : left;
+        }
         if (ke == 0) {
             if (st && drafting) st->rounds++;
             if ((rc = plain_step(c, use_mtp, &pd, nv, &cur)) != PINFER_OK) break;
+            if (adaptive) e_adapt_plain(&ad, now_sec() - r0);
             done = emit(out, &count, n_max, cur, &stop);
             continue;
         }
+        double rv = 0.0; /* start of the verify pass */
         if (use_ng) {
             /* room for this round's rows among the pending ones */
             if (use_mtp && pd.n + ke + 1 > E_MAX_BATCH && (rc = flush_pending(c, &pd, nv)) != PINFER_OK)
@@ -354,16 +377,38 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
                 rc = PINFER_E_ARG;
                 break;
             }
+            rv = now_sec();
             if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
-        } else {
+        } else if (!c->gate_on) {
             if ((rc = flush_pending(c, &pd, nv)) != PINFER_OK) break; /* d1 current */
+            rv = now_sec();
             if ((rc = run_seq(c, ke, nv, SEQ_VERIFY)) != PINFER_OK) break;
+        } else { /* adaptive: chain the MTP head while the newest draft is confident */
+            if ((rc = flush_pending(c, &pd, nv)) != PINFER_OK) break; /* d1 and its gate */
+            int32_t ok = 0, s = 1;
+            if (nmx_download(c->dev, &ok, c->gate, sizeof ok)) {
+                rc = PINFER_E_ARG;
+                break;
+            }
+            while (s < ke && ok) {
+                if ((rc = run_seq(c, s, nv, SEQ_CHAIN)) != PINFER_OK) break;
+                if (nmx_download(c->dev, &ok, c->gate + s, sizeof ok)) {
+                    rc = PINFER_E_ARG;
+                    break;
+                }
+                s++;
+            }
+            if (rc != PINFER_OK) break;
+            ke = s;
+            rv = now_sec();
+            if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
         }
         if (nmx_download(c->dev, host, c->hout, 2 * sizeof(int32_t)) ||
             nmx_download(c->dev, vt, c->vt, (size_t)(ke + 2) * sizeof(int32_t))) {
             rc = PINFER_E_ARG;
             break;
         }
+        const double tv = now_sec() - rv; /* the verify pass (its results read back) */
         const int a = host[0];
         int e = 0;
         while (e <= a && !done) done = emit(out, &count, n_max, vt[++e], &stop);
@@ -390,6 +435,13 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
                 st->ngram_drafted += ke;
                 st->ngram_accepted += a;
             }
+        }
+        if (adaptive) { /* the round's time includes its commit (and MTP pass) */
+            if (nmx_sync(c->dev)) {
+                rc = PINFER_E_ARG;
+                break;
+            }
+            e_adapt_round(&ad, ke + 1, e, now_sec() - r0, tv);
         }
     }
     if (rc == PINFER_OK && use_mtp) rc = flush_pending(c, &pd, nv);

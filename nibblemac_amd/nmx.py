@@ -103,6 +103,8 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_lin_mix": (_i, [_vp, ctypes.POINTER(LinMixArgs)]),
     "nmx_q4k_swiglu": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, ctypes.POINTER(NormIn),
                             _vp, A8, A8, _vp, _vp]),
+    "nmx_top1_gate": (_i, [_vp, _vp, _i, ctypes.c_float, _vp]),
+    "nmx_kv_bytes": (_sz, [_i, _i, _i, _i]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -348,6 +350,11 @@ class Device:
         self.check(self.lib.nmx_head_accept(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
                                             _p(logits), _p(drafts), _p(work), _p(out)),
                    "head_accept")
+
+
+    def top1_gate(self, logits, n: int, tau: float, flag) -> None:
+        """flag[0] = top-1 softmax probability of logits[0, n) >= tau (nmx_top1_gate)."""
+        self.check(self.lib.nmx_top1_gate(self.ctx, _p(logits), n, tau, _p(flag)), "top1_gate")
 
 
 def _p(x) -> int | None:

@@ -53,6 +53,7 @@ _SIGS = {
     "orc_argmax": (_i, [_vp, _i]),
     "orc_accept": (_i, [_vp, _i, _vp, _i, _vp, _vp]),
     "orc_expf_cephes": (_f, [_f]),
+    "orc_top1_prob": (_f, [_vp, _i]),
     "orc_gate_expf": (_f, [_f]),
     "orc_gate_log1pf": (_f, [_f]),
 }
@@ -90,6 +91,8 @@ def ref_lib() -> ctypes.CDLL | None:
         R.pf_lin_apply.restype, R.pf_lin_apply.argtypes = None, [_vp, _vp, _vp, _i, _i, _i, _i]
         R.pf_expf.restype, R.pf_expf.argtypes = _f, [_f]
         R.pf_argmax.restype, R.pf_argmax.argtypes = _i, [_vp, _i]
+        R.pf_softmax_max.restype, R.pf_softmax_max.argtypes = _f, [_vp, _i]
+        R.pf_softmax_exp.restype, R.pf_softmax_exp.argtypes = _f, [_vp, _i, _f]
         _ref = R
     return _ref
 
@@ -161,6 +164,11 @@ def lin_apply(S, log, keep, heads, dk, dv):
     log = np.ascontiguousarray(log, np.float32)
     lib().orc_lin_apply(_ptr(S), _ptr(log), keep, heads, dk, dv)
     return S
+
+
+def top1_prob(logits: np.ndarray) -> np.float32:
+    l = np.ascontiguousarray(logits, np.float32)
+    return np.float32(lib().orc_top1_prob(_ptr(l), l.size))
 
 
 def argmax(v: np.ndarray) -> int:

@@ -23,6 +23,8 @@
  *                                   replay == direct run
  *   orc_argmax / orc_accept         brute force; oracle/_ref pf_argmax
  *   orc_expf_cephes                 oracle/_ref pf_expf bit for bit over a dense sweep
+ *   orc_top1_prob                   oracle/_ref pf_softmax_max + pf_softmax_exp on random and
+ *                                   peaked rows; one-hot closed form (p = 1)
  *   orc_q4k_quantize                numpy restatement byte-for-byte; dequantised error bound
  */
 #ifndef NMX_ORACLE_H
@@ -91,6 +93,9 @@ int orc_accept(const float *logits, int V, const int32_t *drafts, int k, int32_t
 
 /* ---- scalar primitives of the forward pass (engine/src/forward_ops.c) ------------------- */
 float orc_expf_cephes(float x); /* pf_expf, forward_ops.c:41-56 */
+/* top-1 softmax probability of l[0, n) (spec.c:93-97 top1_prob over pf_softmax_max /
+ * pf_softmax_exp, forward_ops.c:294-353): p = s > 0 ? 1 / s : 0 */
+float orc_top1_prob(const float *l, int n);
 
 /* exp / log1p for the DeltaNet gates: evaluated in binary64 and rounded once to binary32.
  * The reference calls glibc expf / log1pf (forward_lin.c:18-19,59-66); these stand in for

@@ -99,6 +99,22 @@ float orc_expf_cephes(float x) {
     return y * s;
 }
 
+/* top1_prob (engine/src/spec.c:93-97): mx = max (pf_softmax_max: greater-than scan, any order
+ * gives the same value); s = sum of pf_expf(l_i - mx) as pf_softmax_exp forms it: partial
+ * sum j over e[4m + j] for the first n / 4 * 4 elements, s = (c0 + c1) + (c2 + c3), then the
+ * tail sequentially into t, s + t (forward_ops.c:320-353). */
+float orc_top1_prob(const float *l, int n) {
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++)
+        if (l[i] > mx) mx = l[i];
+    float c[4] = {0.0f, 0.0f, 0.0f, 0.0f}, t = 0.0f;
+    const int q4 = n / 4 * 4;
+    for (int i = 0; i < q4; i++) c[i % 4] = c[i % 4] + orc_expf_cephes(l[i] - mx);
+    for (int i = q4; i < n; i++) t = t + orc_expf_cephes(l[i] - mx);
+    const float s = ((c[0] + c[1]) + (c[2] + c[3])) + t;
+    return s > 0.0f ? 1.0f / s : 0.0f;
+}
+
 /* ---- gate exp / log1p: binary64 evaluation, one rounding to binary32 -------------------
  * exp: Cody-Waite reduction x = k ln2 + r (ln2 split so k * LN2_HI is exact for |k| < 2^20),
  * |r| <= ln2/2, Taylor polynomial of degree 13 in Horner form (truncation < 2e-17), then the

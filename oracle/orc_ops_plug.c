@@ -5,8 +5,8 @@
  * (kern_act.c:14-42) + the exact Q4K x A8 product (kern_quant.c:148-245); pf_lin_rule /
  * pf_lin_apply = the scalar DeltaNet of matvec_ref.c:114-188; pf_get_row = kern_act.c:53-88.
  * `make -C oracle ref` links it with the reference's own forward pass, attention, DeltaNet
- * mixer + rollback log, MTP head and speculative loop (engine/src/*.c minus the kernel files,
- * compiled from where they lie) into oracle/_ref/libpinfer_refq4k.so: the reference engine
+ * mixer + rollback log, MTP head and speculative loop (the engine/src C files minus the
+ * kernel files, compiled from where they lie) into oracle/_ref/libpinfer_refq4k.so: the reference engine
  * running Q4K models on the CPU, the end-to-end checker of the MI355X engine. The DeltaNet gate
  * exp / log1p calls of those sources are bound to the oracle's binary64 versions (orc_num.c),
  * the values the device computes. */

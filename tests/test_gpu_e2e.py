@@ -141,6 +141,37 @@ def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
 
 
 @needs_ref
+@pytest.mark.parametrize("which,k,ngram", [("agree", 4, 0), ("agree", 8, 7), ("small", 4, 0),
+                                           ("small", 2, 4)])
+def test_adaptive_matches_reference(models, agree_model, which, k, ngram):
+    """The adaptive policy (pinfer_spec_params.adaptive, engine/src/spec_adapt.c): MTP chains
+    cut where the newest draft's top-1 probability falls below 0.6, plain steps while
+    speculation does not pay, probes back. Its choices follow measured times, so the two engines
+    may take different rounds (the counters are not compared); the tokens and the state may not
+    differ: both equal plain greedy, and the state blobs after the generation are identical.
+    The random model's drafts are almost never accepted, so its runs switch to plain steps."""
+    path, base = agree_model if which == "agree" else (models["small"], np.random.default_rng(
+        9).integers(0, pqfile.SMALL.vocab, 24))
+    prompt = np.concatenate([base, base[:20], base]) if ngram else base
+    gpu, ref = pair(path)
+    print(f"[case] adaptive {which} k={k} ngram={ngram}", flush=True)
+    plain, _ = gpu.generate(prompt, 96, k=0)
+    tg, sg = gpu.generate(prompt, 96, k=k, ngram=ngram, adaptive=1)
+    tr, sr = ref.generate(prompt, 96, k=k, ngram=ngram, adaptive=1)
+    print(f"[stats] rounds drafted accepted (+ n-gram): {counters(sg)}, reference {counters(sr)}",
+          flush=True)
+    assert tg == tr == plain
+    assert sg.accepted <= sg.drafted <= k * sg.rounds + ngram * sg.ngram_rounds
+    assert gpu.state_save() == ref.state_save(), "state after an adaptive generation"
+    tg2, _ = gpu.generate([tg[-1]] + list(base[:6]), 24, k=k, ngram=ngram, adaptive=1, cont=True)
+    tr2, _ = ref.generate([tr[-1]] + list(base[:6]), 24, k=k, ngram=ngram, adaptive=1, cont=True)
+    assert tg2 == tr2
+    probe = [1, 2, 3]
+    assert np.array_equal(bits(gpu.eval(probe)), bits(ref.eval(probe)))
+    gpu.close(), ref.close()
+
+
+@needs_ref
 @pytest.mark.parametrize("kv_dtype", [1, 2])
 def test_kv_dtypes_match_reference(models, agree_model, kv_dtype):
     """KV caches stored as binary16 (1) or int8 with row scales (2) (pinfer_params.kv_dtype,

@@ -88,3 +88,32 @@ def test_accept_brute_force():
             a += 1
         got_a, bonus, rows = oracle.accept(logits, drafts)
         assert (got_a, bonus, list(rows)) == (a, am[a], am)
+
+
+def near_threshold_rows(rng, n, p):
+    """Rows whose top-1 probability is about p: one logit 0, the others equal up to small noise,
+    so that (n - 1) exp(x) = 1 / p - 1."""
+    x = np.log((1.0 / p - 1.0) / (n - 1))
+    return (np.concatenate([[0.0], x + rng.normal(0, 1e-3, n - 1)])).astype(np.float32)
+
+
+@pytest.mark.skipif(ref is None, reason="oracle/_ref not built (reference absent)")
+@pytest.mark.parametrize("n", [1, 3, 4, 7, 100, 4099, 32768])
+def test_top1_prob_vs_reference_build(n):
+    """orc_top1_prob against the reference's own pf_softmax_max / pf_softmax_exp (the top1_prob
+    of engine/src/spec.c:93-97 composed from them), on random, peaked and near-0.6 rows."""
+    rng = np.random.default_rng(n)
+    rows = [rng.normal(0, 3, n).astype(np.float32), rng.normal(0, 0.1, n).astype(np.float32)]
+    if n > 1:
+        rows.append(near_threshold_rows(rng, n, 0.6))
+    for l in rows:
+        work = l.copy()
+        s = ref.pf_softmax_exp(work.ctypes.data, n, ref.pf_softmax_max(l.ctypes.data, n))
+        want = np.float32(1.0) / np.float32(s) if s > 0 else np.float32(0.0)
+        got = oracle.top1_prob(l)
+        assert got.view(np.uint32) == want.view(np.uint32), (n, got, want)
+
+
+def test_top1_prob_closed_forms():
+    assert oracle.top1_prob(np.float32([0.0, -1000, -1000, -1000])) == np.float32(1.0)
+    assert oracle.top1_prob(np.zeros(8, np.float32)) == np.float32(0.125)
