@@ -119,7 +119,7 @@ def head_roofline(reps: int = 20, graphs: int = 5, eager: bool = False,
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "q4k_mv_k<5,false,false> (LM head 248320x1024 Q4K x 5 A8 rows, cold)",
+            "kernel": "q4k_mvx_k<5,false> (LM head 248320x1024 Q4K x 5 A8 rows, block dots on the matrix cores, cold)",
             "us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": algo,
             "timing": "eager stream launches" if eager else "graph replays"}
 

@@ -187,6 +187,168 @@ __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, i
     }
 }
 
+/* Bytes i (the lane's row in its tile) of four dwords, gathered into one dword. */
+__device__ __forceinline__ uint32_t gather_byte4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                                 uint32_t sel) {
+    const uint32_t t01 = __builtin_amdgcn_perm(x1, x0, sel); /* [x0.i, x1.i, 0, 0] */
+    const uint32_t t23 = __builtin_amdgcn_perm(x3, x2, sel); /* [x2.i, x3.i, 0, 0] */
+    return __builtin_amdgcn_perm(t23, t01, 0x05040100u);     /* [x0.i, x1.i, x2.i, x3.i] */
+}
+
+/* decode6 for one row, four values per dword: lo = bytes s[0..3], hi = bytes s[4..7]. sel
+ * gathers byte i of two dwords into bytes 0-1, sel2 builds [h0, h1, h0, h1] from the two
+ * high-pair dwords; the 2-bit fields of s[k] sit at bit 2 (k >> 1) of h(k & 1). */
+__device__ __forceinline__ void decode6x4(uint32_t L0, uint32_t L1, uint32_t L2, uint32_t L3,
+                                          uint32_t H0, uint32_t H1, uint32_t sel, uint32_t sel2,
+                                          uint32_t &lo, uint32_t &hi) {
+    const uint32_t P = gather_byte4(L0, L1, L2, L3, sel);
+    const uint32_t Q = __builtin_amdgcn_perm(H1, H0, sel2);
+    const uint32_t q03 = (Q & 0x0000ffffu) | ((Q >> 2) & 0xffff0000u);
+    const uint32_t q47 = ((Q >> 4) & 0x0000ffffu) | ((Q >> 6) & 0xffff0000u);
+    lo = (P & 0x0f0f0f0fu) | ((q03 & 0x03030303u) << 4);
+    hi = ((P >> 4) & 0x0f0f0f0fu) | ((q47 & 0x03030303u) << 4);
+}
+
+__device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xffu); }
+
+/* The same matvec with the int32 block dots on the matrix cores, for 3..MAX_NV vectors (the
+ * verify head). Row per lane as in q4k_mv_k: each lane still owns its row's (row, vector)
+ * chains, in registers, in block order.
+ *
+ * One v_mfma_i32_32x32x32_i8 per half block (16 columns) gives every lane the dots of its own
+ * row with all the vectors, because the activation operand is block-diagonal. B operand: lane
+ * l supplies column l % 32 and K group l / 32 (16 bytes), here its own row's 16 nibbles as
+ * bytes. Result: lane l holds C[m][l % 32] for m = 8 i + 4 (l / 32) + j in element 4 i + j.
+ * A operand: lane l' supplies row m = l' % 32 of K group l' / 32. A[m][group g] is set to
+ * vector v(m) = 4 (m / 8) + m % 4 only where g = (m / 4) % 2, and to zero elsewhere. Then
+ * C[m][n] in lane n + 32 g takes only lane n + 32 g's own B bytes, so element v of every lane
+ * is the dot of the lane's row with vector v. The K order is the B layout's (low then high
+ * nibbles of code dwords 2h, 2h + 1), which the activation table copies.
+ *
+ * That table holds [block][half][vector] 16-byte rows and an all-zero copy of the same size.
+ * Every workgroup builds it in LDS after its first superblock's weight loads are issued; lanes
+ * whose A entries must be zero read the zero copy. Each block's operand reads are ordered
+ * after the previous block's chain steps (an empty asm on the LDS offset), and each superblock's
+ * weight loads after the last one's. Left alone, the compiler hoists every block's MFMAs and
+ * holds all their results, which halves the waves per SIMD. */
+template <int NV, bool AMAX>
+__global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, int v0,
+                                                 const int8_t *__restrict__ q,
+                                                 const float *__restrict__ d,
+                                                 const float *__restrict__ fs,
+                                                 unsigned long long *__restrict__ amax_key) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    extern __shared__ __align__(16) uint8_t xt[];
+    const int nb = cols >> 5, ent = nb * 2 * NV, tbytes = ent * 16;
+    const int wave_raw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const bool wave_live = wave_raw < tab.total_waves; /* every wave reaches the barrier */
+    const int wave = wave_live ? wave_raw : tab.total_waves - 1;
+    const int lane = threadIdx.x & 63;
+    const uint8_t *W = tab.s[0].W;
+    float *Y = tab.s[0].Y;
+    int rows = tab.s[0].rows, ystride = tab.s[0].ystride, wave0 = tab.s[0].wave0;
+#pragma unroll
+    for (int t = 1; t < NMX_MAX_SEGS; t++)
+        if (t < tab.count && wave >= tab.s[t].wave0) {
+            W = tab.s[t].W;
+            Y = tab.s[t].Y;
+            rows = tab.s[t].rows;
+            ystride = tab.s[t].ystride;
+            wave0 = tab.s[t].wave0;
+        }
+    const int row_raw = (wave - wave0) * 64 + lane;
+    const bool valid = wave_live && row_raw < rows;
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const uint32_t i = (uint32_t)(row & 3);
+    const int nsb = cols >> 8;
+    const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * nsb * SB_BYTES);
+    uint4 a0 = tp[0], a1 = tp[1], a2 = tp[2], a3 = tp[3], c[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) c[k] = tp[4 + 4 * k + i];
+
+    for (int e = threadIdx.x; e < ent; e += 256) {
+        const int v = e % NV, bp = e / NV, h = bp & 1, blk = bp >> 1;
+        const uint32_t *x = (const uint32_t *)(q + ((size_t)blk * n + v0 + v) * 32);
+        *(uint4 *)(xt + (size_t)e * 16) = make_uint4(x[2 * h], x[4 + 2 * h], x[2 * h + 1], x[5 + 2 * h]);
+        *(uint4 *)(xt + tbytes + (size_t)e * 16) = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const int m = lane & 31, vl = 4 * (m >> 3) + (m & 3);
+    const bool diag = ((m >> 2) & 1) == (lane >> 5) && vl < NV;
+    const uint8_t *xl = xt + (diag ? vl * 16 : tbytes);
+    const uint32_t sel = 0x0c0c0400u | i | (i << 8), sel2 = i | ((i + 4) << 8) | (i << 16) | ((i + 4) << 24);
+    const v16i zero = {};
+
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) acc[v] = 0.0f;
+    for (int sb = 0; sb < nsb; sb++) {
+        const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
+        const float D = half_bits_to_float(dw >> (16 * (i & 1)));
+        const float M = half_bits_to_float(mw >> (16 * (i & 1)));
+        uint32_t S03, S47, M03, M47;
+        decode6x4(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sel, sel2, S03, S47);
+        decode6x4(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sel, sel2, M03, M47);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float sc = D * byte_f(k < 4 ? S03 : S47, k & 3); /* exact: 6-bit x 11-bit */
+            const float of = M * byte_f(k < 4 ? M03 : M47, k & 3);
+            const int blk = sb * 8 + k;
+            const uint4 w = c[k];
+            const v4i b0 = {(int)(w.x & 0x0f0f0f0fu), (int)((w.x >> 4) & 0x0f0f0f0fu),
+                            (int)(w.y & 0x0f0f0f0fu), (int)((w.y >> 4) & 0x0f0f0f0fu)};
+            const v4i b1 = {(int)(w.z & 0x0f0f0f0fu), (int)((w.z >> 4) & 0x0f0f0f0fu),
+                            (int)(w.w & 0x0f0f0f0fu), (int)((w.w >> 4) & 0x0f0f0f0fu)};
+            int xo = blk * 2 * NV * 16;
+#pragma unroll
+            for (int v = 0; v < NV; v++) asm volatile("" : "+v"(xo) : "v"(acc[v]));
+            const v4i x0 = *(const v4i *)(xl + xo);
+            const v4i x1 = *(const v4i *)(xl + xo + NV * 16);
+            v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b0, zero, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b1, C, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const size_t ai = (size_t)blk * n + v0 + v;
+                acc[v] = __builtin_fmaf((float)C[v], sc * d[ai], acc[v]);
+                acc[v] = __builtin_fmaf(-of, fs[ai], acc[v]);
+            }
+        }
+        if (sb + 1 < nsb) {
+            int nxt = (sb + 1) * (SB_BYTES / 16);
+            asm volatile("" : "+v"(nxt) : "v"(acc[0]), "v"(acc[NV - 1]));
+            const uint4 *p = tp + nxt;
+            a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+#pragma unroll
+            for (int k = 0; k < 8; k++) c[k] = p[4 + 4 * k + i];
+        }
+    }
+    if (valid && Y) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) Y[(size_t)(v0 + v) * ystride + row] = acc[v];
+    }
+    if (AMAX) { /* as in q4k_mv_k */
+        __shared__ unsigned long long wkeys[4][MAX_NV];
+        const int wv = threadIdx.x >> 6;
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            unsigned long long key = valid ? argmax_key(acc[v], row) : 0ull;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const unsigned long long o = __shfl_xor(key, off);
+                key = o > key ? o : key;
+            }
+            if (lane == 0) wkeys[wv][v] = key;
+        }
+        __syncthreads();
+        if (threadIdx.x < NV) {
+            unsigned long long key = wkeys[0][threadIdx.x];
+            for (int w = 1; w < 4; w++) key = wkeys[w][threadIdx.x] > key ? wkeys[w][threadIdx.x] : key;
+            amax_key[(size_t)(v0 + threadIdx.x) * gridDim.x + blockIdx.x] = key;
+        }
+    }
+}
+
 /* Argmax of every row from the per-workgroup partial keys, then the acceptance loop of the
  * reference (engine/src/spec.c:340-345): a = 0; g = argmax(row 0); while a < k and
  * drafts[a] == g: a++, g = argmax(row a). out = [a, g, argmax(row 0..n-1)]. One workgroup of
@@ -522,6 +684,17 @@ template <int NV>
 void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
                const float *d, const float *fs, int32_t *dots, unsigned long long *am) {
     const unsigned blocks = (unsigned)((tab.total_waves + 3) / 4);
+    /* 3 or more vectors: the block dots on the matrix cores (bit-identical results; measured at
+     * 248320 x 1024, 5 vectors: 30 us against 34-38 us), while its activation table fits in
+     * the default 64 KB of LDS */
+    if constexpr (NV >= 3) {
+        const size_t xbytes = (size_t)2 * NV * cols;
+        if (!dots && xbytes <= 65536) {
+            if (am) q4k_mvx_k<NV, true><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+            else q4k_mvx_k<NV, false><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+            return;
+        }
+    }
     if (am) q4k_mv_k<NV, false, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
     else if (dots) q4k_mv_k<NV, true, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
     else q4k_mv_k<NV, false, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);

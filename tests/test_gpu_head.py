@@ -103,9 +103,10 @@ def test_head_ties_pick_first_index(dev):
     assert out[0] == 2 and out[1] == am[2]
 
 
-@pytest.mark.parametrize("n", [1, 2, 5, 9])
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 9])
 def test_head_widths_and_no_logits(dev, n):
-    """Any verify width (k = n - 1, plain step at n = 1), logits optional."""
+    """Any verify width (k = n - 1, plain step at n = 1; 3..8 on the matrix cores, 9 as passes
+    of 5 and 4), logits optional."""
     rng = np.random.default_rng(42 + n)
     rows, cols = 32768, 1024
     W = quantized_head(rng, rows, cols)

@@ -150,6 +150,33 @@ def test_q4k_multi_segment(dev, n):
         assert not dY.numpy()[:, r:].any(), "padding columns written"
 
 
+@pytest.mark.parametrize("n,cols", [(3, 1024), (4, 2048), (5, 1024), (6, 3584), (7, 1024),
+                                    (8, 4096), (11, 1024)])
+def test_q4k_matrix_core_matvec(dev, n, cols):
+    """Matrices past 32767 rows at 3..8 vectors per pass take the matrix-core kernel
+    (q4k_mvx_k, block-diagonal activation operand); n = 11 runs as passes of 6 and 5. Two
+    segments, the second ending inside a wave, outputs with padded strides; bit-exact against
+    the oracle, padding untouched. cols = 4096 at 8 vectors fills the activation table's 64 KB."""
+    print(f"[case] matrix-core matvec n={n} cols={cols}", flush=True)
+    rng = np.random.default_rng(70 + n)
+    shapes = [32768, 1000]
+    Ws = [gaussian_q4k(rng, r, cols) for r in shapes]
+    X = rng.standard_normal((n, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    dq, dd, dfs = dev.to_device(q), dev.to_device(d), dev.to_device(fs)
+    dWs = [dev.to_device(w) for w in Ws]
+    strides = [r + 4 for r in shapes]
+    dYs = [dev.zeros((n, s), np.float32) for s in strides]
+    dev.q4k_matmul_multi(dWs, shapes, dYs, strides, cols, n, dq, dd, dfs)
+    dev.sync()
+    for W, r, dY in zip(Ws, shapes, dYs):
+        ref = oracle.q4k_matmul(W, r, cols, q, d, fs, n)
+        assert_bits_equal(dY.numpy()[:, :r], ref, f"segment rows={r}")
+        assert not dY.numpy()[:, r:].any(), "padding columns written"
+    for b in (dq, dd, dfs, *dWs, *dYs):
+        b.free()
+
+
 @pytest.mark.parametrize("n", [9, 16, 17, 40, 64])
 def test_q4k_prefill_chunk(dev, n):
     """More than 8 vectors (prefill chunks, the MFMA kernel): ragged vector tiles, a matrix whose
