@@ -145,16 +145,24 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
 
 /* Head of one row of s->xn (row index *idx + off): argmax over the first `rows` head rows to
  * dst_dev (if not NULL); the logits of that row to c->logits when want_logits. */
+/* The head over the first `rows` rows for the one row whose A8 is in s->a_1: its argmax to
+ * dst_dev (when not NULL), the logits to c->logits when wanted. */
+static int head_a8(pinfer_ctx *c, int rows, int32_t *dst_dev, int want_logits) {
+    nmx_ctx *D = c->dev;
+    e_scratch *s = &c->s;
+    CK(nmx_head_accept(D, c->head.w, rows, c->H, 1, s->a_1.q, s->a_1.d, s->a_1.fs,
+                       want_logits ? c->logits : NULL, NULL, c->hwork, c->hout2));
+    if (dst_dev) CK(nmx_copy_d2d(D, dst_dev, c->hout2 + 1, sizeof(int32_t)));
+    return PINFER_OK;
+}
+
 static int head_row(pinfer_ctx *c, const int32_t *idx, int off, int rows, int32_t *dst_dev,
                     int want_logits) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     CK(nmx_select_row(D, s->xn, c->H, idx, off, c->H, s->row1));
     CK(nmx_quant_a8(D, s->row1, 1, c->H, s->a_1.q, s->a_1.d, s->a_1.fs));
-    CK(nmx_head_accept(D, c->head.w, rows, c->H, 1, s->a_1.q, s->a_1.d, s->a_1.fs,
-                       want_logits ? c->logits : NULL, NULL, c->hwork, c->hout2));
-    if (dst_dev) CK(nmx_copy_d2d(D, dst_dev, c->hout2 + 1, sizeof(int32_t)));
-    return PINFER_OK;
+    return head_a8(c, rows, dst_dev, want_logits);
 }
 
 int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits) {
@@ -175,11 +183,14 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     const int H = c->H;
     const nmx_a8 none = {NULL, NULL, NULL};
     CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, s->emb, H));
-    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)] */
-    CK(nmx_rmsnorm(D, s->emb, H, NULL, 0, c->mtp_norm_emb, n, H, c->rms_eps, s->cat, 2 * H, none));
+    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)]: each norm writes
+     * the A8 blocks of its half of the 2H row (blocks [0, H/32) and [H/32, 2H/32) of the
+     * [block][n][32] layout); a block never straddles the halves (H % 32 == 0) */
+    const size_t hb = (size_t)(H / 32) * n;
+    const nmx_a8 a8_emb = s->a_w, a8_hid = {s->a_w.q + hb * 32, s->a_w.d + hb, s->a_w.fs + hb};
+    CK(nmx_rmsnorm(D, s->emb, H, NULL, 0, c->mtp_norm_emb, n, H, c->rms_eps, s->cat, 2 * H, a8_emb));
     CK(nmx_rmsnorm(D, (float *)h_dev, H, NULL, 0, c->mtp_norm_hid, n, H, c->rms_eps, s->cat + H,
-                   2 * H, none));
-    CK(nmx_quant_a8(D, s->cat, n, 2 * H, s->a_w.q, s->a_w.d, s->a_w.fs));
+                   2 * H, a8_hid));
     e_resid r = {s->x, s->x2, NULL};
     CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H, NULL));
     const e_layer *L = &c->mtp;
@@ -187,6 +198,15 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     int rc = attn_block(c, L, n, c->mkc, c->mvc, pos_off);
     if (rc) return rc;
     if ((rc = mlp_block(c, L, n, &r))) return rc;
+    if (n == 1 && !head_row_dynamic) {
+        /* one row: the final norm writes the MTP hidden and the head's A8 input itself */
+        CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, 1, H, c->rms_eps,
+                          m_dst ? m_dst : s->xn, H, draft_dst ? s->a_1 : none));
+        if (!draft_dst) return PINFER_OK;
+        TRY(head_a8(c, nv, draft_dst, gate_dst != NULL));
+        if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
+        return PINFER_OK;
+    }
     CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H,
                       none));
     const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
