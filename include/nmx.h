@@ -40,6 +40,11 @@ int nmx_device_count(void);                 /* without creating a context; 0 if 
 
 void *nmx_alloc(nmx_ctx *ctx, size_t bytes);               /* device memory, NULL on failure */
 int nmx_free(nmx_ctx *ctx, void *ptr);
+/* Page-locked host memory that kernels may write (hipHostMalloc); the host reads it after a
+ * synchronisation of the stream, with no copy. No counterpart in the reference, whose engine
+ * runs on the host. NULL on failure. */
+void *nmx_host_alloc(nmx_ctx *ctx, size_t bytes);
+int nmx_host_free(nmx_ctx *ctx, void *ptr);
 int nmx_upload(nmx_ctx *ctx, void *dst, const void *src, size_t bytes);   /* synchronous */
 int nmx_download(nmx_ctx *ctx, void *dst, const void *src, size_t bytes); /* synchronous */
 int nmx_copy_d2d(nmx_ctx *ctx, void *dst, const void *src, size_t bytes); /* enqueued */
@@ -288,6 +293,11 @@ int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p);
 /* After nmx_head_accept: vt[a + 1] = bonus; ctl[1] = a + 1 (the reference's e without a stop,
  * engine/src/spec.c:346-349). */
 int nmx_accept_commit(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl);
+/* The same, also writing [a, bonus, vt[0..nvt) after the update] to mailbox (memory from
+ * nmx_host_alloc, 2 + nvt int32), so one synchronisation hands the round's result to the
+ * host (the reference's host loop reads them in place, engine/src/spec.c:340-351). */
+int nmx_accept_commit_mb(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl,
+                         int32_t *mailbox, int nvt);
 int nmx_ctl_set(nmx_ctx *ctx, int32_t *ctl, int idx, int value);
 int nmx_ctl_advance(nmx_ctx *ctx, int32_t *ctl);   /* ctl[0] += ctl[1] */
 int nmx_copy_token(nmx_ctx *ctx, int32_t *vt, const int32_t *ctl); /* vt[0] = vt[ctl[1]] */

@@ -978,10 +978,17 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
 }
 
 /* a = out[0], g = out[1] of nmx_head_accept: vt[a + 1] = g; ctl[1] = e = a + 1. */
-__global__ void accept_commit_k(const int32_t *out, int32_t *vt, int32_t *ctl) {
+/* mb (optional, host memory): [a, bonus, vt[0..nvt) after the update] */
+__global__ void accept_commit_k(const int32_t *out, int32_t *vt, int32_t *ctl, int32_t *mb, int nvt) {
     const int a = out[0];
-    vt[a + 1] = out[1];
-    ctl[1] = a + 1;
+    if (threadIdx.x == 0) {
+        vt[a + 1] = out[1];
+        ctl[1] = a + 1;
+    }
+    if (mb) {
+        if (threadIdx.x < 2) mb[threadIdx.x] = out[threadIdx.x];
+        for (int i = threadIdx.x; i < nvt; i += blockDim.x) mb[2 + i] = i == a + 1 ? out[1] : vt[i];
+    }
 }
 
 __global__ void ctl_k(int32_t *ctl, int op, int idx, int value) {
@@ -1211,7 +1218,17 @@ int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p) {
 int nmx_accept_commit(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl) {
     if (!ctx) return -1;
     if (!out || !vt || !ctl) return nmx_fail(ctx, "nmx_accept_commit: NULL pointer");
-    accept_commit_k<<<1, 1, 0, ctx->stream>>>(out, vt, ctl);
+    accept_commit_k<<<1, 1, 0, ctx->stream>>>(out, vt, ctl, nullptr, 0);
+    NMX_LAUNCHED(ctx, "accept_commit");
+    return 0;
+}
+
+int nmx_accept_commit_mb(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl,
+                         int32_t *mailbox, int nvt) {
+    if (!ctx) return -1;
+    if (!out || !vt || !ctl || !mailbox || nvt < 1 || nvt > 1024)
+        return nmx_fail(ctx, "nmx_accept_commit_mb: bad arguments");
+    accept_commit_k<<<1, 64, 0, ctx->stream>>>(out, vt, ctl, mailbox, nvt);
     NMX_LAUNCHED(ctx, "accept_commit");
     return 0;
 }

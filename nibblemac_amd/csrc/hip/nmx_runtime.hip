@@ -94,6 +94,28 @@ void *nmx_alloc(nmx_ctx *ctx, size_t bytes) {
     return p;
 }
 
+void *nmx_host_alloc(nmx_ctx *ctx, size_t bytes) {
+    if (!ctx) return nullptr;
+    if (bytes == 0) {
+        nmx_fail(ctx, "nmx_host_alloc: zero bytes");
+        return nullptr;
+    }
+    void *p = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        nmx_fail(ctx, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+int nmx_host_free(nmx_ctx *ctx, void *ptr) {
+    if (!ctx) return -1;
+    if (!ptr) return 0;
+    NMX_HIP(ctx, hipHostFree(ptr));
+    return 0;
+}
+
 int nmx_free(nmx_ctx *ctx, void *ptr) {
     if (!ctx) return -1;
     if (!ptr) return 0;

@@ -133,6 +133,8 @@ static int alloc_state(pinfer_ctx *c) {
     c->tok = dalloc(c, B * 4, &ok);
     c->hout = dalloc(c, (2 + B) * 4, &ok);
     c->hout2 = dalloc(c, 4 * 4, &ok);
+    c->mbox = ok ? (int32_t *)nmx_host_alloc(c->dev, (2 + E_MAX_K + 2) * sizeof(int32_t)) : NULL;
+    if (!c->mbox) ok = 0;
     c->hwork = dalloc(c, nmx_head_work_bytes(c->vocab, E_MAX_K + 1), &ok);
     c->logits = dalloc(c, (size_t)c->vocab * 4, &ok);
     if (!ok || e_ngram_init(&c->ng, c->max_ctx + 1)) return PINFER_E_NOMEM;
@@ -184,6 +186,7 @@ void pinfer_free(pinfer_ctx *c) {
     if (!c) return;
     if (c->dev) {
         e_drop_graphs(c);
+        nmx_host_free(c->dev, c->mbox);
         pinfer_checkpoint_clear(c);
         nmx_sync(c->dev);
         nmx_free(c->dev, c->blob);

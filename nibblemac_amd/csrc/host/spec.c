@@ -67,7 +67,7 @@ static int seq_verify(pinfer_ctx *c, int ke, int nv) {
     e_scratch *sc = &c->s;
     CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
                        NULL, c->vt + 1, c->hwork, c->hout));
-    CK(nmx_accept_commit(c->dev, c->hout, c->vt, c->ctl));
+    CK(nmx_accept_commit_mb(c->dev, c->hout, c->vt, c->ctl, c->mbox, ke + 2));
     return PINFER_OK;
 }
 
@@ -91,7 +91,7 @@ static int seq_verify_ng(pinfer_ctx *c, int ke) {
     e_scratch *sc = &c->s;
     CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
                        NULL, c->vt + 1, c->hwork, c->hout));
-    CK(nmx_accept_commit(c->dev, c->hout, c->vt, c->ctl));
+    CK(nmx_accept_commit_mb(c->dev, c->hout, c->vt, c->ctl, c->mbox, ke + 2));
     return PINFER_OK;
 }
 
@@ -403,11 +403,12 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             rv = now_sec();
             if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
         }
-        if (nmx_download(c->dev, host, c->hout, 2 * sizeof(int32_t)) ||
-            nmx_download(c->dev, vt, c->vt, (size_t)(ke + 2) * sizeof(int32_t))) {
+        if (nmx_sync(c->dev)) { /* the verify wrote (a, bonus, vt) to the host mailbox */
             rc = PINFER_E_ARG;
             break;
         }
+        memcpy(host, c->mbox, 2 * sizeof(int32_t));
+        memcpy(vt, c->mbox + 2, (size_t)(ke + 2) * sizeof(int32_t));
         const double tv = now_sec() - rv; /* the verify pass (its results read back) */
         const int a = host[0];
         int e = 0;
