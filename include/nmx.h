@@ -294,8 +294,10 @@ int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p);
  * engine/src/spec.c:346-349). */
 int nmx_accept_commit(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl);
 /* The same, also writing [a, bonus, vt[0..nvt) after the update] to mailbox (memory from
- * nmx_host_alloc, 2 + nvt int32), so one synchronisation hands the round's result to the
- * host (the reference's host loop reads them in place, engine/src/spec.c:340-351). */
+ * nmx_host_alloc, 3 + nvt int32) and then mailbox[2 + nvt] = 1 with a system-scope release:
+ * a host that clears that word before the launch and polls it (acquire) reads the round's
+ * result without a stream synchronisation (the reference's host loop reads them in place,
+ * engine/src/spec.c:340-351). */
 int nmx_accept_commit_mb(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl,
                          int32_t *mailbox, int nvt);
 int nmx_ctl_set(nmx_ctx *ctx, int32_t *ctl, int idx, int value);

@@ -978,16 +978,18 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
 }
 
 /* a = out[0], g = out[1] of nmx_head_accept: vt[a + 1] = g; ctl[1] = e = a + 1. */
-/* mb (optional, host memory): [a, bonus, vt[0..nvt) after the update] */
+/* mb (optional, host memory): [a, bonus, vt[0..nvt) after the update], then mb[2 + nvt] = 1
+ * with a system-scope release, so a host that reads 1 there (acquire) sees the values. One
+ * thread writes everything, in that order. */
 __global__ void accept_commit_k(const int32_t *out, int32_t *vt, int32_t *ctl, int32_t *mb, int nvt) {
-    const int a = out[0];
-    if (threadIdx.x == 0) {
-        vt[a + 1] = out[1];
-        ctl[1] = a + 1;
-    }
+    const int a = out[0], bonus = out[1];
+    vt[a + 1] = bonus;
+    ctl[1] = a + 1;
     if (mb) {
-        if (threadIdx.x < 2) mb[threadIdx.x] = out[threadIdx.x];
-        for (int i = threadIdx.x; i < nvt; i += blockDim.x) mb[2 + i] = i == a + 1 ? out[1] : vt[i];
+        mb[0] = a;
+        mb[1] = bonus;
+        for (int i = 0; i < nvt; i++) mb[2 + i] = i == a + 1 ? bonus : vt[i];
+        __hip_atomic_store(mb + 2 + nvt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -1228,7 +1230,7 @@ int nmx_accept_commit_mb(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t 
     if (!ctx) return -1;
     if (!out || !vt || !ctl || !mailbox || nvt < 1 || nvt > 1024)
         return nmx_fail(ctx, "nmx_accept_commit_mb: bad arguments");
-    accept_commit_k<<<1, 64, 0, ctx->stream>>>(out, vt, ctl, mailbox, nvt);
+    accept_commit_k<<<1, 1, 0, ctx->stream>>>(out, vt, ctl, mailbox, nvt);
     NMX_LAUNCHED(ctx, "accept_commit");
     return 0;
 }

@@ -153,11 +153,29 @@ static int graph_for(pinfer_ctx *c, int ke, int nv, int kind, nmx_graph **out) {
 }
 
 static int run_seq(pinfer_ctx *c, int ke, int nv, int kind) {
+    if (kind == SEQ_VERIFY || kind == SEQ_VERIFY_NG) /* cleared before the launch that sets it */
+        __atomic_store_n(c->mbox + 2 + ke + 2, 0, __ATOMIC_RELAXED);
     if (!c->use_graphs) return seq_run(c, ke, nv, kind);
     nmx_graph *g;
     TRY(graph_for(c, ke, nv, kind, &g));
     CK(nmx_graph_launch(c->dev, g));
     return PINFER_OK;
+}
+
+static double now_sec(void);
+
+/* Waits for the verify round's mailbox flag (mbox[2 + ke + 2], set last by the accept kernel
+ * with a system-scope release): a short spin on the host copy, then, after 2 s, the stream
+ * synchronisation, which also reports a failed launch. */
+static int wait_mailbox(pinfer_ctx *c, int ke) {
+    const int32_t *flag = c->mbox + 2 + ke + 2;
+    const double t0 = now_sec();
+    for (long spins = 0; !__atomic_load_n(flag, __ATOMIC_ACQUIRE); spins++)
+        if ((spins & 1023) == 1023 && now_sec() - t0 > 2.0) {
+            if (nmx_sync(c->dev)) return -1;
+            return __atomic_load_n(flag, __ATOMIC_ACQUIRE) ? 0 : -1;
+        }
+    return 0;
 }
 
 /* ---- host driver ------------------------------------------------------------------------- */
@@ -403,7 +421,7 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             rv = now_sec();
             if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
         }
-        if (nmx_sync(c->dev)) { /* the verify wrote (a, bonus, vt) to the host mailbox */
+        if (wait_mailbox(c, ke)) { /* the verify wrote (a, bonus, vt) to the host mailbox */
             rc = PINFER_E_ARG;
             break;
         }
