@@ -133,6 +133,11 @@ size_t nmx_head_work_bytes(int rows, int n);
 int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
                     const float *d, const float *fsum, float *logits, const int32_t *drafts,
                     void *work, int32_t *out);
+/* The same, also writing out[1] (the bonus / greedy token) to tok_dst (device int32, may be
+ * NULL): the MTP draft lands in the verify token row without a copy. */
+int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                       const float *d, const float *fsum, float *logits, const int32_t *drafts,
+                       void *work, int32_t *out, int32_t *tok_dst);
 
 /* ---- verify-step glue (the rest of one forward pass, engine/src/forward*.c) -------------
  * All enqueue on the context's stream; positions come from a device control block so a

@@ -356,7 +356,8 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
 __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *__restrict__ keys,
                                                       int nblk, int n,
                                                       const int32_t *__restrict__ drafts,
-                                                      int32_t *__restrict__ out) {
+                                                      int32_t *__restrict__ out,
+                                                      int32_t *__restrict__ tok_dst) {
     __shared__ unsigned long long red[16][8];
     __shared__ int am[64];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -398,6 +399,7 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
         out[0] = a;
         out[1] = g;
         for (int t = 0; t < n; t++) out[2 + t] = am[t];
+        if (tok_dst) *tok_dst = g;
     }
 }
 
@@ -876,6 +878,12 @@ size_t nmx_head_work_bytes(int rows, int n) {
 int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
                     const float *d, const float *fsum, float *logits, const int32_t *drafts,
                     void *work, int32_t *out) {
+    return nmx_head_accept_to(ctx, W, rows, cols, n, q, d, fsum, logits, drafts, work, out, nullptr);
+}
+
+int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                       const float *d, const float *fsum, float *logits, const int32_t *drafts,
+                       void *work, int32_t *out, int32_t *tok_dst) {
     if (!ctx) return -1;
     if (!W || !q || !d || !fsum || !work || !out || (n > 1 && !drafts))
         return nmx_fail(ctx, "nmx_head_accept: NULL pointer");
@@ -900,7 +908,7 @@ int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, cons
     const int blocks = (tab.total_waves + 3) / 4;
     unsigned long long *keys = (unsigned long long *)work;
     if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, keys)) return -1;
-    head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out);
+    head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out, tok_dst);
     NMX_LAUNCHED(ctx, "head_finish");
     return 0;
 }

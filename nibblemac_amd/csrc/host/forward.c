@@ -150,9 +150,8 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
 static int head_a8(pinfer_ctx *c, int rows, int32_t *dst_dev, int want_logits) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
-    CK(nmx_head_accept(D, c->head.w, rows, c->H, 1, s->a_1.q, s->a_1.d, s->a_1.fs,
-                       want_logits ? c->logits : NULL, NULL, c->hwork, c->hout2));
-    if (dst_dev) CK(nmx_copy_d2d(D, dst_dev, c->hout2 + 1, sizeof(int32_t)));
+    CK(nmx_head_accept_to(D, c->head.w, rows, c->H, 1, s->a_1.q, s->a_1.d, s->a_1.fs,
+                          want_logits ? c->logits : NULL, NULL, c->hwork, c->hout2, dst_dev));
     return PINFER_OK;
 }
 

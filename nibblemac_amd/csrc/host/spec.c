@@ -77,8 +77,8 @@ static int seq_commit(pinfer_ctx *c, int ke, int nv) {
     nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
                          c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl};
     if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
-    CK(nmx_copy_d2d(c->dev, c->hbuf, c->s.xn, (size_t)(ke + 1) * c->H * sizeof(float)));
-    TRY(e_mtp_forward(c, c->hbuf, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c),
+    /* the MTP pass reads the final-normed rows before it writes s.xn itself */
+    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c),
                       c->gate_on ? c->gate : NULL));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
