@@ -93,6 +93,11 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_lin_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "nmx_head_work_bytes": (_sz, [_i, _i]),
     "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nmx_head_accept_to": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nmx_accept_commit": (_i, [_vp, _vp, _vp, _vp]),
+    "nmx_accept_commit_mb": (_i, [_vp, _vp, _vp, _vp, _vp, _i]),
+    "nmx_host_alloc": (_vp, [_vp, _sz]),
+    "nmx_host_free": (_i, [_vp, _vp]),
     "nmx_rmsnorm_xo": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _i,
                             A8]),
     "nmx_silu_mul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, A8]),
@@ -346,10 +351,33 @@ class Device:
         return int(self.lib.nmx_head_work_bytes(rows, n))
 
     def head_accept(self, W, rows: int, cols: int, n: int, q, d, fs, logits, drafts, work,
-                    out) -> None:
-        self.check(self.lib.nmx_head_accept(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
-                                            _p(logits), _p(drafts), _p(work), _p(out)),
-                   "head_accept")
+                    out, tok_dst=None) -> None:
+        """nmx_head_accept, or nmx_head_accept_to when tok_dst (a device int32) is given."""
+        if tok_dst is None:
+            rc = self.lib.nmx_head_accept(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
+                                          _p(logits), _p(drafts), _p(work), _p(out))
+        else:
+            rc = self.lib.nmx_head_accept_to(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
+                                             _p(logits), _p(drafts), _p(work), _p(out), _p(tok_dst))
+        self.check(rc, "head_accept")
+
+    def accept_commit(self, out, vt, ctl, mailbox=None, nvt: int = 0) -> None:
+        """nmx_accept_commit, or nmx_accept_commit_mb writing the host mailbox."""
+        if mailbox is None:
+            rc = self.lib.nmx_accept_commit(self.ctx, _p(out), _p(vt), _p(ctl))
+        else:
+            rc = self.lib.nmx_accept_commit_mb(self.ctx, _p(out), _p(vt), _p(ctl), mailbox, nvt)
+        self.check(rc, "accept_commit")
+
+    def host_alloc(self, nbytes: int) -> int:
+        """Page-locked host memory kernels may write (nmx_host_alloc); free with host_free."""
+        p = self.lib.nmx_host_alloc(self.ctx, nbytes)
+        if not p:
+            raise NmxError(f"nmx_host_alloc({nbytes}): {self.lib.nmx_error(self.ctx).decode()}")
+        return p
+
+    def host_free(self, p: int) -> None:
+        self.check(self.lib.nmx_host_free(self.ctx, p), "host_free")
 
 
     def top1_gate(self, logits, n: int, tau: float, flag) -> None:

@@ -152,3 +152,52 @@ def test_head_accept_graph_replays_reuse_work(dev):
         assert got[0] == a_ref and got[1] == bonus_ref, (rep, got, a_ref, bonus_ref)
         assert np.array_equal(got[2:], am)
 
+
+
+@pytest.mark.parametrize("a", [0, 2, 4])
+def test_accept_commit_mailbox(dev, a):
+    """nmx_accept_commit_mb: vt[a + 1] = bonus and ctl[1] = a + 1 as nmx_accept_commit, and
+    the host mailbox holds [a, bonus, vt after the update] with its flag word set last (the
+    engine clears the flag before the launch and polls it)."""
+    import ctypes
+
+    k = 4
+    vt0 = np.arange(100, 100 + k + 2, dtype=np.int32)
+    out = dev.to_device(np.array([a, 777] + [0] * (k + 1), np.int32))
+    vt, ctl = dev.to_device(vt0), dev.zeros(16, np.int32)
+    nvt = k + 2
+    mb = dev.host_alloc((3 + nvt) * 4)
+    try:
+        view = (ctypes.c_int32 * (3 + nvt)).from_address(mb)
+        for i in range(3 + nvt):
+            view[i] = -1
+        view[2 + nvt] = 0
+        dev.accept_commit(out, vt, ctl, mailbox=mb, nvt=nvt)
+        dev.sync()
+        want_vt = vt0.copy()
+        want_vt[a + 1] = 777
+        assert list(view) == [a, 777] + list(want_vt) + [1]
+        assert np.array_equal(vt.numpy(), want_vt) and ctl.numpy()[1] == a + 1
+    finally:
+        dev.host_free(mb)
+        for b in (out, vt, ctl):
+            b.free()
+
+
+def test_head_accept_to_writes_token(dev):
+    """nmx_head_accept_to stores out[1] (the greedy token) at tok_dst as well."""
+    rng = np.random.default_rng(5)
+    rows, cols = 4096, 1024
+    W = quantized_head(rng, rows, cols)
+    X = rng.standard_normal((1, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, 1)
+    dW, dq, dd, dfs = dev.to_device(W), dev.to_device(q), dev.to_device(d), dev.to_device(fs)
+    work = dev.zeros(dev.head_work_bytes(rows, 1), np.uint8)
+    out, tok = dev.zeros(3, np.int32), dev.to_device(np.array([-5, -6], np.int32))
+    dev.head_accept(dW, rows, cols, 1, dq, dd, dfs, None, None, work, out, tok_dst=tok.ptr + 4)
+    dev.sync()
+    g = oracle.argmax(ref[0])
+    assert list(out.numpy()) == [0, g, g] and list(tok.numpy()) == [-5, g]
+    for b in (dW, dq, dd, dfs, work, out, tok):
+        b.free()
