@@ -26,7 +26,7 @@ def quantized_head(rng, rows, cols, chunk=16384):
 
 def planted_drafts(argmax_rows, a, k):
     """Drafts d_1..d_k with exactly a accepted: d_t = argmax(row t-1) for t <= a, then a draft
-    that differs from argmax(row a)."""
+    that differs from argmax(row a) (acceptance planted at 0 / 50 / 100 %)."""
     d = np.zeros(k, np.int32)
     for t in range(k):
         d[t] = argmax_rows[t] if t < a else (argmax_rows[t] + 1 + t) % 1000003
@@ -50,27 +50,27 @@ def run_head(dev, W, rows, cols, X, drafts, logits=True):
     return res
 
 
-_CONFIG4: dict = {}
+_HEAD_CASE: dict = {}
 
 
-def config4_case():
+def head_248320x1024_case():
     """248320 x 1024 Q4K head (N(0, 0.02) quantized) and 5 rows N(0, 1), built once."""
-    if not _CONFIG4:
+    if not _HEAD_CASE:
         rng = np.random.default_rng(40)
         rows, cols = 248320, 1024
         W = quantized_head(rng, rows, cols)
         X = rng.standard_normal((5, cols)).astype(np.float32)
         q, d, fs = oracle.quant_a8(X)
-        _CONFIG4.update(W=W, X=X, ref=oracle.q4k_matmul(W, rows, cols, q, d, fs, 5, threads=8))
-    return _CONFIG4["W"], _CONFIG4["X"], _CONFIG4["ref"]
+        _HEAD_CASE.update(W=W, X=X, ref=oracle.q4k_matmul(W, rows, cols, q, d, fs, 5, threads=8))
+    return _HEAD_CASE["W"], _HEAD_CASE["X"], _HEAD_CASE["ref"]
 
 
 @pytest.mark.parametrize("accept", [0, 2, 4])
-def test_config4_head_accept(dev, accept):
+def test_head_248320x1024_accept(dev, accept):
     """The config-4 head with 4 planted drafts at 0 / 50 / 100 % acceptance."""
-    print(f"[case] config4 head accept={accept}", flush=True)
+    print(f"[case] head 248320x1024 accept={accept}", flush=True)
     rows, cols = 248320, 1024
-    W, X, ref = config4_case()
+    W, X, ref = head_248320x1024_case()
     am = np.array([oracle.argmax(ref[t]) for t in range(5)], np.int32)
     drafts = planted_drafts(am, accept, 4)
     a_ref, bonus_ref, rows_ref = oracle.accept(ref, drafts)

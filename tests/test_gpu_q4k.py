@@ -94,9 +94,9 @@ def test_q4k_check_a8_shapes(dev, rows, cols, n):
     check_case(dev, W, rows, cols, X)
 
 
-def test_q4k_config1_matvec(dev):
+def test_q4k_3584x1024_matvec(dev):
     """3584x1024 Q4K (N(0, 0.02) quantized), one activation row N(0, 1)."""
-    print("[case] config1 3584x1024 n=1", flush=True)
+    print("[case] matvec 3584x1024 n=1", flush=True)
     rng = np.random.default_rng(1)
     W = gaussian_q4k(rng, 3584, 1024)
     X = rng.standard_normal((1, 1024)).astype(np.float32)
@@ -104,12 +104,12 @@ def test_q4k_config1_matvec(dev):
 
 
 @pytest.mark.parametrize("layer", ["deltanet", "fullattn"])
-def test_q4k_config2_verify_layer(dev, layer):
+def test_q4k_verify_layer_5_rows(dev, layer):
     """Every matrix of one decoder layer against k+1 = 5 activation rows."""
     mats = DELTANET_LAYER if layer == "deltanet" else FULLATTN_LAYER
     rng = np.random.default_rng(2)
     for name, rows, cols in mats:
-        print(f"[case] config2 {layer}.{name} {rows}x{cols} n=5", flush=True)
+        print(f"[case] verify layer {layer}.{name} {rows}x{cols} n=5", flush=True)
         W = gaussian_q4k(rng, rows, cols)
         X = rng.standard_normal((5, cols)).astype(np.float32)
         check_case(dev, W, rows, cols, X)
