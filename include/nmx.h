@@ -165,6 +165,12 @@ int nmx_rmsnorm(nmx_ctx *ctx, float *x, int x_stride, const float *add, int add_
 int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add, int add_stride,
                    float *xo, int xo_stride, const float *w, int n, int cols, float eps, float *y,
                    int y_stride, nmx_a8 a8);
+/* Two independent nmx_rmsnorm calls of n rows each (no residual), in one launch when
+ * cols <= 1024 and the rows are 16-byte aligned (else two launches): the MTP head's fc input
+ * [norm_e(embed(tok)) | norm_h(h)] (engine/src/mtp.c:60-75). Returns 0 or -1. */
+int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
+                     const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,
+                     int x1_stride, const float *w1, float *y1, int y1_stride, nmx_a8 a1);
 
 /* Gated DeltaNet pre (engine/src/forward_lin.c:36-67): causal conv + SiLU per channel with the
  * conv state, q/k L2 norm (+ q scale), beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)).
@@ -292,6 +298,7 @@ typedef struct {
     float *pend;           /* [layers][cap][row] */
     int cap, row;
     int32_t *ctl;
+    int32_t *vt;           /* optional: also vt[0] = vt[ctl[1]], as nmx_copy_token */
 } nmx_commit_args;
 int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p);
 

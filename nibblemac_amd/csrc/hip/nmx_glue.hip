@@ -196,17 +196,15 @@ __device__ __forceinline__ void a8_block4(float4 x, int b, int v, int n, int8_t 
     }
 }
 
+/* One row of rmsnorm4_k (row of the workgroup; sq / red its LDS). */
 template <int P4>
-__global__ __launch_bounds__(256) void rmsnorm4_k(const float *x, int x_stride,
-                                                  const float *add, int add_stride,
-                                                  float *xo, int xo_stride,
-                                                  const float *__restrict__ w, int cols, float eps,
-                                                  float *__restrict__ y, int y_stride,
-                                                  int8_t *__restrict__ q, float *__restrict__ d,
-                                                  float *__restrict__ fs, int n) {
-    extern __shared__ float sq[]; /* chain-major squares */
-    __shared__ float red[8];
-    const int row = blockIdx.x, tid = threadIdx.x;
+__device__ __forceinline__ void rms4_row(const float *x, int x_stride, const float *add,
+                                         int add_stride, float *xo, int xo_stride,
+                                         const float *__restrict__ w, int cols, float eps,
+                                         float *__restrict__ y, int y_stride, int8_t *__restrict__ q,
+                                         float *__restrict__ d, float *__restrict__ fs, int n,
+                                         int row, float *sq, float *red) {
+    const int tid = threadIdx.x;
     const int c4 = cols >> 2, s4 = cm_stride(cols);
     const float4 *xr = (const float4 *)(x + (size_t)row * x_stride);
     float4 v[P4], wv[P4];
@@ -247,6 +245,41 @@ __global__ __launch_bounds__(256) void rmsnorm4_k(const float *x, int x_stride,
         if (y) ((float4 *)(y + (size_t)row * y_stride))[j] = o;
         if (q) a8_block4(o, j >> 3, row, n, q, d, fs);
     }
+}
+
+template <int P4>
+__global__ __launch_bounds__(256) void rmsnorm4_k(const float *x, int x_stride,
+                                                  const float *add, int add_stride,
+                                                  float *xo, int xo_stride,
+                                                  const float *__restrict__ w, int cols, float eps,
+                                                  float *__restrict__ y, int y_stride,
+                                                  int8_t *__restrict__ q, float *__restrict__ d,
+                                                  float *__restrict__ fs, int n) {
+    extern __shared__ float sq[]; /* chain-major squares */
+    __shared__ float red[8];
+    rms4_row<P4>(x, x_stride, add, add_stride, xo, xo_stride, w, cols, eps, y, y_stride, q, d, fs,
+                 n, blockIdx.x, sq, red);
+}
+
+/* Two independent norms of n rows each in one launch (blockIdx.y picks the set). */
+struct RmsSet {
+    const float *x;
+    int x_stride;
+    const float *w;
+    float *y;
+    int y_stride;
+    int8_t *q;
+    float *d, *fs;
+};
+
+template <int P4>
+__global__ __launch_bounds__(256) void rmsnorm4_pair_k(RmsSet s0, RmsSet s1, int cols, float eps,
+                                                       int n) {
+    extern __shared__ float sq[];
+    __shared__ float red[8];
+    const RmsSet &s = blockIdx.y ? s1 : s0;
+    rms4_row<P4>(s.x, s.x_stride, nullptr, 0, nullptr, 0, s.w, cols, eps, s.y, s.y_stride, s.q,
+                 s.d, s.fs, n, blockIdx.x, sq, red);
 }
 
 /* ---- Gated DeltaNet pre (engine/src/forward_lin.c:36-67): per channel the causal conv over
@@ -951,6 +984,7 @@ struct Commit {
     float *pend;                 /* [layers][cap][row] */
     int cap, row;                /* rows per log, floats per log row (heads (dk + dv + 1)) */
     int32_t *ctl;
+    int32_t *vt;                 /* optional: vt[0] = vt[ctl[1]] */
 };
 
 __global__ __launch_bounds__(256) void commit_k(Commit a) {
@@ -974,7 +1008,10 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
     const float *lg = a.log + (size_t)l * a.cap * a.row;
     float *pd = a.pend + (size_t)l * a.cap * a.row;
     for (int i = tid; i < E * a.row; i += stride) pd[i] = lg[a.row + i];
-    if (l == 0 && tid == 0) a.ctl[2] = E;
+    if (l == 0 && tid == 0) {
+        a.ctl[2] = E;
+        if (a.vt) a.vt[0] = a.vt[E + 1]; /* cur <- vt[e] */
+    }
 }
 
 /* a = out[0], g = out[1] of nmx_head_accept: vt[a + 1] = g; ctl[1] = e = a + 1. */
@@ -1058,6 +1095,30 @@ int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
     else NMX_RMS(64);
 #undef NMX_RMS
     NMX_LAUNCHED(ctx, "rmsnorm");
+    return 0;
+}
+
+int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
+                     const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,
+                     int x1_stride, const float *w1, float *y1, int y1_stride, nmx_a8 a1) {
+    if (!ctx) return -1;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool fast = cols % 32 == 0 && cols <= 1024 && x0 && x1 && w0 && w1 && al16(x0) &&
+                      al16(x1) && al16(w0) && al16(w1) && x0_stride % 4 == 0 && x1_stride % 4 == 0 &&
+                      (!y0 || (al16(y0) && y0_stride % 4 == 0 && y0_stride >= cols)) &&
+                      (!y1 || (al16(y1) && y1_stride % 4 == 0 && y1_stride >= cols)) &&
+                      x0_stride >= cols && x1_stride >= cols && n >= 1 && n <= 4096 &&
+                      (!a0.q || (a0.d && a0.fs)) && (!a1.q || (a1.d && a1.fs));
+    if (!fast) /* the general kernel, one launch per set */
+        return nmx_rmsnorm_xo(ctx, x0, x0_stride, nullptr, 0, nullptr, 0, w0, n, cols, eps, y0,
+                              y0_stride, a0) ||
+               nmx_rmsnorm_xo(ctx, x1, x1_stride, nullptr, 0, nullptr, 0, w1, n, cols, eps, y1,
+                              y1_stride, a1);
+    const RmsSet s0{x0, x0_stride, w0, y0, y0_stride, a0.q, a0.d, a0.fs};
+    const RmsSet s1{x1, x1_stride, w1, y1, y1_stride, a1.q, a1.d, a1.fs};
+    const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
+    rmsnorm4_pair_k<1><<<dim3((unsigned)n, 2), 256, lds, ctx->stream>>>(s0, s1, cols, eps, n);
+    NMX_LAUNCHED(ctx, "rmsnorm_pair");
     return 0;
 }
 
@@ -1210,7 +1271,7 @@ int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p) {
         p->row < 1 || !p->state || !p->xin || !p->log || !p->pend || !p->ctl)
         return nmx_fail(ctx, "nmx_lin_commit: bad arguments");
     Commit a{p->layers, p->C, p->conv_k - 1, p->state, p->xin, p->log, p->pend, p->cap, p->row,
-             p->ctl};
+             p->ctl, p->vt};
     dim3 grid((unsigned)((p->C + 255) / 256), (unsigned)p->layers);
     commit_k<<<grid, 256, 0, ctx->stream>>>(a);
     NMX_LAUNCHED(ctx, "lin_commit");

@@ -187,9 +187,8 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
      * [block][n][32] layout); a block never straddles the halves (H % 32 == 0) */
     const size_t hb = (size_t)(H / 32) * n;
     const nmx_a8 a8_emb = s->a_w, a8_hid = {s->a_w.q + hb * 32, s->a_w.d + hb, s->a_w.fs + hb};
-    CK(nmx_rmsnorm(D, s->emb, H, NULL, 0, c->mtp_norm_emb, n, H, c->rms_eps, s->cat, 2 * H, a8_emb));
-    CK(nmx_rmsnorm(D, (float *)h_dev, H, NULL, 0, c->mtp_norm_hid, n, H, c->rms_eps, s->cat + H,
-                   2 * H, a8_hid));
+    CK(nmx_rmsnorm_pair(D, n, H, c->rms_eps, s->emb, H, c->mtp_norm_emb, s->cat, 2 * H, a8_emb,
+                        h_dev, H, c->mtp_norm_hid, s->cat + H, 2 * H, a8_hid));
     e_resid r = {s->x, s->x2, NULL};
     CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H, NULL));
     const e_layer *L = &c->mtp;

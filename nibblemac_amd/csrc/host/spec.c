@@ -72,11 +72,18 @@ static int seq_verify(pinfer_ctx *c, int ke, int nv) {
 }
 
 /* Commit e = ctl[1] tokens and run the MTP head over them (engine/src/spec.c:346-365). */
-static int seq_commit(pinfer_ctx *c, int ke, int nv) {
-    CK(nmx_copy_token(c->dev, c->vt, c->ctl)); /* cur <- vt[e] */
+/* The rollback commit of every linear layer, which also sets cur <- vt[e] (a kernel of its
+ * own without linear layers). */
+static int commit_lin_cur(pinfer_ctx *c) {
     nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
-                         c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl};
+                         c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl, c->vt};
     if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
+    else CK(nmx_copy_token(c->dev, c->vt, c->ctl));
+    return PINFER_OK;
+}
+
+static int seq_commit(pinfer_ctx *c, int ke, int nv) {
+    TRY(commit_lin_cur(c));
     /* the MTP pass reads the final-normed rows before it writes s.xn itself */
     TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c),
                       c->gate_on ? c->gate : NULL));
@@ -98,10 +105,7 @@ static int seq_verify_ng(pinfer_ctx *c, int ke) {
 /* The n-gram round's commit: cur <- vt[e], the rollback commit, n_past += e. The committed
  * rows stay in s.xn for the host to queue for the MTP pass. */
 static int seq_commit_ng(pinfer_ctx *c) {
-    CK(nmx_copy_token(c->dev, c->vt, c->ctl));
-    nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
-                         c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl};
-    if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
+    TRY(commit_lin_cur(c));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
 }
