@@ -171,6 +171,15 @@ int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
 int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
                      const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,
                      int x1_stride, const float *w1, float *y1, int y1_stride, nmx_a8 a1);
+/* The embedding rows tok[0..n) of the Q4K matrix E (nmx_embed_q4k), written to xo0 when not
+ * NULL, RMS-normalised with w0 into y0 / a0 as nmx_rmsnorm, and, when x1 is not NULL, a second
+ * norm as in nmx_rmsnorm_pair, in one launch when cols <= 1024 and the rows are 16-byte
+ * aligned: the first layer's input norm (engine/src/forward.c:92-100) and the MTP head's fc
+ * input (engine/src/mtp.c:60-75). Returns 0 or -1. */
+int nmx_embed_norm(nmx_ctx *ctx, const void *E, int vocab, const int32_t *tok, int n, int cols,
+                   float eps, const float *w0, float *xo0, int xo0_stride, float *y0, int y0_stride,
+                   nmx_a8 a0, const float *x1, int x1_stride, const float *w1, float *y1,
+                   int y1_stride, nmx_a8 a1);
 
 /* Gated DeltaNet pre (engine/src/forward_lin.c:36-67): causal conv + SiLU per channel with the
  * conv state, q/k L2 norm (+ q scale), beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)).

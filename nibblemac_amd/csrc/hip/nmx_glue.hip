@@ -197,22 +197,47 @@ __device__ __forceinline__ void a8_block4(float4 x, int b, int v, int n, int8_t 
 }
 
 /* One row of rmsnorm4_k (row of the workgroup; sq / red its LDS). */
+/* Columns 4 j .. 4 j + 3 of Q4K row `row` (cols columns), as embed_k computes them. */
+__device__ __forceinline__ float4 embed4(const uint8_t *E, int row, int cols, int j) {
+    const int c = 4 * j, sb = c >> 8, k = (c & 255) >> 5, jj = c & 31, i = row & 3;
+    const uint8_t *p = E + ((size_t)(row >> 2) * (cols >> 8) + sb) * 576;
+    const float D = nmx_half(p + 2 * i), M = nmx_half(p + 8 + 2 * i);
+    const float dd = D * (float)nmx_get6(p + 16, 4 * k + i);
+    const float mm = M * (float)nmx_get6(p + 40, 4 * k + i);
+    const uint32_t b4 = *(const uint32_t *)(p + 64 + 64 * k + 16 * i + (jj & 15));
+    const uint32_t u4 = jj < 16 ? (b4 & 0x0f0f0f0fu) : ((b4 >> 4) & 0x0f0f0f0fu);
+    return make_float4(dd * (float)(u4 & 0xffu) - mm, dd * (float)((u4 >> 8) & 0xffu) - mm,
+                       dd * (float)((u4 >> 16) & 0xffu) - mm, dd * (float)(u4 >> 24) - mm);
+}
+
+/* E (optional): row `row` is the Q4K embedding row tok[row] of E instead of x's row. */
 template <int P4>
 __device__ __forceinline__ void rms4_row(const float *x, int x_stride, const float *add,
                                          int add_stride, float *xo, int xo_stride,
                                          const float *__restrict__ w, int cols, float eps,
                                          float *__restrict__ y, int y_stride, int8_t *__restrict__ q,
                                          float *__restrict__ d, float *__restrict__ fs, int n,
-                                         int row, float *sq, float *red) {
+                                         int row, float *sq, float *red,
+                                         const uint8_t *E = nullptr, const int32_t *tok = nullptr) {
     const int tid = threadIdx.x;
     const int c4 = cols >> 2, s4 = cm_stride(cols);
-    const float4 *xr = (const float4 *)(x + (size_t)row * x_stride);
     float4 v[P4], wv[P4];
+    if (E) {
+        const int er = tok[row];
 #pragma unroll
-    for (int u = 0; u < P4; u++) { /* clamped (always in-bounds) loads */
-        const int j = tid + 256 * u, jc = j < c4 ? j : c4 - 1;
-        v[u] = xr[jc];
-        wv[u] = ((const float4 *)w)[jc];
+        for (int u = 0; u < P4; u++) {
+            const int j = tid + 256 * u, jc = j < c4 ? j : c4 - 1;
+            v[u] = embed4(E, er, cols, jc);
+            wv[u] = ((const float4 *)w)[jc];
+        }
+    } else {
+        const float4 *xr = (const float4 *)(x + (size_t)row * x_stride);
+#pragma unroll
+        for (int u = 0; u < P4; u++) { /* clamped (always in-bounds) loads */
+            const int j = tid + 256 * u, jc = j < c4 ? j : c4 - 1;
+            v[u] = xr[jc];
+            wv[u] = ((const float4 *)w)[jc];
+        }
     }
     if (add) {
         const float4 *ar = (const float4 *)(add + (size_t)row * add_stride);
@@ -270,6 +295,10 @@ struct RmsSet {
     int y_stride;
     int8_t *q;
     float *d, *fs;
+    const uint8_t *E;     /* optional: rows from the Q4K embedding E (rows tok[]) instead of x */
+    const int32_t *tok;
+    float *xo;            /* optional: the rows (as read or decoded) written here */
+    int xo_stride;
 };
 
 template <int P4>
@@ -278,8 +307,8 @@ __global__ __launch_bounds__(256) void rmsnorm4_pair_k(RmsSet s0, RmsSet s1, int
     extern __shared__ float sq[];
     __shared__ float red[8];
     const RmsSet &s = blockIdx.y ? s1 : s0;
-    rms4_row<P4>(s.x, s.x_stride, nullptr, 0, nullptr, 0, s.w, cols, eps, s.y, s.y_stride, s.q,
-                 s.d, s.fs, n, blockIdx.x, sq, red);
+    rms4_row<P4>(s.x, s.x_stride, nullptr, 0, s.xo, s.xo_stride, s.w, cols, eps, s.y, s.y_stride,
+                 s.q, s.d, s.fs, n, blockIdx.x, sq, red, s.E, s.tok);
 }
 
 /* ---- Gated DeltaNet pre (engine/src/forward_lin.c:36-67): per channel the causal conv over
@@ -1114,11 +1143,44 @@ int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, 
                               y0_stride, a0) ||
                nmx_rmsnorm_xo(ctx, x1, x1_stride, nullptr, 0, nullptr, 0, w1, n, cols, eps, y1,
                               y1_stride, a1);
-    const RmsSet s0{x0, x0_stride, w0, y0, y0_stride, a0.q, a0.d, a0.fs};
-    const RmsSet s1{x1, x1_stride, w1, y1, y1_stride, a1.q, a1.d, a1.fs};
+    const RmsSet s0{x0, x0_stride, w0, y0, y0_stride, a0.q, a0.d, a0.fs, nullptr, nullptr, nullptr, 0};
+    const RmsSet s1{x1, x1_stride, w1, y1, y1_stride, a1.q, a1.d, a1.fs, nullptr, nullptr, nullptr, 0};
     const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
     rmsnorm4_pair_k<1><<<dim3((unsigned)n, 2), 256, lds, ctx->stream>>>(s0, s1, cols, eps, n);
     NMX_LAUNCHED(ctx, "rmsnorm_pair");
+    return 0;
+}
+
+int nmx_embed_norm(nmx_ctx *ctx, const void *E, int vocab, const int32_t *tok, int n, int cols,
+                   float eps, const float *w0, float *xo0, int xo0_stride, float *y0, int y0_stride,
+                   nmx_a8 a0, const float *x1, int x1_stride, const float *w1, float *y1,
+                   int y1_stride, nmx_a8 a1) {
+    if (!ctx) return -1;
+    if (!E || !tok || !w0 || vocab <= 0 || vocab % 4 || cols % 256 || cols < 256 || n < 1 ||
+        n > 4096 || (xo0 && xo0_stride < cols) || (y0 && y0_stride < cols) ||
+        (x1 && (!w1 || x1_stride < cols || (y1 && y1_stride < cols))))
+        return nmx_fail(ctx, "nmx_embed_norm: bad arguments");
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool fast = cols <= 1024 && al16(w0) && (!xo0 || (al16(xo0) && xo0_stride % 4 == 0)) &&
+                      (!y0 || (al16(y0) && y0_stride % 4 == 0)) && (!a0.q || (a0.d && a0.fs)) &&
+                      (!x1 || (al16(x1) && al16(w1) && x1_stride % 4 == 0 &&
+                               (!y1 || (al16(y1) && y1_stride % 4 == 0)) && (!a1.q || (a1.d && a1.fs))));
+    if (!fast) { /* the embedding into xo0 (required then), then the norms */
+        if (!xo0) return nmx_fail(ctx, "nmx_embed_norm: unaligned rows need xo0");
+        if (nmx_embed_q4k(ctx, E, vocab, cols, tok, n, xo0, xo0_stride)) return -1;
+        if (nmx_rmsnorm_xo(ctx, xo0, xo0_stride, nullptr, 0, nullptr, 0, w0, n, cols, eps, y0,
+                           y0_stride, a0))
+            return -1;
+        return x1 ? nmx_rmsnorm_xo(ctx, x1, x1_stride, nullptr, 0, nullptr, 0, w1, n, cols, eps, y1,
+                                   y1_stride, a1)
+                  : 0;
+    }
+    const RmsSet s0{nullptr, 0, w0, y0, y0_stride, a0.q, a0.d, a0.fs,
+                    (const uint8_t *)E, tok, xo0, xo0_stride};
+    const RmsSet s1{x1, x1_stride, w1, y1, y1_stride, a1.q, a1.d, a1.fs, nullptr, nullptr, nullptr, 0};
+    const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
+    rmsnorm4_pair_k<1><<<dim3((unsigned)n, x1 ? 2 : 1), 256, lds, ctx->stream>>>(s0, s1, cols, eps, n);
+    NMX_LAUNCHED(ctx, "embed_norm");
     return 0;
 }
 

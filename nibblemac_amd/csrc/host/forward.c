@@ -128,10 +128,13 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
     e_scratch *s = &c->s;
     const int H = c->H;
     e_resid r = {s->x, s->x2, NULL};
-    CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, r.cur, H));
+    /* the embedding rows (the residual stream) and the first layer's input norm, one launch */
+    const nmx_a8 none = {NULL, NULL, NULL};
+    CK(nmx_embed_norm(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps, c->layers[0].in_norm,
+                      r.cur, H, NULL, 0, s->a_h, NULL, 0, NULL, NULL, 0, none));
     for (int l = 0; l < c->n_layers; l++) {
         const e_layer *L = &c->layers[l];
-        TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
+        if (l > 0) TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
         int rc = L->is_full ? attn_block(c, L, n, kv_of(c->kc, c, L->full),
                                          kv_of(c->vc, c, L->full), 0)
                             : lin_block(c, L, n, logged);
@@ -181,14 +184,15 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     e_scratch *s = &c->s;
     const int H = c->H;
     const nmx_a8 none = {NULL, NULL, NULL};
-    CK(nmx_embed_q4k(D, c->embed.w, c->vocab, H, tok_dev, n, s->emb, H));
-    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)]: each norm writes
-     * the A8 blocks of its half of the 2H row (blocks [0, H/32) and [H/32, 2H/32) of the
-     * [block][n][32] layout); a block never straddles the halves (H % 32 == 0) */
+    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)], the embedding and
+     * both norms in one launch: each norm writes the A8 blocks of its half of the 2H row
+     * (blocks [0, H/32) and [H/32, 2H/32) of the [block][n][32] layout); a block never
+     * straddles the halves (H % 32 == 0) */
     const size_t hb = (size_t)(H / 32) * n;
     const nmx_a8 a8_emb = s->a_w, a8_hid = {s->a_w.q + hb * 32, s->a_w.d + hb, s->a_w.fs + hb};
-    CK(nmx_rmsnorm_pair(D, n, H, c->rms_eps, s->emb, H, c->mtp_norm_emb, s->cat, 2 * H, a8_emb,
-                        h_dev, H, c->mtp_norm_hid, s->cat + H, 2 * H, a8_hid));
+    CK(nmx_embed_norm(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps, c->mtp_norm_emb, s->emb,
+                      H, s->cat, 2 * H, a8_emb, h_dev, H, c->mtp_norm_hid, s->cat + H, 2 * H,
+                      a8_hid));
     e_resid r = {s->x, s->x2, NULL};
     CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H, NULL));
     const e_layer *L = &c->mtp;
