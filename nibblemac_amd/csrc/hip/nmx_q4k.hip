@@ -375,6 +375,7 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
+            if (t0 + j >= n) break; /* uniform: only the pass's vectors */
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) {
                 const unsigned long long o = __shfl_xor(k[j], off);
