@@ -42,6 +42,33 @@ __device__ __forceinline__ int nmx_sum32(int v) {
     return v + nmx_swz16(v);
 }
 
+/* Maximum of a 64-bit unsigned key over the wave (every lane active), returned to every
+ * lane: DPP quad swaps and row mirrors within 16 lanes, a swizzle across the 16-lane rows
+ * of each half, then the two halves through readlane. No LDS permutes. */
+__device__ __forceinline__ void nmx_max_u64_step(uint32_t &lo, uint32_t &hi, uint32_t olo,
+                                                 uint32_t ohi) {
+    const bool take = ohi > hi || (ohi == hi && olo > lo);
+    lo = take ? olo : lo;
+    hi = take ? ohi : hi;
+}
+
+__device__ __forceinline__ unsigned long long nmx_max_u64_wave(unsigned long long key) {
+    uint32_t lo = (uint32_t)key, hi = (uint32_t)(key >> 32);
+#define NMX_MAX64_DPP(C)                                                                      \
+    nmx_max_u64_step(lo, hi, (uint32_t)nmx_dpp<C>((int)lo), (uint32_t)nmx_dpp<C>((int)hi))
+    NMX_MAX64_DPP(NMX_DPP_XOR1);
+    NMX_MAX64_DPP(NMX_DPP_XOR2);
+    NMX_MAX64_DPP(NMX_DPP_HALF_MIRROR);
+    NMX_MAX64_DPP(NMX_DPP_MIRROR);
+#undef NMX_MAX64_DPP
+    nmx_max_u64_step(lo, hi, (uint32_t)nmx_swz16((int)lo), (uint32_t)nmx_swz16((int)hi));
+    uint32_t lo0 = (uint32_t)__builtin_amdgcn_readlane((int)lo, 0);
+    uint32_t hi0 = (uint32_t)__builtin_amdgcn_readlane((int)hi, 0);
+    nmx_max_u64_step(lo0, hi0, (uint32_t)__builtin_amdgcn_readlane((int)lo, 32),
+                     (uint32_t)__builtin_amdgcn_readlane((int)hi, 32));
+    return ((unsigned long long)hi0 << 32) | lo0;
+}
+
 template <int DK4>
 __device__ __forceinline__ float nmx_quad_chain(const float (&p)[DK4]) {
     float carry = 0.0f;

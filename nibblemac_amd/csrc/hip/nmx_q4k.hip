@@ -19,6 +19,7 @@
  * Several matrices that share one input run in one launch (segment table). */
 #include "nmx_internal.h"
 #include "nmx_a8.h"
+#include "nmx_lanes.h"
 
 namespace {
 
@@ -170,12 +171,7 @@ __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, i
         const int wv = threadIdx.x >> 6;
 #pragma unroll
         for (int v = 0; v < NV; v++) {
-            unsigned long long key = valid ? argmax_key(acc[v], row) : 0ull;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const unsigned long long o = __shfl_xor(key, off);
-                key = o > key ? o : key;
-            }
+            const unsigned long long key = nmx_max_u64_wave(valid ? argmax_key(acc[v], row) : 0ull);
             if (lane == 0) wkeys[wv][v] = key;
         }
         __syncthreads();
@@ -332,12 +328,7 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
         const int wv = threadIdx.x >> 6;
 #pragma unroll
         for (int v = 0; v < NV; v++) {
-            unsigned long long key = valid ? argmax_key(acc[v], row) : 0ull;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const unsigned long long o = __shfl_xor(key, off);
-                key = o > key ? o : key;
-            }
+            const unsigned long long key = nmx_max_u64_wave(valid ? argmax_key(acc[v], row) : 0ull);
             if (lane == 0) wkeys[wv][v] = key;
         }
         __syncthreads();
@@ -376,11 +367,7 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (t0 + j >= n) break; /* uniform: only the pass's vectors */
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const unsigned long long o = __shfl_xor(k[j], off);
-                k[j] = o > k[j] ? o : k[j];
-            }
+            k[j] = nmx_max_u64_wave(k[j]);
             if (lane == 0) red[wv][j] = k[j];
         }
         __syncthreads();
