@@ -12,6 +12,7 @@
 #include "nmx_internal.h"
 #include "nmx_math.h"
 #include "nmx_a8.h"
+#include "nmx_lanes.h"
 
 namespace {
 
@@ -798,8 +799,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     __syncthreads();
     float mx = -INFINITY;
     for (int p = tid; p < np; p += 256) mx = fmaxf(mx, att[p]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = nmx_max_f32_wave(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -899,8 +899,7 @@ __global__ __launch_bounds__(256) void attn_pv_long_k(Attn a, const float *__res
 
     float mx = -INFINITY;
     for (int p = tid; p < np; p += 256) mx = fmaxf(mx, srow[p]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = nmx_max_f32_wave(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -961,8 +960,7 @@ __global__ __launch_bounds__(1024) void top1_gate_k(const float *__restrict__ l,
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     float mx = -INFINITY;
     for (int i = tid; i < n; i += 1024) mx = fmaxf(mx, l[i]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = nmx_max_f32_wave(mx);
     if (lane == 0) redf[w] = mx;
     __syncthreads();
     mx = redf[0];

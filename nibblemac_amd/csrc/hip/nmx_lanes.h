@@ -42,6 +42,14 @@ __device__ __forceinline__ int nmx_sum32(int v) {
     return v + nmx_swz16(v);
 }
 
+/* Maximum of a float over the wave (every lane active; exact in any order), returned to
+ * every lane: nmx_max32 within each half, then the halves through readlane. */
+__device__ __forceinline__ float nmx_max_f32_wave(float v) {
+    const float m = nmx_max32(v);
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
+}
+
 /* Maximum of a 64-bit unsigned key over the wave (every lane active), returned to every
  * lane: DPP quad swaps and row mirrors within 16 lanes, a swizzle across the 16-lane rows
  * of each half, then the two halves through readlane. No LDS permutes. */
