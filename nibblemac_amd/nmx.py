@@ -97,6 +97,8 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_accept_commit": (_i, [_vp, _vp, _vp, _vp]),
     "nmx_accept_commit_mb": (_i, [_vp, _vp, _vp, _vp, _vp, _i]),
     "nmx_host_alloc": (_vp, [_vp, _sz]),
+    "nmx_embed_norm": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _vp, _i, _vp, _i, A8,
+                            _vp, _i, _vp, _vp, _i, A8]),
     "nmx_host_free": (_i, [_vp, _vp]),
     "nmx_rmsnorm_xo": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _i,
                             A8]),
@@ -296,6 +298,16 @@ class Device:
         self.check(self.lib.nmx_rmsnorm_xo(self.ctx, _p(x), cols, _p(add), cols, _p(xo), cols,
                                            _p(w), n, cols, eps, _p(y), cols,
                                            A8(*[_p(t) for t in a8])), "rmsnorm")
+
+    def embed_norm(self, E, vocab: int, tok, n: int, cols: int, eps: float, w0, *, xo0=None,
+                   y0=None, a0=(None, None, None), x1=None, w1=None, y1=None,
+                   a1=(None, None, None)) -> None:
+        """nmx_embed_norm on contiguous rows: Q4K embedding rows tok -> xo0, norm -> y0 / a0,
+        and an optional second norm of x1 -> y1 / a1."""
+        self.check(self.lib.nmx_embed_norm(self.ctx, _p(E), vocab, _p(tok), n, cols, eps, _p(w0),
+                                           _p(xo0), cols, _p(y0), cols, A8(*[_p(t) for t in a0]),
+                                           _p(x1), cols, _p(w1), _p(y1), cols,
+                                           A8(*[_p(t) for t in a1])), "embed_norm")
 
     def silu_mul(self, gate, up, n: int, cols: int, y=None, a8=(None, None, None)) -> None:
         self.check(self.lib.nmx_silu_mul(self.ctx, _p(gate), _p(up), cols, n, cols, _p(y),

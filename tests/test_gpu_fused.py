@@ -159,3 +159,32 @@ def test_fused_invalid_calls_rejected(dev):
     out = a8_bufs(dev, 2, 32)
     with pytest.raises(NmxError):   # no input
         dev.q4k_swiglu(W, W, 32, 256, 2, out)
+
+
+@pytest.mark.parametrize("cols", [1024, 2048])
+@pytest.mark.parametrize("n", [1, 5])
+def test_embed_norm(dev, cols, n):
+    """nmx_embed_norm (the embedding decoded inside the first norm, with a second independent
+    norm in the same launch at cols <= 1024; embedding + two norms at 2048): the rows equal the
+    oracle's Q4K row dequantisation, both norms and their A8 the restated order and the oracle."""
+    print(f"[case] embed_norm cols={cols} n={n}", flush=True)
+    rng = np.random.default_rng(31 * cols + n)
+    vocab = 256
+    E = oracle.q4k_quantize((rng.standard_normal((vocab, cols)) * 0.02).astype(np.float32))
+    tok = rng.integers(0, vocab, n).astype(np.int32)
+    emb = np.stack([oracle.q4k_get_row(E, vocab, cols, int(t)) for t in tok])
+    x1 = rng.standard_normal((n, cols)).astype(np.float32)
+    w0, w1 = (rng.uniform(0.5, 1.5, cols).astype(np.float32) for _ in range(2))
+    dE, dtok, dx1 = dev.to_device(E), dev.to_device(tok), dev.to_device(x1)
+    dw0, dw1 = dev.to_device(w0), dev.to_device(w1)
+    xo0, y0, y1 = (dev.zeros((n, cols), np.float32) for _ in range(3))
+    a0, a1 = a8_bufs(dev, n, cols), a8_bufs(dev, n, cols)
+    dev.embed_norm(dE, vocab, dtok, n, cols, EPS, dw0, xo0=xo0, y0=y0, a0=a0, x1=dx1, w1=dw1,
+                   y1=y1, a1=a1)
+    dev.sync()
+    assert_bits_equal(xo0.numpy(), emb, "embedding rows")
+    for got_y, got_a, x, w, what in ((y0, a0, emb, w0, "set 0"), (y1, a1, x1, w1, "set 1")):
+        want = rmsnorm_restated(x, w, EPS)
+        assert_bits_equal(got_y.numpy(), want, f"{what} y")
+        for got, ref, part in zip(got_a, oracle.quant_a8(want), ("codes", "scales", "fsum")):
+            assert_bits_equal(got.numpy(), ref, f"{what} A8 {part}")
