@@ -168,6 +168,14 @@ int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
 /* Two independent nmx_rmsnorm calls of n rows each (no residual), in one launch when
  * cols <= 1024 and the rows are 16-byte aligned (else two launches): the MTP head's fc input
  * [norm_e(embed(tok)) | norm_h(h)] (engine/src/mtp.c:60-75). Returns 0 or -1. */
+/* nmx_rmsnorm of the single row *idx + off of x (+ add), the index read on the device and
+ * clamped to [0, nrows), into y [cols] and a one-vector A8 (either may be NULL; cols a multiple
+ * of 32, at most 1024; 16-byte aligned rows): the MTP head's final norm of the row whose draft
+ * is wanted (engine/src/mtp.c:88-100). */
+int nmx_rmsnorm_row(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
+                    int add_stride, const float *w, int cols, float eps, const int32_t *idx,
+                    int off, int nrows, float *y, nmx_a8 a8);
+
 int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
                      const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,
                      int x1_stride, const float *w1, float *y1, int y1_stride, nmx_a8 a1);

@@ -287,6 +287,25 @@ __global__ __launch_bounds__(256) void rmsnorm4_k(const float *x, int x_stride,
                  n, blockIdx.x, sq, red);
 }
 
+/* One row chosen on the device (row *idx + off of x, + add, clamped to [0, nrows)) into
+ * row 0 of y and of a one-vector A8 layout. */
+template <int P4>
+__global__ __launch_bounds__(256) void rmsnorm4_row_k(const float *x, int x_stride,
+                                                      const float *add, int add_stride,
+                                                      const float *__restrict__ w, int cols,
+                                                      float eps, const int32_t *idx, int off,
+                                                      int nrows, float *__restrict__ y,
+                                                      int8_t *__restrict__ q,
+                                                      float *__restrict__ d,
+                                                      float *__restrict__ fs) {
+    extern __shared__ float sq[];
+    __shared__ float red[8];
+    const int ri = *idx + off;
+    const size_t r = (size_t)(ri < 0 ? 0 : ri >= nrows ? nrows - 1 : ri);
+    rms4_row<P4>(x + r * x_stride, 0, add ? add + r * add_stride : nullptr, 0, nullptr, 0, w, cols,
+                 eps, y, 0, q, d, fs, 1, 0, sq, red);
+}
+
 /* Two independent norms of n rows each in one launch (blockIdx.y picks the set). */
 struct RmsSet {
     const float *x;
@@ -1146,6 +1165,22 @@ int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, 
     const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
     rmsnorm4_pair_k<1><<<dim3((unsigned)n, 2), 256, lds, ctx->stream>>>(s0, s1, cols, eps, n);
     NMX_LAUNCHED(ctx, "rmsnorm_pair");
+    return 0;
+}
+
+int nmx_rmsnorm_row(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
+                    int add_stride, const float *w, int cols, float eps, const int32_t *idx,
+                    int off, int nrows, float *y, nmx_a8 a8) {
+    if (!ctx) return -1;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (!x || !w || !idx || nrows < 1 || cols % 32 || cols < 32 || cols > 1024 || x_stride < cols ||
+        x_stride % 4 || !al16(x) || !al16(w) || (add && (add_stride < cols || add_stride % 4 ||
+        !al16(add))) || (y && !al16(y)) || (a8.q && (!a8.d || !a8.fs)))
+        return nmx_fail(ctx, "nmx_rmsnorm_row: bad arguments cols=%d", cols);
+    const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
+    rmsnorm4_row_k<1><<<1, 256, lds, ctx->stream>>>(x, x_stride, add, add_stride, w, cols, eps, idx,
+                                                    off, nrows, y, a8.q, a8.d, a8.fs);
+    NMX_LAUNCHED(ctx, "rmsnorm_row");
     return 0;
 }
 

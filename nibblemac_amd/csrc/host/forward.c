@@ -209,10 +209,19 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
         if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
         return PINFER_OK;
     }
-    CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H,
-                      none));
     const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
     const int off = head_row_dynamic ? -1 : n - 1;
+    if (H <= 1024 && H % 32 == 0 && (m_dst || draft_dst)) {
+        /* only the selected row: its MTP hidden and the head's A8 input, one launch */
+        CK(nmx_rmsnorm_row(D, r.cur, H, r.add, H, c->mtp_norm_out, H, c->rms_eps, idx, off, n,
+                           m_dst, draft_dst ? s->a_1 : none));
+        if (!draft_dst) return PINFER_OK;
+        TRY(head_a8(c, nv, draft_dst, gate_dst != NULL));
+        if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
+        return PINFER_OK;
+    }
+    CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H,
+                      none));
     if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));
     if (!draft_dst) return PINFER_OK;
     TRY(head_row(c, idx, off, nv, draft_dst, gate_dst != NULL));

@@ -100,6 +100,8 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_embed_norm": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _vp, _i, _vp, _i, A8,
                             _vp, _i, _vp, _vp, _i, A8]),
     "nmx_host_free": (_i, [_vp, _vp]),
+    "nmx_rmsnorm_row": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, ctypes.c_float, _vp, _i, _i, _vp,
+                             A8]),
     "nmx_rmsnorm_xo": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _i,
                             A8]),
     "nmx_silu_mul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, A8]),
@@ -298,6 +300,14 @@ class Device:
         self.check(self.lib.nmx_rmsnorm_xo(self.ctx, _p(x), cols, _p(add), cols, _p(xo), cols,
                                            _p(w), n, cols, eps, _p(y), cols,
                                            A8(*[_p(t) for t in a8])), "rmsnorm")
+
+    def rmsnorm_row(self, x, nrows: int, cols: int, w, eps: float, idx, off: int, *, add=None,
+                    y=None, a8=(None, None, None)) -> None:
+        """nmx_rmsnorm_row: the norm of row idx[0] + off (read on the device) of contiguous
+        rows [nrows][cols] (+ add) into y [cols] and a one-vector A8."""
+        self.check(self.lib.nmx_rmsnorm_row(self.ctx, _p(x), cols, _p(add), cols, _p(w), cols,
+                                            eps, _p(idx), off, nrows, _p(y),
+                                            A8(*[_p(t) for t in a8])), "rmsnorm_row")
 
     def embed_norm(self, E, vocab: int, tok, n: int, cols: int, eps: float, w0, *, xo0=None,
                    y0=None, a0=(None, None, None), x1=None, w1=None, y1=None,

@@ -188,3 +188,29 @@ def test_embed_norm(dev, cols, n):
         assert_bits_equal(got_y.numpy(), want, f"{what} y")
         for got, ref, part in zip(got_a, oracle.quant_a8(want), ("codes", "scales", "fsum")):
             assert_bits_equal(got.numpy(), ref, f"{what} A8 {part}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sel", [(0, 0), (4, -1), (2, 2), (9, -1)])
+def test_rmsnorm_row(dev, sel):
+    """nmx_rmsnorm_row (the MTP head's final norm of one device-selected row): y and the
+    one-vector A8 equal the restated norm of row idx + off of x + add and the oracle's A8 of it;
+    an index past the rows takes the last row."""
+    idx0, off = sel
+    n, cols = 5, 1024
+    print(f"[case] rmsnorm_row idx={idx0} off={off}", flush=True)
+    rng = np.random.default_rng(77 + idx0)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    add = rng.standard_normal((n, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    r = min(max(idx0 + off, 0), n - 1)
+    want = rmsnorm_restated((x[r] + add[r])[None, :], w, EPS)
+    dx, dadd, dw = dev.to_device(x), dev.to_device(add), dev.to_device(w)
+    didx = dev.to_device(np.array([idx0], np.int32))
+    y = dev.zeros((1, cols), np.float32)
+    a = a8_bufs(dev, 1, cols)
+    dev.rmsnorm_row(dx, n, cols, dw, EPS, didx, off, add=dadd, y=y, a8=a)
+    dev.sync()
+    assert_bits_equal(y.numpy(), want, "y")
+    for got, ref, part in zip(a, oracle.quant_a8(want), ("codes", "scales", "fsum")):
+        assert_bits_equal(got.numpy(), ref, f"A8 {part}")
