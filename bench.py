@@ -1,27 +1,29 @@
 #!/usr/bin/env python3
 """Benchmark of speculative greedy decoding (draft k = 4, verify + commit) on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--roofline-only]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-kernels]
+                    [--head-only [--eager] [--copy-mib M]]
 
-Workload: a 0.8B-shaped Qwen3.5 hybrid (24 layers: 18 Gated DeltaNet + 6 gated full attention,
-hidden 1024, FFN 3584, vocab 248320 with the Q4K embedding tied to the LM head, one MTP layer),
-random-init weights N(0, 0.02) packed as Q4K_G32 into a .pq file, loaded by libpinfer.so into
-HBM. One step is the reference CLI's benchmark (engine/tools/pinfer_run.c:384-430): prefill a
-512-token random prompt, then generate exactly 128 tokens with EOS ignored at k = 4 drafts per
-verification pass, drafts from the MTP head over the first 32768 ids. `value` is verified
-tokens per second of the decode: (128 - 1) per step / decode seconds, over K steps.
+Workload (config 5): a 0.8B-shaped Qwen3.5 hybrid (24 layers: 18 Gated DeltaNet + 6 gated full
+attention, hidden 1024, FFN 3584, vocab 248320 with the Q4K embedding tied to the LM head, one MTP
+layer), random-init weights N(0, 0.02) packed as Q4K_G32 into a .pq file, loaded by libpinfer.so
+into HBM. One step is the reference CLI's benchmark (engine/tools/pinfer_run.c:384-430): prefill
+a 512-token random prompt, then generate exactly 128 tokens with EOS ignored at k = 4 drafts per
+verification pass, drafts from the MTP head over the first 32768 ids. `value` is verified tokens
+per second of the decode: (128 - 1) per step / decode seconds, over K steps.
 
-`roofline` is the Q4K x A8 matvec kernel on the LM-head shape (248320 x 1024, 5 rows = k + 1,
-two copies rotating so the 143 MB head never sits in the 256 MB MALL), timed with HIP events on
-the stream it runs on. `cpu_baseline` is the reference engine's own sources with the oracle's
-threaded Q4K operators (oracle/_ref/libpinfer_refq4k.so) on the host cores, on a bounded sample
-of the same workload (shorter prompt and generation); its tokens are checked against the GPU's
-on the same sample.
+`roofline` is the LM head as the verify pass runs it (nmx_head_accept: the Q4K x A8 matvec
+248320 x 1024 over k + 1 = 5 rows with the fused argmax, then the acceptance), four rotating
+copies of the 143 MB head so no launch finds it in the 256 MB MALL, timed with HIP events on the
+stream it runs on. `kernels` holds configs 1-4 (nibblemac_amd/kbench.py). `cpu_baseline` is the
+reference engine's own sources with the oracle's threaded Q4K operators
+(oracle/_ref/libpinfer_refq4k.so) on the host cores: the config-5 workload itself on the GPU
+box's CPU share (16 threads), its tokens checked against the GPU's, plus a 1-thread run on a
+bounded sample and the oracle's Q4K matvec of config 1 on 1 thread.
 """
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import sys
@@ -34,16 +36,17 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from nibblemac_amd import pqfile, pqtool  # noqa: E402
+from nibblemac_amd import kbench, pqfile, pqtool  # noqa: E402
 from nibblemac_amd.nmx import Device  # noqa: E402
-from nibblemac_amd.pinfer import Model, SpecParams, SpecStats, load_library  # noqa: E402
+from nibblemac_amd.pinfer import Model  # noqa: E402
 from nibblemac_amd.synth import QWEN35_08B  # noqa: E402
 
 METRIC = "verified tok/s at draft k=4 (0.8B-shape Q4K); Q4K matvec GB/s vs HBM peak"
 HBM_PEAK_GBS = 8000.0
 K_DRAFT, DRAFT_VOCAB = 4, 32768
 N_PROMPT, N_GEN = 512, 128
-CPU_PROMPT, CPU_GEN = 32, 17
+CPU_SHARE = 16                       # host threads of one GPU's share of the box
+ONE_PROMPT, ONE_GEN = 16, 5          # the bounded 1-thread sample
 TRAFFIC_FILE = ROOT / "profiles" / "q4k_head_n5_traffic.json"
 
 
@@ -51,28 +54,17 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def host_threads() -> int:
-    return max(1, min(16, len(os.sched_getaffinity(0))))
+def host_threads() -> tuple[int, int]:
+    """(threads used, CPUs in this process's affinity mask)."""
+    aff = len(os.sched_getaffinity(0))
+    return max(1, min(CPU_SHARE, aff)), aff
 
 
-def time_graph(dev: Device, g, reps: int) -> float:
-    e0, e1 = dev.event(), dev.event()
-    dev.record(e0)
-    for _ in range(reps):
-        dev.graph_launch(g)
-    dev.record(e1)
-    return dev.elapsed_ms(e0, e1)
-
-
-def head_roofline(reps: int = 20, graphs: int = 5, eager: bool = False,
-                  copy_mib: int = 0) -> dict:
-    """The Q4K matvec of the LM head (248320 x 1024) over k + 1 = 5 A8 rows, logits written,
-    two rotating weight copies (cold), `reps` launches per graph, timed with HIP events on the
-    stream the kernels run on. eager: plain stream launches instead of graph replays (for
-    profiler counter runs); copy_mib: first copy that many MiB device to device (the plain copy
+def head_roofline(copies: int = 4, eager: bool = False, copy_mib: int = 0) -> dict:
+    """The in-path LM head (nmx_head_accept at 5 rows, 4 drafts, no logits written) over
+    `copies` rotating head copies, timed with HIP events over graph replays (eager: stream
+    launches, for profiler counter runs; copy_mib: a plain device copy of that many MiB first,
     whose counters scale the HBM traffic readings)."""
-    s, n = QWEN35_08B, K_DRAFT + 1
-    thr = host_threads()
     with Device(0) as dev:
         if copy_mib:
             a = dev.zeros(copy_mib << 20, np.uint8)
@@ -80,108 +72,93 @@ def head_roofline(reps: int = 20, graphs: int = 5, eager: bool = False,
             dev.copy(b, a, copy_mib << 20)
             dev.sync()
             a.free(), b.free()
-        W = pqtool.gauss_q4k(7, 10_000, s.vocab, s.hidden, 0.02, thr)
-        heads = [dev.to_device(W), dev.to_device(W)]
-        X = dev.to_device(np.random.default_rng(7).standard_normal((n, s.hidden))
-                          .astype(np.float32))
-        q = dev.empty((s.hidden // 32, n, 32), np.int8)
-        d = dev.empty((s.hidden // 32, n), np.float32)
-        fs = dev.empty((s.hidden // 32, n), np.float32)
-        dev.quant_a8(X, n, s.hidden, q, d, fs)
-        logits = dev.empty((n, s.vocab), np.float32)
-
-        def launches():
-            for r in range(reps):
-                dev.q4k_matmul(heads[r % 2], s.vocab, s.hidden, n, q, d, fs, logits)
-
         if eager:
-            launches()
-            dev.sync()
-            e0, e1 = dev.event(), dev.event()
-            dev.record(e0)
-            for _ in range(graphs):
-                launches()
-            dev.record(e1)
-            ms = dev.elapsed_ms(e0, e1) / (reps * graphs)
-        else:
-            dev.graph_begin()
-            launches()
-            g = dev.graph_end()
-            dev.graph_launch(g)
-            dev.sync()
-            ms = time_graph(dev, g, graphs) / (reps * graphs)
-        dev.sync()
-    wbytes = s.vocab // 4 * (s.hidden // 256) * 576
-    algo = wbytes + n * s.hidden + 2 * 4 * n * (s.hidden // 32) + 4 * n * s.vocab
-    achieved = algo / (ms * 1e-3) / 1e9
+            return head_eager(dev, copies)
+        r = kbench.config4_head(dev, copies=copies)
+    line = r["accept0of4"]
     traffic = None
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "q4k_mvx_k<5,false> (LM head 248320x1024 Q4K x 5 A8 rows, block dots on the matrix cores, cold)",
-            "us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": algo,
-            "timing": "eager stream launches" if eager else "graph replays"}
+    gbs = line["GB_s"]
+    return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": "q4k_mvx_k<5,true> + head_finish_k (LM head 248320x1024 Q4K x 5 A8 rows, "
+                      "fused argmax + acceptance, as the verify pass runs it; cold)",
+            "us_per_launch": line["us"], "algorithmic_bytes": r["algorithmic_bytes"],
+            "copies": copies, "timing": "graph replays, HIP events on the kernels' stream",
+            "accept_sweep_us": {k: v["us"] for k, v in r.items() if k.startswith("accept")}}
 
 
-class PfStop(ctypes.Structure):
-    """The reference's stop conditions (engine/src/spec.h:89-96)."""
-    _fields_ = [("eos", ctypes.c_int), ("stop_ids", ctypes.c_void_p), ("n_stop", ctypes.c_int),
-                ("on_token", ctypes.c_void_p), ("user", ctypes.c_void_p)]
+def head_eager(dev: Device, copies: int, reps: int = 40) -> dict:
+    """Eager launches of the in-path head (for rocprofv3 counter runs)."""
+    s, n = QWEN35_08B, K_DRAFT + 1
+    W = pqtool.gauss_q4k(7, 10_000, s.vocab, s.hidden, 0.02)
+    heads = [dev.to_device(W) for _ in range(copies)]
+    X = dev.to_device(np.random.default_rng(4).standard_normal((n, s.hidden)).astype(np.float32))
+    q = dev.empty((s.hidden // 32, n, 32), np.int8)
+    d = dev.empty((s.hidden // 32, n), np.float32)
+    fs = dev.empty((s.hidden // 32, n), np.float32)
+    dev.quant_a8(X, n, s.hidden, q, d, fs)
+    work = dev.alloc(dev.head_work_bytes(s.vocab, n))
+    out, drafts = dev.zeros(66, np.int32), dev.zeros(n - 1, np.int32)
+    e0, e1 = dev.event(), dev.event()
+    dev.record(e0)
+    for r in range(reps):
+        dev.head_accept(heads[r % copies], s.vocab, s.hidden, n, q, d, fs, None, drafts, work, out)
+    dev.record(e1)
+    dev.sync()
+    return {"us_per_call": round(dev.elapsed_ms(e0, e1) / reps * 1e3, 2), "timing": "eager"}
 
 
-def ref_bench_generate(path: Path, prompt: np.ndarray, n_gen: int, threads: int):
-    """The reference engine's benchmark sequence (pinfer_run.c:384-397): pf_spec_prefill, then
-    pf_spec_decode with EOS disabled; returns (tokens, stats, prefill s, decode s)."""
-    import oracle  # the reference build lives with the checker
+def cpu_baseline(path: Path, gpu_run: tuple, prompt: np.ndarray) -> dict:
+    """The reference engine on the host: the config-5 workload on CPU_SHARE threads (tokens and
+    statistics checked against the GPU's), a 1-thread run of a bounded sample, and the
+    oracle's config-1 matvec on 1 thread."""
+    from oracle import refengine  # the checker and CPU baseline live with the oracle
 
-    lib = load_library(str(oracle.HERE / "_ref" / "libpinfer_refq4k.so"))
-    cd = lib.cdll
-    cd.pf_spec_prefill.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
-                                   ctypes.c_void_p, ctypes.c_int]
-    cd.pf_spec_decode.argtypes = [ctypes.c_void_p] * 8
-    p = lib.pinfer_default_params()
-    p.max_ctx, p.n_threads = 1024, threads
-    err = ctypes.c_int(0)
-    ctx = lib.pinfer_load(str(path).encode(), ctypes.byref(p), ctypes.byref(err))
-    if not ctx:
-        raise RuntimeError(f"reference pinfer_load failed: {err.value}")
-    try:
-        prompt = np.ascontiguousarray(prompt, np.int32)
-        out = np.zeros(n_gen, np.int32)
-        sp, st = SpecParams(K_DRAFT, DRAFT_VOCAB, 0, 0), SpecStats()
-        stop, status = PfStop(-1, None, 0, None, None), ctypes.c_int(0)
-        t0 = time.perf_counter()
-        rc = cd.pf_spec_prefill(ctx, prompt.ctypes.data, prompt.size, ctypes.byref(sp), 0)
-        t1 = time.perf_counter()
-        if rc < 0:
-            raise RuntimeError(f"reference prefill failed: {rc}")
-        n = cd.pf_spec_decode(ctx, out.ctypes.data, n_gen, ctypes.byref(sp), ctypes.byref(stop),
-                              ctypes.byref(st), None, ctypes.byref(status))
-        t2 = time.perf_counter()
-        if n != n_gen or status.value != 0:
-            raise RuntimeError(f"reference decode failed: {n} tokens, status {status.value}")
-        return [int(x) for x in out], st, t1 - t0, t2 - t1
-    finally:
-        lib.pinfer_free(ctx)
-
-
-def cpu_baseline(path: Path, gpu: Model, prompt: np.ndarray) -> dict:
-    thr = host_threads()
-    sample = prompt[:CPU_PROMPT]
-    toks, st, tp, td = ref_bench_generate(path, sample, CPU_GEN, thr)
-    gtoks, gst, _, _ = gpu.bench_generate(sample, CPU_GEN, K_DRAFT, DRAFT_VOCAB)
-    match = toks == gtoks and (st.rounds, st.drafted, st.accepted) == \
+    thr, aff = host_threads()
+    full = refengine.bench_generate(path, prompt, N_GEN, K_DRAFT, DRAFT_VOCAB, thr)
+    gtoks, gst = gpu_run
+    match = full.tokens == gtoks and (full.rounds, full.drafted, full.accepted) == \
         (gst.rounds, gst.drafted, gst.accepted)
-    log(f"cpu reference: prefill {CPU_PROMPT} tok {tp:.2f} s, decode {CPU_GEN} tok {td:.2f} s "
-        f"({(CPU_GEN - 1) / td:.3f} tok/s), GPU tokens match: {match}")
+    log(f"cpu reference ({thr} threads): prefill {N_PROMPT} tok {full.prefill_s:.2f} s, decode "
+        f"{N_GEN} tok {full.decode_s:.2f} s ({(N_GEN - 1) / full.decode_s:.3f} tok/s), GPU "
+        f"tokens match: {match}")
     if not match:
-        raise SystemExit("bench.py: GPU tokens differ from the reference engine on the sample")
-    return {"value": round((CPU_GEN - 1) / td, 4), "unit": "tok/s", "cores": thr,
-            "kind": "reference", "tokens_match_gpu": match,
-            "sample": f"reference engine sources + oracle Q4K operators on {thr} threads: "
-                      f"prefill {CPU_PROMPT} random ids, then {CPU_GEN} tokens at k={K_DRAFT} "
-                      f"(draft vocab {DRAFT_VOCAB}, EOS ignored), decode timed"}
+        raise SystemExit("bench.py: GPU tokens differ from the reference engine")
+    one = refengine.bench_generate(path, prompt[:ONE_PROMPT], ONE_GEN, K_DRAFT, DRAFT_VOCAB, 1)
+    log(f"cpu reference (1 thread): prefill {ONE_PROMPT} tok {one.prefill_s:.2f} s, decode "
+        f"{ONE_GEN} tok {one.decode_s:.2f} s ({(ONE_GEN - 1) / one.decode_s:.4f} tok/s)")
+    mv = cpu_matvec_1t()
+    log(f"cpu oracle Q4K matvec 3584x1024 n=1, 1 thread: {mv['us']:.0f} us, {mv['GB_s']} GB/s")
+    return {"value": round((N_GEN - 1) / full.decode_s, 4), "unit": "tok/s", "cores": thr,
+            "kind": "reference", "tokens_match_gpu": match, "affinity_cpus": aff,
+            "prefill_tok_s": round(N_PROMPT / full.prefill_s, 2),
+            "sample": f"the config-5 workload itself: reference engine sources (Q4K operators from "
+                      f"the oracle's scalar C restatement; the reference's Q4K kernels are "
+                      f"NEON-only) on {thr} threads (this GPU's share of the host; {aff} CPUs in "
+                      f"the affinity mask): prefill {N_PROMPT} random ids, then {N_GEN} tokens at "
+                      f"k={K_DRAFT}, draft vocab {DRAFT_VOCAB}, EOS ignored; decode timed",
+            "one_thread": {"value": round((ONE_GEN - 1) / one.decode_s, 4), "unit": "tok/s",
+                           "sample": f"prefill {ONE_PROMPT} ids, then {ONE_GEN} tokens at k={K_DRAFT}"},
+            "matvec_config1_1t": mv}
+
+
+def cpu_matvec_1t(reps: int = 20) -> dict:
+    """The oracle's scalar Q4K x A8 matvec of config 1 (3584 x 1024, n = 1) on 1 thread."""
+    import oracle
+
+    rows, cols = 3584, 1024
+    W = pqtool.gauss_q4k(1, 0, rows, cols, 0.02)
+    q, d, fs = oracle.quant_a8(np.random.default_rng(1).standard_normal((1, cols)).astype(np.float32))
+    oracle.q4k_matmul(W, rows, cols, q, d, fs, 1)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.q4k_matmul(W, rows, cols, q, d, fs, 1)
+    us = (time.perf_counter() - t0) / reps * 1e6
+    algo = kbench.matvec_algo_bytes(rows, cols, 1)
+    return {"us": round(us, 1), "GB_s": round(algo / (us * 1e-6) / 1e9, 3), "cores": 1,
+            "kind": "port", "algorithmic_bytes": algo}
 
 
 def main() -> int:
@@ -190,21 +167,28 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--roofline-only", action="store_true",
-                    help="only the LM-head matvec launches (for counter runs)")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the config 1-4 lines")
+    ap.add_argument("--head-only", action="store_true",
+                    help="only the in-path LM head launches (for counter runs)")
+    ap.add_argument("--kernels-only", action="store_true", help="only the config 1-4 lines")
     ap.add_argument("--eager", action="store_true",
-                    help="with --roofline-only: stream launches instead of graph replays")
+                    help="with --head-only: stream launches instead of graph replays")
     ap.add_argument("--copy-mib", type=int, default=0,
-                    help="with --roofline-only: a device copy of this size first (counter scale)")
+                    help="with --head-only: a device copy of this size first (counter scale)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
               "(the multi-GPU sharding is a design, not a measured path)", file=sys.stderr)
         return 2
-    if a.roofline_only:
+    if a.head_only:
         roof = head_roofline(eager=a.eager, copy_mib=a.copy_mib)
-        log(f"head matvec: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+        log(f"head: {roof}")
         print(json.dumps({"roofline": roof}), flush=True)
+        return 0
+    if a.kernels_only:
+        with Device(0) as dev:
+            ks = kbench.run_all(dev)
+        print(json.dumps({"kernels": ks}), flush=True)
         return 0
     rng = np.random.default_rng(512)
     prompt = rng.integers(0, QWEN35_08B.vocab, N_PROMPT).astype(np.int32)
@@ -216,10 +200,10 @@ def main() -> int:
         with Model(str(path), max_ctx=1024) as gpu:
             for w in range(a.warmup):
                 gpu.bench_generate(prompt, N_GEN, K_DRAFT, DRAFT_VOCAB)
-            dec, pre, stats, first = 0.0, 0.0, [0, 0, 0], None
+            dec, pre, stats, first, first_st = 0.0, 0.0, [0, 0, 0], None, None
             for s in range(a.steps):
                 toks, st, tp, td = gpu.bench_generate(prompt, N_GEN, K_DRAFT, DRAFT_VOCAB)
-                first = first or toks
+                first, first_st = first or toks, first_st or st
                 if toks != first:
                     raise SystemExit("bench.py: generations differ between steps")
                 dec, pre = dec + td, pre + tp
@@ -227,9 +211,15 @@ def main() -> int:
                 log(f"step {s}: prefill {tp * 1e3:.1f} ms, decode {td * 1e3:.1f} ms, "
                     f"{(N_GEN - 1) / td:.1f} tok/s, rounds {st.rounds} accepted {st.accepted}")
             tps = a.steps * (N_GEN - 1) / dec
-            cpu = None if a.no_cpu else cpu_baseline(path, gpu, prompt)
+        cpu = None if a.no_cpu else cpu_baseline(path, (first, first_st), prompt)
     roof = head_roofline()
-    log(f"head matvec: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+    log(f"head (in path, cold): {roof['us_per_launch']} us, {roof['achieved']} GB/s")
+    kernels = None
+    if not a.no_kernels:
+        with Device(0) as dev:
+            kernels = kbench.run_all(dev)
+        for k, v in kernels.items():
+            log(f"{k}: {json.dumps(v)}")
     rounds = stats[0] / a.steps
     rec = {
         "metric": METRIC, "value": round(tps, 2), "unit": "tok/s", "n_gpus": 1,
@@ -247,7 +237,7 @@ def main() -> int:
                  "tokens_per_pass": round((N_GEN - 1) / rounds, 3) if rounds else None,
                  "ms_per_pass": round(dec / stats[0] * 1e3, 4) if stats[0] else None},
         "prefill_tok_s": round(a.steps * N_PROMPT / pre, 1),
-        "roofline": roof, "cpu_baseline": cpu,
+        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels,
     }
     print(json.dumps(rec), flush=True)
     return 0

@@ -36,8 +36,9 @@ enum {
 
 typedef struct pinfer_ctx pinfer_ctx;
 
-/* KV-cache storage formats. This engine stores fp32 (PINFER_KV_F32) only; the others are
- * refused with PINFER_E_ARG. */
+/* KV-cache storage formats (engine/include/pinfer.h:29-38): fp32 rows, binary16 rows (round
+ * to nearest even), or int8 rows with one fp32 scale per row. All three are supported; state
+ * blobs record the format and load only into a context of the same format. */
 enum {
     PINFER_KV_F32 = 0,
     PINFER_KV_F16 = 1,
@@ -47,7 +48,7 @@ enum {
 typedef struct {
     int n_threads;   /* host threads (unused by the device path; kept for the ABI) */
     int max_ctx;     /* tokens kept in the KV cache; <= 0 means 4096 */
-    int kv_dtype;    /* PINFER_KV_F32 */
+    int kv_dtype;    /* PINFER_KV_F32, PINFER_KV_F16 or PINFER_KV_I8 */
     float gpu_split; /* kept for the ABI; the whole model runs on the device */
 } pinfer_params;
 

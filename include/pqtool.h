@@ -1,5 +1,5 @@
-/* pqtool — .pq format tools exported by libpinfer.so next to the pinfer_* API: a seeded
- * Gaussian weight generator and the Q4K_G32 packer, used to build synthetic random-init models
+/* pqtool — .pq format tools in their own library, libpqtool.so (libpinfer.so exports the
+ * pinfer_* API only, like engine/pkg/pinfer.map:3-8): a seeded Gaussian weight generator and the Q4K_G32 packer, used to build synthetic random-init models
  * of the Qwen3.5 shapes (the role of the reference's tools/quant.py + tools/convert.py for a
  * checkpoint, and of engine/bench/kbench_util.c's kb_fill_matrix for benchmarks). */
 #ifndef PQTOOL_H

@@ -1,10 +1,11 @@
 """Build the native libraries of nibblemac_amd in-tree.
 
-    python -m nibblemac_amd.build          # libnmx.so (HIP, gfx950) + libpinfer.so (C11 host)
+    python -m nibblemac_amd.build          # libnmx.so (HIP, gfx950), libpinfer.so, libpqtool.so
 
 libnmx.so   hand-written HIP kernels for gfx950 behind the C ABI of include/nmx.h
 libpinfer.so the C11 host engine exporting the pinfer_* API of include/pinfer.h; it calls the
              device only through libnmx.so
+libpqtool.so seeded synthetic weights and the Q4K_G32 packer (include/pqtool.h), host only
 
 Both land in nibblemac_amd/lib/. Every call recompiles (sources are few and hipcc
 cross-compiles gfx950 without a GPU).
@@ -22,6 +23,7 @@ ROOT = PKG.parent
 INCLUDE = ROOT / "include"
 HIP_DIR = PKG / "csrc" / "hip"
 HOST_DIR = PKG / "csrc" / "host"
+TOOL_DIR = PKG / "csrc" / "tool"
 LIB_DIR = PKG / "lib"
 OBJ_DIR = PKG / "_build"
 
@@ -81,11 +83,22 @@ def build_pinfer() -> Path | None:
     return out
 
 
+def build_pqtool() -> Path:
+    """Compile csrc/tool/*.c (C11) into libpqtool.so (no device code)."""
+    LIB_DIR.mkdir(exist_ok=True)
+    out = LIB_DIR / "libpqtool.so"
+    tmp = out.with_suffix(".so.tmp")
+    _run([CC, *C_FLAGS, "-shared", *map(str, sorted(TOOL_DIR.glob("*.c"))), "-lm", "-o", str(tmp)])
+    tmp.replace(out)
+    return out
+
+
 def build_all() -> list[Path]:
     outs = [build_nmx()]
     p = build_pinfer()
     if p:
         outs.append(p)
+    outs.append(build_pqtool())
     return outs
 
 

@@ -101,7 +101,10 @@ void *nmx_host_alloc(nmx_ctx *ctx, size_t bytes) {
         return nullptr;
     }
     void *p = nullptr;
-    hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+    /* coherent (fine-grained) memory: a host thread may poll what a kernel writes with a
+     * system-scope release while the stream still runs; coarse-grained memory guarantees the
+     * visibility of device writes only after a synchronisation */
+    hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocCoherent);
     if (e != hipSuccess) {
         nmx_fail(ctx, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
         return nullptr;

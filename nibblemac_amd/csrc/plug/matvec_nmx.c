@@ -37,6 +37,7 @@
 typedef struct {
     const void *host;
     void *dev;
+    int rows; /* rows of the device copy */
 } plug_weight;
 
 struct pf_pool {
@@ -82,14 +83,28 @@ static size_t q4k_bytes(const pf_mat *W) {
     return (size_t)(W->rows / 4) * (size_t)(W->cols / PQ_SB_COLS) * pq_sb_bytes(PQ_Q4K_G32);
 }
 
-/* Device copy of W, uploaded on first use. */
+/* Device copy of W, uploaded on first use. The same host data may come with fewer rows (the
+ * MTP draft head passes the head's data with rows = draft vocabulary, engine/src/mtp.c:94-95):
+ * a copy serves every request of at most its rows, and a request of more rows replaces it. */
 static void *weights(pf_pool *p, const pf_mat *W) {
-    for (int i = p->n_w - 1; i >= 0; i--)
-        if (p->w[i].host == W->data) return p->w[i].dev;
+    int slot = -1;
+    for (int i = p->n_w - 1; i >= 0 && slot < 0; i--)
+        if (p->w[i].host == W->data) slot = i;
+    if (slot >= 0 && p->w[slot].rows >= W->rows) return p->w[slot].dev;
     if (W->dtype != PQ_Q4K_G32 || W->rows % 4 || W->cols % PQ_SB_COLS) {
         fprintf(stderr, "matvec_nmx: matrix %dx%d of dtype %u: only Q4K_G32 with rows %% 4 == 0 "
                 "and cols %% %d == 0 runs on the device\n", W->rows, W->cols, W->dtype, PQ_SB_COLS);
         abort();
+    }
+    if (slot >= 0) { /* more rows than the cached copy: upload the larger one in its place */
+        if (nmx_free(p->dev, p->w[slot].dev)) plug_die(p, "free weights");
+        const size_t bytes = q4k_bytes(W);
+        void *d = nmx_alloc(p->dev, bytes);
+        if (!d) plug_die(p, "weight allocation");
+        up(p, d, W->data, bytes);
+        p->w[slot].dev = d;
+        p->w[slot].rows = W->rows;
+        return d;
     }
     if (p->n_w == p->cap_w) {
         const int cap = p->cap_w ? 2 * p->cap_w : 256;
@@ -104,6 +119,7 @@ static void *weights(pf_pool *p, const pf_mat *W) {
     up(p, d, W->data, bytes);
     p->w[p->n_w].host = W->data;
     p->w[p->n_w].dev = d;
+    p->w[p->n_w].rows = W->rows;
     p->n_w++;
     return d;
 }

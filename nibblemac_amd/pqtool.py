@@ -1,4 +1,4 @@
-"""ctypes binding of the .pq tools in libpinfer.so (include/pqtool.h): seeded Gaussian weights
+"""ctypes binding of the .pq tools in libpqtool.so (include/pqtool.h): seeded Gaussian weights
 and the Q4K_G32 packer for synthetic random-init models."""
 from __future__ import annotations
 
@@ -8,7 +8,7 @@ from pathlib import Path
 
 import numpy as np
 
-LIB = Path(__file__).resolve().parent / "lib" / "libpinfer.so"
+LIB = Path(__file__).resolve().parent / "lib" / "libpqtool.so"
 _lib = None
 
 

@@ -294,6 +294,34 @@ def test_qwen35_08b_shape(tmp_path):
     gpu.close(), ref.close()
 
 
+@needs_ref
+def test_qwen35_08b_config5_workload(tmp_path):
+    """The end-to-end workload at its stated size: the 0.8B shape (seed 1), a 512-token random
+    prompt (eight 64-row prefill chunks), then exactly 128 tokens at k = 4 with draft vocabulary
+    32768 and EOS ignored (engine/tools/pinfer_run.c:384-430), on the GPU engine and on the
+    reference engine's sources (16 host threads). Tokens, (rounds, drafted, accepted) and the
+    state blob after the decode (every DeltaNet state after 127 rounds of deferred replays, the
+    KV caches of all 640 positions, the MTP rows) must be identical."""
+    from oracle import refengine
+
+    path = pqfile.write_model(tmp_path / "q08.pq", QWEN35_08B, seed=1)
+    prompt = np.random.default_rng(512).integers(0, QWEN35_08B.vocab, 512).astype(np.int32)
+    print("[case] 0.8B shape, prompt 512, 128 tokens, k=4: GPU", flush=True)
+    gpu = Model(str(path), max_ctx=1024)
+    toks, st, tp, td = gpu.bench_generate(prompt, 128, k=4, draft_vocab=32768)
+    blob = gpu.state_save()
+    gpu.close()
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    print(f"[case] 0.8B shape, prompt 512, 128 tokens, k=4: reference on {threads} threads",
+          flush=True)
+    ref = refengine.bench_generate(path, prompt, 128, 4, 32768, threads, max_ctx=1024,
+                                   want_state=True)
+    print(f"[case] reference prefill {ref.prefill_s:.1f} s, decode {ref.decode_s:.1f} s", flush=True)
+    assert toks == ref.tokens
+    assert (st.rounds, st.drafted, st.accepted) == (ref.rounds, ref.drafted, ref.accepted)
+    assert blob == ref.state, "state blobs differ after the config-5 decode"
+
+
 def test_invalid_arguments(models):
     gpu = Model(str(models["small"]), max_ctx=64)
     from nibblemac_amd.pinfer import PinferError

@@ -1,6 +1,6 @@
 """The C-ABI libraries load (no GPU needed) and export every function their headers declare;
-nothing else leaks from libpinfer.so (its version script exports pinfer_* / pqt_* only, like
-the reference's engine/pkg/pinfer.map:3-8)."""
+nothing else leaks from libpinfer.so (its version script exports pinfer_* only, like the
+reference's engine/pkg/pinfer.map:3-8); the synthetic-model tools live in libpqtool.so."""
 from __future__ import annotations
 
 import ctypes
@@ -27,7 +27,7 @@ def exported(lib: Path) -> set[str]:
 
 
 @pytest.mark.parametrize("lib,header,prefix", [("libnmx.so", "nmx.h", "nmx_"),
-                                               ("libpinfer.so", "pqtool.h", "pqt_"),
+                                               ("libpqtool.so", "pqtool.h", "pqt_"),
                                                ("libpinfer.so", "pinfer.h", "pinfer_")])
 def test_headers_fully_exported(lib, header, prefix):
     path = LIB / lib
@@ -41,4 +41,4 @@ def test_headers_fully_exported(lib, header, prefix):
 
 def test_pinfer_exports_only_its_prefixes():
     syms = exported(LIB / "libpinfer.so")
-    assert all(s.startswith(("pinfer_", "pqt_")) for s in syms), sorted(syms)[:20]
+    assert all(s.startswith("pinfer_") for s in syms), sorted(syms)[:20]
