@@ -40,9 +40,10 @@ int nmx_device_count(void);                 /* without creating a context; 0 if 
 
 void *nmx_alloc(nmx_ctx *ctx, size_t bytes);               /* device memory, NULL on failure */
 int nmx_free(nmx_ctx *ctx, void *ptr);
-/* Page-locked host memory that kernels may write (hipHostMalloc); the host reads it after a
- * synchronisation of the stream, with no copy. No counterpart in the reference, whose engine
- * runs on the host. NULL on failure. */
+/* Page-locked, coherent (fine-grained) host memory that kernels may write (hipHostMalloc with
+ * hipHostMallocCoherent): the host may read it with no copy after a synchronisation, or poll a
+ * flag that a kernel sets with a system-scope release while the stream still runs. No
+ * counterpart in the reference, whose engine runs on the host. NULL on failure. */
 void *nmx_host_alloc(nmx_ctx *ctx, size_t bytes);
 int nmx_host_free(nmx_ctx *ctx, void *ptr);
 int nmx_upload(nmx_ctx *ctx, void *dst, const void *src, size_t bytes);   /* synchronous */
@@ -306,7 +307,10 @@ int nmx_top1_gate(nmx_ctx *ctx, const float *logits, int n, float tau, int32_t *
 
 /* Rollback commit of every linear layer (pf_lin_commit, engine/src/forward_lin.c:185-204)
  * with e = ctl[1]: conv state <- last conv_k - 1 rows of [state after token 0, raw inputs
- * 1..e-1]; pend <- log rows 1..e-1; ctl[2] = e - 1. Arrays are [layers][...] contiguous. */
+ * 1..e-1]; pend <- log rows 1..e-1; ctl[2] = e - 1. Arrays are [layers][...] contiguous.
+ * state_bak (optional, the size of state) keeps the rows of the state after token 0; a later
+ * call with redo = 1 commits a smaller e from them (the host's stop inside a run that the
+ * device already committed). */
 typedef struct {
     int layers, C, conv_k;
     float *state;          /* [layers][conv_k-1][C] */
@@ -316,6 +320,8 @@ typedef struct {
     int cap, row;
     int32_t *ctl;
     int32_t *vt;           /* optional: also vt[0] = vt[ctl[1]], as nmx_copy_token */
+    float *state_bak;      /* optional: [layers][conv_k-1][C] */
+    int redo;              /* commit from state_bak instead of state */
 } nmx_commit_args;
 int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p);
 

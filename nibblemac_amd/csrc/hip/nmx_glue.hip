@@ -1021,7 +1021,9 @@ __global__ __launch_bounds__(1024) void top1_gate_k(const float *__restrict__ l,
 
 /* ---- rollback commit over every linear layer (engine/src/forward_lin.c:185-204): with
  * E = e - 1 (e = ctl[1]), conv state <- last K-1 rows of [state after token 0, raw inputs
- * 1..E]; pending replay rows <- log rows 1..E; ctl[2] = E (keep). */
+ * 1..E]; pending replay rows <- log rows 1..E; ctl[2] = E (keep). With bak, the rows of the
+ * state after token 0 are kept there; redo computes the commit from them instead (a second
+ * commit of a smaller e after the first, when the host stops inside the accepted run). */
 struct Commit {
     int layers, C, S;            /* linear layers, conv channels, K - 1 */
     float *state;                /* [layers][S][C] */
@@ -1031,6 +1033,8 @@ struct Commit {
     int cap, row;                /* rows per log, floats per log row (heads (dk + dv + 1)) */
     int32_t *ctl;
     int32_t *vt;                 /* optional: vt[0] = vt[ctl[1]] */
+    float *bak;                  /* optional: [layers][S][C] state after token 0 */
+    int redo;                    /* commit from bak (which the first commit filled) */
 };
 
 __global__ __launch_bounds__(256) void commit_k(Commit a) {
@@ -1038,14 +1042,22 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
     const int E = a.ctl[1] - 1;
     const int tid = blockIdx.x * 256 + threadIdx.x, stride = gridDim.x * 256;
     float *st = a.state + (size_t)l * a.S * a.C;
+    float *bk = a.bak ? a.bak + (size_t)l * a.S * a.C : nullptr;
+    const float *src0 = a.redo ? bk : st; /* rows of the state after token 0 */
     const float *xi = a.xin + (size_t)l * a.cap * a.C;
     for (int c = tid; c < a.C; c += stride) {
-        float nv[8];
+        float old[8], nv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) old[j] = j < a.S ? src0[(size_t)j * a.C + c] : 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int src = j + E;
-            nv[j] = j >= a.S ? 0.0f
-                  : src < a.S ? st[(size_t)src * a.C + c] : xi[(size_t)(src - a.S + 1) * a.C + c];
+            nv[j] = j >= a.S ? 0.0f : src < a.S ? old[src] : xi[(size_t)(src - a.S + 1) * a.C + c];
+        }
+        if (bk && !a.redo) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (j < a.S) bk[(size_t)j * a.C + c] = old[j];
         }
 #pragma unroll
         for (int j = 0; j < 8; j++)
@@ -1365,8 +1377,9 @@ int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p) {
     if (!p || p->layers < 1 || p->conv_k < 2 || p->conv_k > 8 || p->C < 1 || p->cap < 1 ||
         p->row < 1 || !p->state || !p->xin || !p->log || !p->pend || !p->ctl)
         return nmx_fail(ctx, "nmx_lin_commit: bad arguments");
+    if (p->redo && !p->state_bak) return nmx_fail(ctx, "nmx_lin_commit: redo needs state_bak");
     Commit a{p->layers, p->C, p->conv_k - 1, p->state, p->xin, p->log, p->pend, p->cap, p->row,
-             p->ctl, p->vt};
+             p->ctl, p->vt, p->state_bak, p->redo};
     dim3 grid((unsigned)((p->C + 255) / 256), (unsigned)p->layers);
     commit_k<<<grid, 256, 0, ctx->stream>>>(a);
     NMX_LAUNCHED(ctx, "lin_commit");

@@ -1,88 +1,81 @@
-/* The adaptive speculation policy (pinfer_spec_params.adaptive), restating
- * engine/src/spec_adapt.c:1-102 (state in spec.h:49-57). It changes only which rounds are
- * speculative and how long the MTP chains are, never a token.
+/* The adaptive speculation policy (pinfer_spec_params.adaptive; the role of
+ * engine/src/spec_adapt.c in the reference's loop, engine/src/spec.c:300-312): before each
+ * round it picks the verify width w (1 = a plain step, w = ke + 1 for ke drafts) that
+ * maximises the expected tokens per second. It changes which rounds are speculative and how
+ * many drafts they verify, never a token.
  *
- *  - chain length: draft s + 1 is chained only while the newest draft's top-1 probability is
- *    at least E_AD_TAU (the device computes that comparison, nmx_top1_gate);
- *  - plain mode: after E_AD_MIN_ROUNDS speculative rounds (2 when a 2-token verify costs at
- *    least 1.5 plain steps), a speculative rate (decayed tokens / seconds) below E_AD_MARGIN of
- *    the plain-step rate switches to plain steps; after E_AD_PROBE0, 2x, .. E_AD_PROBE_MAX plain
- *    steps, E_AD_PROBE_ROUNDS speculative rounds are judged on their own. The plain step's time
- *    is measured when plain steps were taken, else estimated from the verify passes of widths 2
- *    and 3 as 2 tv(2) - tv(3) (at least tv(2) / 2); without either, only a rate below
- *    1 / (cheapest verify pass) counts as slow, since any pass of n >= 2 tokens costs at least
- *    one plain step.
- * Host code; the constants are the reference's, so the same timings give the same decisions. */
+ * Model. Draft j of a round is reached when drafts 1..j-1 were accepted; p_j estimates the
+ * probability that it is then accepted (decayed hit / try counts with a uniform prior, so an
+ * unseen position counts as 1/2). A round of width w emits E(w) = 1 + sum_{s<w} prod_{j<=s} p_j
+ * tokens on average and takes T(w) seconds, the running average of that width's measured
+ * rounds (the whole round: MTP drafts, verify pass, commit). The policy plays argmax E(w)/T(w).
+ *
+ * Exploration. A width never measured is costed as the cheapest measured one (so a wider
+ * round is tried whenever its expected tokens could pay, and a plain step is tried early,
+ * since it is costed below everything until measured); every E_AD_PROBE rounds the width with
+ * the oldest measurement is played once, so the costs follow the context as it grows. Host
+ * code. */
 #include <string.h>
 
 #include "engine.h"
 
-#define E_AD_ALPHA 0.25      /* weight of a new pass time in its running average */
-#define E_AD_DECAY 0.95      /* memory of the speculative rate per round */
-#define E_AD_MARGIN 0.95
-#define E_AD_MIN_ROUNDS 8
-#define E_AD_PROBE_ROUNDS 2
-#define E_AD_PROBE0 8
-#define E_AD_PROBE_MAX 64
+#define E_AD_ALPHA 0.25   /* weight of a new round time in its running average */
+#define E_AD_FORGET 0.97  /* decay of the acceptance counts per observed draft */
+#define E_AD_PROBE 32     /* rounds between re-measurements of the stalest width */
 
-static double running(double old, double x) { return old <= 0 ? x : old + E_AD_ALPHA * (x - old); }
-
-void e_adapt_init(e_adapt *a) {
+void e_adapt_init(e_adapt *a, int k) {
     memset(a, 0, sizeof *a);
-    a->probe_after = E_AD_PROBE0;
+    a->k = k < 0 ? 0 : k > PINFER_SPEC_MAX_K ? PINFER_SPEC_MAX_K : k;
 }
 
-int e_adapt_plain_now(e_adapt *a) {
-    if (!a->plain_mode) return 0;
-    if (a->plain_run < a->probe_after) return 1;
-    if (!a->probing) { /* a probe begins, judged on its own rounds */
-        a->probing = 1;
-        a->n_spec = 0;
-        a->r_tok = a->r_sec = 0.0;
+static double p_accept(const e_adapt *a, int j) {
+    return (a->hits[j] + 1.0) / (a->tries[j] + 2.0);
+}
+
+/* expected tokens of a round of width w */
+static double expected_tokens(const e_adapt *a, int w) {
+    double e = 1.0, reach = 1.0;
+    for (int j = 1; j < w; j++) {
+        reach *= p_accept(a, j);
+        e += reach;
     }
-    return 0;
+    return e;
 }
 
-void e_adapt_plain(e_adapt *a, double sec) {
-    a->t_plain = running(a->t_plain, sec);
-    if (a->plain_mode) a->plain_run++;
-}
-
-/* seconds of a plain step: measured, else estimated from verify widths 2 and 3, else 0 */
-static double plain_seconds(const e_adapt *a) {
-    if (a->t_plain > 0) return a->t_plain;
-    if (a->tv[2] > 0 && a->tv[3] > 0) {
-        const double t = 2.0 * a->tv[2] - a->tv[3];
-        return t > 0.5 * a->tv[2] ? t : 0.5 * a->tv[2];
+int e_adapt_width(e_adapt *a) {
+    const int wmax = a->k + 1;
+    a->rounds++;
+    double cheapest = 0.0;
+    for (int w = 1; w <= wmax; w++)
+        if (a->t[w] > 0 && (cheapest <= 0 || a->t[w] < cheapest)) cheapest = a->t[w];
+    if (cheapest <= 0) return wmax; /* nothing measured: the full width first */
+    if (a->rounds % E_AD_PROBE == 0) { /* re-measure the stalest width */
+        int w_old = 1;
+        for (int w = 2; w <= wmax; w++)
+            if (a->seen[w] < a->seen[w_old]) w_old = w;
+        return w_old;
     }
-    return 0.0;
+    int best = wmax;
+    double best_rate = -1.0;
+    for (int w = 1; w <= wmax; w++) {
+        /* an unmeasured plain step is costed below the cheapest round, so it is tried once */
+        const double t = a->t[w] > 0 ? a->t[w] : w == 1 ? 0.5 * cheapest : cheapest;
+        const double rate = expected_tokens(a, w) / t;
+        if (rate > best_rate) {
+            best_rate = rate;
+            best = w;
+        }
+    }
+    return best;
 }
 
-void e_adapt_round(e_adapt *a, int n, int emitted, double sec, double t_verify) {
-    if (n < 2 || n >= E_AD_W) return;
-    a->tv[n] = running(a->tv[n], t_verify);
-    a->r_tok = E_AD_DECAY * a->r_tok + emitted;
-    a->r_sec = E_AD_DECAY * a->r_sec + sec;
-    a->n_spec++;
-    double tv_min = 0.0;
-    for (int i = 2; i < E_AD_W; i++)
-        if (a->tv[i] > 0 && (tv_min <= 0 || a->tv[i] < tv_min)) tv_min = a->tv[i];
-    const double ts = plain_seconds(a);
-    const int slow = a->r_tok * tv_min < E_AD_MARGIN * a->r_sec ||
-                     (ts > 0 && a->r_tok * ts < E_AD_MARGIN * a->r_sec);
-    if (a->plain_mode) { /* a probe round */
-        if (a->n_spec < E_AD_PROBE_ROUNDS) return;
-        a->probing = 0;
-        a->plain_mode = slow;
-        if (!slow) a->probe_after = E_AD_PROBE0;
-        else a->probe_after = 2 * a->probe_after < E_AD_PROBE_MAX ? 2 * a->probe_after : E_AD_PROBE_MAX;
-        a->plain_run = 0;
-        a->n_spec = 0;
-        if (slow) a->r_tok = a->r_sec = 0.0;
-    } else if (slow && (a->n_spec >= E_AD_MIN_ROUNDS ||
-                        (ts > 0 && a->tv[2] >= 1.5 * ts && a->n_spec >= 2))) {
-        a->plain_mode = 1;
-        a->plain_run = 0;
-        a->probe_after = E_AD_PROBE0;
+void e_adapt_observe(e_adapt *a, int w, int accepted, double sec) {
+    if (w < 1 || w > a->k + 1) return;
+    a->t[w] = a->t[w] > 0 ? a->t[w] + E_AD_ALPHA * (sec - a->t[w]) : sec;
+    a->seen[w] = a->rounds;
+    /* drafts 1..accepted were accepted; draft accepted + 1 (if verified) was rejected */
+    for (int j = 1; j < w && j <= accepted + 1; j++) {
+        a->hits[j] = E_AD_FORGET * a->hits[j] + (j <= accepted ? 1.0 : 0.0);
+        a->tries[j] = E_AD_FORGET * a->tries[j] + 1.0;
     }
 }

@@ -88,6 +88,7 @@ static int alloc_state(pinfer_ctx *c) {
     const size_t logw = (size_t)c->lk_dim + c->lv_dim + 1;
     c->cap = E_MAX_K + 1;
     c->conv_state = dalloc(c, (size_t)imax(c->n_lin, 1) * (S ? S : 1) * c->conv_dim * 4, &ok);
+    c->conv_bak = dalloc(c, (size_t)imax(c->n_lin, 1) * (S ? S : 1) * c->conv_dim * 4, &ok);
     c->rec = dalloc(c, (size_t)imax(c->n_lin, 1) * c->lv_heads * c->lk_dim * c->lv_dim * 4, &ok);
     c->kv_bytes = nmx_kv_bytes(c->kv_dtype, c->n_kv, c->max_ctx, c->hd);
     if (!c->kv_bytes) return PINFER_E_ARG;
@@ -129,7 +130,6 @@ static int alloc_state(pinfer_ctx *c) {
     c->mbuf = dalloc(c, (size_t)3 * H * 4, &ok);
     c->ctl = dalloc(c, 16 * 4, &ok);
     c->vt = dalloc(c, (E_MAX_K + 2) * 4, &ok);
-    c->gate = dalloc(c, (E_MAX_K + 2) * 4, &ok);
     c->tok = dalloc(c, B * 4, &ok);
     c->hout = dalloc(c, (2 + B) * 4, &ok);
     c->hout2 = dalloc(c, 4 * 4, &ok);
@@ -154,6 +154,8 @@ pinfer_ctx *pinfer_load(const char *path, const pinfer_params *params, int *err)
     else if (p.max_ctx > (1 << 20)) {
         fprintf(stderr, "pinfer: max_ctx %d above the attention kernels' 1048576\n", p.max_ctx);
         rc = PINFER_E_ARG;
+    } else if ((rc = e_model_check(path)) != PINFER_OK) {
+        /* refused before any device call */
     } else if (!(c = calloc(1, sizeof *c))) rc = PINFER_E_NOMEM;
     if (rc == PINFER_OK) {
         const char *dv = getenv("PINFER_DEVICE");

@@ -47,22 +47,24 @@ typedef struct {
     float *row1;       /* [hidden] */
 } e_scratch;
 
-/* Prompt-lookup drafts (engine/src/ngram.h:13-47, spec.h:40-47): n-gram lengths looked up,
- * the backward extension of a match, and the draft rule (a match of at least E_NG_TRUST tokens
- * drafts in full; E_NG_ASK.. tokens only when its first token equals the MTP head's draft, then
- * at most E_NG_SHORT tokens; without the MTP head, shorter matches draft E_NG_SHORT tokens). */
+/* Prompt-lookup drafts (ngram.c; the role of engine/src/ngram.h:13-47): a draft continues the
+ * most recent earlier occurrence of the history's tail that agrees with it over the most
+ * tokens (at least E_NG_MIN, counted up to E_NG_EXT). The draft rule of the speculative loop
+ * (spec.c ngram_pick): an agreement of at least E_NG_TRUST tokens drafts in full; E_NG_ASK..
+ * tokens only when the draft's first token equals the MTP head's d1, then at most E_NG_SHORT
+ * tokens; without the MTP head, shorter agreements draft E_NG_SHORT tokens. */
 #define E_NG_MIN 2
-#define E_NG_MAX 4
 #define E_NG_EXT 32
 #define E_NG_TRUST 16
 #define E_NG_ASK 4
 #define E_NG_SHORT 3
 
 typedef struct {
-    int32_t *tok;  /* [cap] token history, oldest first */
-    int32_t *tab;  /* [E_NG_MAX - E_NG_MIN + 1][1 << bits] end position + 1, 0 = empty */
-    int cap, n;    /* capacity, tokens in the history */
-    int indexed;   /* n-grams ending before this position are in tab */
+    int32_t *tok;   /* [cap] token history, oldest first */
+    int32_t *link;  /* [cap] next older position whose 2-gram shares the bucket, -1: none */
+    int32_t *head;  /* [1 << bits] newest indexed position per 2-gram bucket, -1: none */
+    int cap, n;     /* capacity, tokens in the history */
+    int indexed;    /* positions [1, indexed) are in the chains */
     int bits;
 } e_ngram;
 
@@ -71,28 +73,27 @@ void e_ngram_free(e_ngram *g);
 void e_ngram_reset(e_ngram *g);
 void e_ngram_push(e_ngram *g, const int32_t *t, int m);
 void e_ngram_pop(e_ngram *g);
-/* Up to max tokens that followed the most recent earlier occurrence of the history's longest
- * matching tail n-gram; returns the count (0: no match) and, if match != NULL, how many
- * tokens the two occurrences share backwards. */
+/* Up to max tokens that followed the chosen earlier occurrence of the history's tail; returns
+ * the count (0: no occurrence) and, if match != NULL, how many tokens the occurrence agrees
+ * with the tail, counted backwards from the newest (E_NG_MIN .. E_NG_EXT). */
 int e_ngram_draft(e_ngram *g, int32_t *out, int max, int *match);
 
-/* The adaptive speculation policy (adapt.c, engine/src/spec.h:49-57, spec_adapt.c) */
-#define E_AD_W (PINFER_SPEC_MAX_K + 2) /* verify widths 1..PINFER_SPEC_MAX_K + 1 */
-#define E_AD_TAU 0.6f                  /* chain on while the newest draft's top-1 p >= this */
+/* The adaptive speculation policy (adapt.c; the role of engine/src/spec_adapt.c): the verify
+ * width of the next round (1 = a plain step) from decayed acceptance counts per draft position
+ * and the measured seconds of each width's rounds. */
+#define E_AD_W (PINFER_SPEC_MAX_K + 2) /* widths 1..PINFER_SPEC_MAX_K + 1 */
 typedef struct {
-    double tv[E_AD_W];    /* running seconds of a verify pass of n tokens, 0 = not measured */
-    double t_plain;       /* running seconds of the plain steps taken, 0 = none yet */
-    double r_tok, r_sec;  /* decayed tokens emitted and seconds spent by speculative rounds */
-    int n_spec;           /* speculative rounds since speculation (or a probe) started */
-    int plain_mode;       /* plain steps; speculation is probed after probe_after of them */
-    int plain_run, probe_after;
-    int probing;          /* plain mode: the current speculative rounds are a probe */
+    int k;                 /* largest draft count: widths 1..k + 1 */
+    double t[E_AD_W];      /* running seconds of a round of width w, 0 = not measured */
+    long seen[E_AD_W];     /* round count when width w was last measured */
+    double hits[E_AD_W], tries[E_AD_W]; /* decayed counts: draft j reached / accepted */
+    long rounds;           /* widths chosen so far */
 } e_adapt;
 
-void e_adapt_init(e_adapt *a);
-int e_adapt_plain_now(e_adapt *a);
-void e_adapt_plain(e_adapt *a, double sec);
-void e_adapt_round(e_adapt *a, int n, int emitted, double sec, double t_verify);
+void e_adapt_init(e_adapt *a, int k);
+int e_adapt_width(e_adapt *a);
+/* a round of width w (w - 1 drafts) accepted `accepted` drafts and took sec seconds */
+void e_adapt_observe(e_adapt *a, int w, int accepted, double sec);
 
 struct pinfer_ctx {
     nmx_ctx *dev;
@@ -144,15 +145,11 @@ struct pinfer_ctx {
 
     /* host mirror of the position state */
     int n_past, mtp_rows, keep;
-    /* captured rounds: verify graph and commit graph per draft count */
-    nmx_graph *g_verify[E_MAX_K + 1], *g_commit[E_MAX_K + 1];
-    /* n-gram rounds: verify without the MTP chain, commit without the MTP pass */
-    nmx_graph *g_verify_ng[E_MAX_K + 1], *g_commit_ng;
-    /* adaptive rounds: one MTP chain step per graph (draft s + 1 and its confidence gate) */
-    nmx_graph *g_chain[E_MAX_K + 1];
-    int gate_on;              /* this generation computes the confidence gates (adaptive) */
-    int graph_gate;           /* gate_on when the graphs were captured */
-    int32_t *gate;            /* [E_MAX_K + 2] device: top-1 p of draft s >= E_AD_TAU (0: d1) */
+    /* captured rounds, one graph per draft count: MTP rounds (MTP chain, verify pass, head
+     * and acceptance, commit, MTP pass over the committed rows) and n-gram rounds (verify
+     * pass, head and acceptance, commit) */
+    nmx_graph *g_round[E_MAX_K + 1], *g_round_ng[E_MAX_K + 1];
+    float *conv_bak;          /* [n_lin][conv_k-1][conv_dim]: conv state before the last commit */
     e_ngram ng;               /* token history of the prompt-lookup drafts */
     int graph_nv;             /* draft vocabulary the graphs were captured with */
     int use_graphs;
@@ -168,8 +165,7 @@ struct pinfer_ctx {
 int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged);
 int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits);
 int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst,
-                  int32_t *gate_dst);
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst);
 int e_set_pos(pinfer_ctx *c, int pos);
 
 /* spec.c */
@@ -188,7 +184,10 @@ void e_drop_graphs(pinfer_ctx *c);
 size_t e_kv_row_bytes(const pinfer_ctx *c);
 int e_kv_zero_rows(pinfer_ctx *c, void *cache, int p0, int p1);
 
-/* model.c */
+/* model.c: e_model_check validates a .pq file (header, directory, every tensor the engine
+ * maps, the kernels' limits) with no device call; e_model_load does the same, then uploads the
+ * data section and builds the device views */
+int e_model_check(const char *path);
 int e_model_load(pinfer_ctx *c, const char *path);
 
 #endif

@@ -174,12 +174,9 @@ int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits) {
 /* The MTP draft head (engine/src/mtp.c:60-100) over n rows: h_dev [n][H] final-normed
  * hiddens, tok_dev [n] the tokens that follow them, positions ctl[0] + pos_off + i. The
  * selected row (n - 1, or ctl[1] - 1 when head_row_dynamic) gives the draft (argmax over the
- * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL); with
- * gate_dst, also whether the draft's top-1 probability over those rows is >= E_AD_TAU
- * (engine/src/spec.c:93-97 top1_prob, spec_adapt.c pf_adapt_chain_more). */
+ * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL). */
 int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst,
-                  int32_t *gate_dst) {
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H;
@@ -204,10 +201,7 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
         /* one row: the final norm writes the MTP hidden and the head's A8 input itself */
         CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, 1, H, c->rms_eps,
                           m_dst ? m_dst : s->xn, H, draft_dst ? s->a_1 : none));
-        if (!draft_dst) return PINFER_OK;
-        TRY(head_a8(c, nv, draft_dst, gate_dst != NULL));
-        if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
-        return PINFER_OK;
+        return draft_dst ? head_a8(c, nv, draft_dst, 0) : PINFER_OK;
     }
     const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
     const int off = head_row_dynamic ? -1 : n - 1;
@@ -215,16 +209,10 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
         /* only the selected row: its MTP hidden and the head's A8 input, one launch */
         CK(nmx_rmsnorm_row(D, r.cur, H, r.add, H, c->mtp_norm_out, H, c->rms_eps, idx, off, n,
                            m_dst, draft_dst ? s->a_1 : none));
-        if (!draft_dst) return PINFER_OK;
-        TRY(head_a8(c, nv, draft_dst, gate_dst != NULL));
-        if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
-        return PINFER_OK;
+        return draft_dst ? head_a8(c, nv, draft_dst, 0) : PINFER_OK;
     }
     CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H,
                       none));
     if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));
-    if (!draft_dst) return PINFER_OK;
-    TRY(head_row(c, idx, off, nv, draft_dst, gate_dst != NULL));
-    if (gate_dst) CK(nmx_top1_gate(D, c->logits, nv, E_AD_TAU, gate_dst));
-    return PINFER_OK;
+    return draft_dst ? head_row(c, idx, off, nv, draft_dst, 0) : PINFER_OK;
 }

@@ -256,7 +256,9 @@ static uint64_t fingerprint(const loader *L) {
     return f;
 }
 
-int e_model_load(pinfer_ctx *c, const char *path) {
+/* upload = 0: every check and view of the load with no device call (the views point into a
+ * dummy base that is never dereferenced), so a file is refused before a device is touched. */
+static int model_load(pinfer_ctx *c, const char *path, int upload) {
     int fd = open(path, O_RDONLY);
     if (fd < 0) {
         perror(path);
@@ -289,12 +291,14 @@ int e_model_load(pinfer_ctx *c, const char *path) {
             rc = PINFER_E_FORMAT;
         }
     }
-    if (rc == PINFER_OK) {
+    if (rc == PINFER_OK && upload) {
         const size_t bytes = L.size - h->data_offset;
         c->blob = nmx_alloc(c->dev, bytes ? bytes : 1);
         if (!c->blob) rc = PINFER_E_NOMEM;
         else if (nmx_upload(c->dev, c->blob, L.map + h->data_offset, bytes)) rc = PINFER_E_NOMEM;
         L.dev_base = c->blob;
+    } else if (rc == PINFER_OK) {
+        L.dev_base = (const uint8_t *)(uintptr_t)4096;
     }
     if (rc == PINFER_OK) {
         c->H = (int)h->hidden;
@@ -334,3 +338,14 @@ int e_model_load(pinfer_ctx *c, const char *path) {
     munmap(map, L.size);
     return rc;
 }
+
+int e_model_check(const char *path) {
+    pinfer_ctx *t = calloc(1, sizeof *t);
+    if (!t) return PINFER_E_NOMEM;
+    const int rc = model_load(t, path, 0);
+    free(t->layers);
+    free(t);
+    return rc;
+}
+
+int e_model_load(pinfer_ctx *c, const char *path) { return model_load(c, path, 1); }

@@ -1,20 +1,25 @@
 /* Speculative greedy decoding with the MTP head on the device (engine/src/spec.c:153-383,
- * restated for a device-resident model). One round with P = n_past and cur the newest token:
+ * restated for a device-resident model). One round with P = n_past and cur the newest token is
+ * ONE graph launch:
  *
- *   verify graph (one submit):  MTP chain d2..dk (d1 is ready from the last round), the
- *       logged main pass over [cur, d1..dk], the LM head fused with argmax + acceptance;
- *   host:  reads a and the tokens, emits them until a stop condition -> e (normally a + 1);
- *   commit graph (one submit):  cur <- vt[e], the rollback commit of every linear layer (conv
- *       state now, the e - 1 recurrent updates deferred to the next pass), the MTP head over
- *       the committed rows (next d1 and its hidden), n_past += e.
+ *   MTP chain d2..dk (d1 is ready from the last round); the logged main pass over
+ *   [cur, d1..dk]; the LM head fused with argmax + acceptance, which writes (a, tokens) to the
+ *   host mailbox; the commit of e = a + 1 tokens (cur <- vt[e], the rollback commit of every
+ *   linear layer: conv state now, the e - 1 recurrent updates deferred into the next pass); the
+ *   MTP head over the committed rows (next d1 and its hidden); n_past += e.
  *
- * Both graphs are captured once per draft count and replayed at any position (the kernels read
- * n_past, e and keep from the device control block). With pinfer_spec_params.ngram a round may
- * instead draft by prompt lookup (ngram.c, engine/src/spec.c:133-151): its verify graph has no
- * MTP chain (the host uploads the drafts) and its commit graph no MTP pass (the committed rows
- * wait, with those of plain steps, for one batched MTP pass before the next MTP round,
- * engine/src/spec.c:110-131). Tokens emitted equal plain greedy
- * decoding whatever the drafts are. */
+ * The host reads the mailbox while the graph's commit part still runs, emits the tokens and
+ * launches the next round behind it, so the stream never drains between rounds. When a stop
+ * condition ends the generation inside the accepted run (e < a + 1), one corrective commit is
+ * enqueued after the graph: the linear layers' commit redone for e from the kept conv rows,
+ * n_past and e set; the MTP rows past the stop are never read. Graphs are captured once per
+ * draft count and replayed at any position (the kernels read n_past, e and keep from the
+ * device control block). With pinfer_spec_params.ngram a round may instead draft by prompt
+ * lookup (ngram.c, engine/src/spec.c:133-151): its graph has no MTP chain (the host uploads the
+ * drafts) and no MTP pass (the committed rows wait, with those of plain steps, for one batched
+ * MTP pass before the next MTP round, engine/src/spec.c:110-131). With
+ * pinfer_spec_params.adaptive the draft count of each round (0: a plain step) comes from the
+ * policy of adapt.c. Tokens emitted equal plain greedy decoding whatever the drafts are. */
 #define _POSIX_C_SOURCE 200809L
 #include <stdio.h>
 #include <stdlib.h>
@@ -38,14 +43,10 @@
 
 void e_drop_graphs(pinfer_ctx *c) {
     for (int i = 0; i <= E_MAX_K; i++) {
-        nmx_graph_destroy(c->g_verify[i]);
-        nmx_graph_destroy(c->g_commit[i]);
-        nmx_graph_destroy(c->g_verify_ng[i]);
-        nmx_graph_destroy(c->g_chain[i]);
-        c->g_verify[i] = c->g_commit[i] = c->g_verify_ng[i] = c->g_chain[i] = NULL;
+        nmx_graph_destroy(c->g_round[i]);
+        nmx_graph_destroy(c->g_round_ng[i]);
+        c->g_round[i] = c->g_round_ng[i] = NULL;
     }
-    nmx_graph_destroy(c->g_commit_ng);
-    c->g_commit_ng = NULL;
 }
 
 static int draft_vocab(const pinfer_ctx *c, const pinfer_spec_params *sp) {
@@ -57,90 +58,64 @@ static int draft_vocab(const pinfer_ctx *c, const pinfer_spec_params *sp) {
 static float *m_cur(pinfer_ctx *c) { return c->mbuf; }
 static float *m_ping(pinfer_ctx *c, int i) { return c->mbuf + (size_t)(1 + (i & 1)) * c->H; }
 
-/* MTP chain + verify pass + head/acceptance for ke drafts (engine/src/spec.c:303-345). */
-static int seq_verify(pinfer_ctx *c, int ke, int nv) {
+/* The logged main pass over vt[0..ke] and the head with the acceptance of vt[1..ke]; the
+ * result (a, bonus, vt) goes to the host mailbox, and ctl[1] = e = a + 1
+ * (engine/src/spec.c:323-351). */
+static int seq_verify(pinfer_ctx *c, int ke) {
+    TRY(e_forward(c, c->vt, ke + 1, 1));
+    e_scratch *sc = &c->s;
+    CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
+                       NULL, c->vt + 1, c->hwork, c->hout));
+    CK(nmx_accept_commit_mb(c->dev, c->hout, c->vt, c->ctl, c->mbox, ke + 2));
+    return PINFER_OK;
+}
+
+/* The rollback commit of every linear layer for e = ctl[1], which also sets cur <- vt[e] (a
+ * kernel of its own without linear layers); redo: from the conv rows the last commit kept,
+ * leaving vt alone (engine/src/forward_lin.c:185-204). */
+static int commit_lin_cur(pinfer_ctx *c, int redo) {
+    nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
+                         c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl,
+                         redo ? NULL : c->vt, c->conv_bak, redo};
+    if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
+    else if (!redo) CK(nmx_copy_token(c->dev, c->vt, c->ctl));
+    return PINFER_OK;
+}
+
+/* One MTP round of ke drafts (engine/src/spec.c:303-365): the chain d2..dk, the verify, the
+ * commit of e = ctl[1], the MTP head over the committed rows (its hidden of row e - 1 and the
+ * next d1; the pass reads the verify's final-normed rows, s.xn, which at hidden <= 1024 it
+ * never writes, and otherwise writes only after its last read), n_past += e. */
+static int seq_round(pinfer_ctx *c, int ke, int nv) {
     for (int s = 1; s < ke; s++) {
         const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
-        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), NULL));
+        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s)));
     }
-    TRY(e_forward(c, c->vt, ke + 1, 1));
-    e_scratch *sc = &c->s;
-    CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
-                       NULL, c->vt + 1, c->hwork, c->hout));
-    CK(nmx_accept_commit_mb(c->dev, c->hout, c->vt, c->ctl, c->mbox, ke + 2));
-    return PINFER_OK;
-}
-
-/* Commit e = ctl[1] tokens and run the MTP head over them (engine/src/spec.c:346-365). */
-/* The rollback commit of every linear layer, which also sets cur <- vt[e] (a kernel of its
- * own without linear layers). */
-static int commit_lin_cur(pinfer_ctx *c) {
-    nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
-                         c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl, c->vt};
-    if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
-    else CK(nmx_copy_token(c->dev, c->vt, c->ctl));
-    return PINFER_OK;
-}
-
-static int seq_commit(pinfer_ctx *c, int ke, int nv) {
-    TRY(commit_lin_cur(c));
-    /* the MTP pass reads the final-normed rows before it writes s.xn itself */
-    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c),
-                      c->gate_on ? c->gate : NULL));
+    TRY(seq_verify(c, ke));
+    TRY(commit_lin_cur(c, 0));
+    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c)));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
 }
 
-/* The n-gram round's verify: [cur, drafts] (the drafts uploaded into vt[1..ke] by the host)
- * through the logged main pass, the head with acceptance. */
-static int seq_verify_ng(pinfer_ctx *c, int ke) {
-    TRY(e_forward(c, c->vt, ke + 1, 1));
-    e_scratch *sc = &c->s;
-    CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
-                       NULL, c->vt + 1, c->hwork, c->hout));
-    CK(nmx_accept_commit_mb(c->dev, c->hout, c->vt, c->ctl, c->mbox, ke + 2));
-    return PINFER_OK;
-}
-
-/* The n-gram round's commit: cur <- vt[e], the rollback commit, n_past += e. The committed
- * rows stay in s.xn for the host to queue for the MTP pass. */
-static int seq_commit_ng(pinfer_ctx *c) {
-    TRY(commit_lin_cur(c));
+/* One n-gram round (the host uploaded the drafts into vt[1..ke]): the verify, the commit,
+ * n_past += e. The committed rows stay in s.xn for the host to queue for the MTP pass. */
+static int seq_round_ng(pinfer_ctx *c, int ke) {
+    TRY(seq_verify(c, ke));
+    TRY(commit_lin_cur(c, 0));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
 }
 
-/* Adaptive rounds: chain step s drafts vt[s + 1] from (m of draft s, vt[s]) at position
- * n_past - 1 + s and gates it (gate[s]) (engine/src/spec.c:369-383). */
-static int seq_chain(pinfer_ctx *c, int s, int nv) {
-    const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
-    return e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), c->gate + s);
-}
-
-enum { SEQ_VERIFY, SEQ_COMMIT, SEQ_VERIFY_NG, SEQ_COMMIT_NG, SEQ_CHAIN };
-
-static int seq_run(pinfer_ctx *c, int ke, int nv, int kind) {
-    switch (kind) {
-    case SEQ_VERIFY: return seq_verify(c, ke, nv);
-    case SEQ_COMMIT: return seq_commit(c, ke, nv);
-    case SEQ_VERIFY_NG: return seq_verify_ng(c, ke);
-    case SEQ_CHAIN: return seq_chain(c, ke, nv);
-    default: return seq_commit_ng(c);
-    }
-}
-
-static int graph_for(pinfer_ctx *c, int ke, int nv, int kind, nmx_graph **out) {
-    nmx_graph **slot = kind == SEQ_VERIFY ? &c->g_verify[ke] : kind == SEQ_COMMIT ? &c->g_commit[ke]
-                     : kind == SEQ_VERIFY_NG ? &c->g_verify_ng[ke]
-                     : kind == SEQ_CHAIN ? &c->g_chain[ke] : &c->g_commit_ng;
-    if (c->graph_nv != nv || c->graph_gate != c->gate_on) {
+static int graph_for(pinfer_ctx *c, int ke, int nv, int ng, nmx_graph **out) {
+    nmx_graph **slot = ng ? &c->g_round_ng[ke] : &c->g_round[ke];
+    if (c->graph_nv != nv) {
         e_drop_graphs(c);
         c->graph_nv = nv;
-        c->graph_gate = c->gate_on;
     }
     if (!*slot) {
         CK(nmx_graph_begin(c->dev));
-        int rc = seq_run(c, ke, nv, kind);
+        int rc = ng ? seq_round_ng(c, ke) : seq_round(c, ke, nv);
         nmx_graph *g = nmx_graph_end(c->dev);
         if (rc != PINFER_OK) {
             nmx_graph_destroy(g);
@@ -156,20 +131,31 @@ static int graph_for(pinfer_ctx *c, int ke, int nv, int kind, nmx_graph **out) {
     return PINFER_OK;
 }
 
-static int run_seq(pinfer_ctx *c, int ke, int nv, int kind) {
-    if (kind == SEQ_VERIFY || kind == SEQ_VERIFY_NG) /* cleared before the launch that sets it */
-        __atomic_store_n(c->mbox + 2 + ke + 2, 0, __ATOMIC_RELAXED);
-    if (!c->use_graphs) return seq_run(c, ke, nv, kind);
+/* Enqueue one round; its mailbox flag (mbox[2 + ke + 2]) is cleared first. */
+static int launch_round(pinfer_ctx *c, int ke, int nv, int ng) {
+    __atomic_store_n(c->mbox + 2 + ke + 2, 0, __ATOMIC_RELAXED);
+    if (!c->use_graphs) return ng ? seq_round_ng(c, ke) : seq_round(c, ke, nv);
     nmx_graph *g;
-    TRY(graph_for(c, ke, nv, kind, &g));
+    TRY(graph_for(c, ke, nv, ng, &g));
     CK(nmx_graph_launch(c->dev, g));
+    return PINFER_OK;
+}
+
+/* A stop inside the accepted run: commit e (< a + 1) instead of the device's a + 1, after the
+ * round on the stream: ctl[1] = e, the linear layers' commit redone from the kept conv rows,
+ * ctl[0] = P + e, cur = the host's vt[e] (the round's MTP pass has overwritten vt[1]). */
+static int recommit(pinfer_ctx *c, int P, int e, int32_t cur) {
+    CK(nmx_ctl_set(c->dev, c->ctl, 1, e));
+    TRY(commit_lin_cur(c, 1));
+    CK(nmx_ctl_set(c->dev, c->ctl, 0, P + e));
+    CK(nmx_upload(c->dev, c->vt, &cur, sizeof cur));
     return PINFER_OK;
 }
 
 static double now_sec(void);
 
-/* Waits for the verify round's mailbox flag (mbox[2 + ke + 2], set last by the accept kernel
- * with a system-scope release): a short spin on the host copy, then, after 2 s, the stream
+/* Waits for a round's mailbox flag (mbox[2 + ke + 2], set by the accept kernel with a
+ * system-scope release): a spin on the host copy, then, after 2 s, the stream
  * synchronisation, which also reports a failed launch. */
 static int wait_mailbox(pinfer_ctx *c, int ke) {
     const int32_t *flag = c->mbox + 2 + ke + 2;
@@ -225,7 +211,7 @@ static int prefill(pinfer_ctx *c, const int32_t *prompt, int n, int use_mtp, int
             CK(nmx_upload(c->dev, c->tok, next, (size_t)nb * sizeof(int32_t)));
             if (last) CK(nmx_copy_d2d(c->dev, c->tok + nb - 1, c->vt, sizeof(int32_t)));
             TRY(e_mtp_forward(c, c->hbuf, c->tok, nb, 0, 0, nv, last ? c->vt + 1 : NULL,
-                              last ? m_cur(c) : NULL, last && c->gate_on ? c->gate : NULL));
+                              last ? m_cur(c) : NULL));
         }
         c->n_past += nb;
     }
@@ -260,8 +246,7 @@ static int flush_pending(pinfer_ctx *c, e_pending *pd, int nv) {
     if (pd->n == 0) return PINFER_OK;
     CK(nmx_upload(c->dev, c->tok, pd->tok, (size_t)pd->n * sizeof(int32_t)));
     TRY(e_set_pos(c, pd->pos));
-    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c),
-                      c->gate_on ? c->gate : NULL));
+    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c)));
     c->mtp_rows = pd->pos + pd->n;
     pd->n = 0;
     TRY(e_set_pos(c, c->n_past));
@@ -343,7 +328,6 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
     const int use_mtp = sp->k > 0, nv = draft_vocab(c, sp);
     const int drafting = sp->k > 0 || sp->ngram > 0;
     const int adaptive = sp->adaptive && drafting;
-    c->gate_on = adaptive && use_mtp; /* the MTP passes also gate their drafts */
     e_stop stop = {no_eos ? -1 : c->eos, opts ? opts->stop_ids : NULL, opts ? opts->n_stop : 0,
                    opts ? opts->on_token : NULL, opts ? opts->user : NULL};
     /* the n-gram history is the fed tokens plus the last emitted one, with which a continuation
@@ -363,8 +347,9 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
     e_pending pd;
     pd.n = pd.pos = 0;
     e_adapt ad;
-    e_adapt_init(&ad);
-    int32_t host[2 + E_MAX_BATCH], vt[E_MAX_K + 2];
+    e_adapt_init(&ad, sp->k > 0 ? sp->k : sp->ngram);
+    double t_last = now_sec(); /* end of the last round: a round's cost runs to its results */
+    int32_t vt[E_MAX_K + 2];
     while (!done) {
         const int P = c->n_past;
         int left = n_max - count - 1;
@@ -373,24 +358,25 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             rc = PINFER_E_CTX_FULL;
             break;
         }
-        const double r0 = now_sec();
-        /* prompt lookup first, else MTP drafts, else a plain step (the adaptive policy may
-         * take plain steps instead, engine/src/spec.c:300-312) */
+        /* drafts wanted: the adaptive policy's width - 1 (0: a plain step), else k; prompt
+         * lookup first, else MTP drafts (engine/src/spec.c:300-312) */
+        const int want = adaptive ? e_adapt_width(&ad) - 1 : sp->k;
         int ke = 0, use_ng = 0;
-        if (!(adaptive && e_adapt_plain_now(&ad))) {
-            if (sp->ngram > 0 && left > 0) ke = ngram_pick(c, sp, left, vt + 1, &pd, nv, &rc);
+        if (sp->ngram > 0 && left > 0 && !(adaptive && want == 0)) {
+            ke = ngram_pick(c, sp, left, vt + 1, &pd, nv, &rc);
             if (rc != PINFER_OK) break;
             use_ng = ke > 0;
-            if (!use_ng) ke = sp->k < left ? sp->k : left;
         }
+        if (!use_ng && use_mtp) ke = want < left ? want : left;
         if (ke == 0) {
             if (st && drafting) st->rounds++;
             if ((rc = plain_step(c, use_mtp, &pd, nv, &cur)) != PINFER_OK) break;
-            if (adaptive) e_adapt_plain(&ad, now_sec() - r0);
+            const double t = now_sec();
+            if (adaptive) e_adapt_observe(&ad, 1, 0, t - t_last);
+            t_last = t;
             done = emit(out, &count, n_max, cur, &stop);
             continue;
         }
-        double rv = 0.0; /* start of the verify pass */
         if (use_ng) {
             /* room for this round's rows among the pending ones */
             if (use_mtp && pd.n + ke + 1 > E_MAX_BATCH && (rc = flush_pending(c, &pd, nv)) != PINFER_OK)
@@ -399,47 +385,19 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
                 rc = PINFER_E_ARG;
                 break;
             }
-            rv = now_sec();
-            if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
-        } else if (!c->gate_on) {
-            if ((rc = flush_pending(c, &pd, nv)) != PINFER_OK) break; /* d1 current */
-            rv = now_sec();
-            if ((rc = run_seq(c, ke, nv, SEQ_VERIFY)) != PINFER_OK) break;
-        } else { /* adaptive: chain the MTP head while the newest draft is confident */
-            if ((rc = flush_pending(c, &pd, nv)) != PINFER_OK) break; /* d1 and its gate */
-            int32_t ok = 0, s = 1;
-            if (nmx_download(c->dev, &ok, c->gate, sizeof ok)) {
-                rc = PINFER_E_ARG;
-                break;
-            }
-            while (s < ke && ok) {
-                if ((rc = run_seq(c, s, nv, SEQ_CHAIN)) != PINFER_OK) break;
-                if (nmx_download(c->dev, &ok, c->gate + s, sizeof ok)) {
-                    rc = PINFER_E_ARG;
-                    break;
-                }
-                s++;
-            }
-            if (rc != PINFER_OK) break;
-            ke = s;
-            rv = now_sec();
-            if ((rc = run_seq(c, ke, nv, SEQ_VERIFY_NG)) != PINFER_OK) break;
+        } else if ((rc = flush_pending(c, &pd, nv)) != PINFER_OK) { /* d1 current */
+            break;
         }
+        if ((rc = launch_round(c, ke, nv, use_ng)) != PINFER_OK) break;
         if (wait_mailbox(c, ke)) { /* the verify wrote (a, bonus, vt) to the host mailbox */
             rc = PINFER_E_ARG;
             break;
         }
-        memcpy(host, c->mbox, 2 * sizeof(int32_t));
+        const int a = c->mbox[0];
         memcpy(vt, c->mbox + 2, (size_t)(ke + 2) * sizeof(int32_t));
-        const double tv = now_sec() - rv; /* the verify pass (its results read back) */
-        const int a = host[0];
         int e = 0;
         while (e <= a && !done) done = emit(out, &count, n_max, vt[++e], &stop);
-        if (e != a + 1 && nmx_ctl_set(c->dev, c->ctl, 1, e)) {
-            rc = PINFER_E_ARG;
-            break;
-        }
-        if ((rc = run_seq(c, ke, nv, use_ng ? SEQ_COMMIT_NG : SEQ_COMMIT)) != PINFER_OK) break;
+        if (e != a + 1 && (rc = recommit(c, P, e, vt[e])) != PINFER_OK) break;
         if (use_ng) {
             if (use_mtp && (rc = defer_rows(c, &pd, vt + 1, e, P)) != PINFER_OK) break;
         } else {
@@ -459,13 +417,9 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
                 st->ngram_accepted += a;
             }
         }
-        if (adaptive) { /* the round's time includes its commit (and MTP pass) */
-            if (nmx_sync(c->dev)) {
-                rc = PINFER_E_ARG;
-                break;
-            }
-            e_adapt_round(&ad, ke + 1, e, now_sec() - r0, tv);
-        }
+        const double t = now_sec();
+        if (adaptive) e_adapt_observe(&ad, ke + 1, a, t - t_last);
+        t_last = t;
     }
     if (rc == PINFER_OK && use_mtp) rc = flush_pending(c, &pd, nv);
     int frc = lin_flush(c);

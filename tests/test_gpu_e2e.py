@@ -116,8 +116,10 @@ def counters(s):
 def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
     """Prompt-lookup drafts (pinfer_spec_params.ngram, engine/src/spec.c:133-151): a prompt
     that repeats a span, so the history holds matches of every class (trusted, checked against
-    the MTP draft, short; with k = 0 the no-MTP rule). Tokens and all six speculative counters
-    equal the reference engine's; the output equals plain greedy; the states agree."""
+    the MTP draft, short; with k = 0 the no-MTP rule). The drafter is this engine's own
+    (ngram.c), so its rounds may differ from the reference engine's; the tokens equal the
+    reference's and plain greedy, the states agree, and n-gram rounds were drafted and
+    accepted."""
     path, base = agree_model if which == "agree" else (models["small"], np.random.default_rng(
         9).integers(0, pqfile.SMALL.vocab, 24))
     prompt = np.concatenate([base, base[:20], base])
@@ -125,8 +127,11 @@ def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
     print(f"[case] ngram {which} k={k} ngram={ngram}", flush=True)
     tg, sg = gpu.generate(prompt, 64, k=k, ngram=ngram)
     tr, sr = ref.generate(prompt, 64, k=k, ngram=ngram)
+    print(f"[stats] rounds drafted accepted (+ n-gram): {counters(sg)}, reference {counters(sr)}",
+          flush=True)
     assert tg == tr
-    assert counters(sg) == counters(sr)
+    assert sg.ngram_accepted <= sg.ngram_drafted and sg.ngram_rounds <= sg.rounds
+    assert sg.accepted <= sg.drafted
     if which == "agree":  # its output repeats itself; the random model's rarely does
         assert sg.ngram_rounds > 0 and sg.ngram_accepted > 0, "no accepted n-gram round"
     assert gpu.state_save() == ref.state_save(), "state after an n-gram generation"
@@ -134,7 +139,7 @@ def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
     # a continuation leading with the last emitted token keeps the history (both engines)
     tg2, sg2 = gpu.generate([tg[-1]] + list(base[:6]), 24, k=k, ngram=ngram, cont=True)
     tr2, sr2 = ref.generate([tr[-1]] + list(base[:6]), 24, k=k, ngram=ngram, cont=True)
-    assert tg2 == tr2 and counters(sg2) == counters(sr2)
+    assert tg2 == tr2
     probe = [1, 2, 3]
     assert np.array_equal(bits(gpu.eval(probe)), bits(ref.eval(probe)))
     gpu.close(), ref.close()
@@ -144,12 +149,13 @@ def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
 @pytest.mark.parametrize("which,k,ngram", [("agree", 4, 0), ("agree", 8, 7), ("small", 4, 0),
                                            ("small", 2, 4)])
 def test_adaptive_matches_reference(models, agree_model, which, k, ngram):
-    """The adaptive policy (pinfer_spec_params.adaptive, engine/src/spec_adapt.c): MTP chains
-    cut where the newest draft's top-1 probability falls below 0.6, plain steps while
-    speculation does not pay, probes back. Its choices follow measured times, so the two engines
-    may take different rounds (the counters are not compared); the tokens and the state may not
-    differ: both equal plain greedy, and the state blobs after the generation are identical.
-    The random model's drafts are almost never accepted, so its runs switch to plain steps."""
+    """The adaptive policy (pinfer_spec_params.adaptive; this engine's own, adapt.c: the
+    verify width with the best expected tokens per second from acceptance counts and measured
+    round times, plain steps included). The reference's policy differs and both follow
+    measured times, so the engines take different rounds (the counters are not compared); the
+    tokens and the state may not differ: both equal plain greedy, and the state blobs after
+    the generation are identical. The random model's drafts are almost never accepted, so its
+    runs move to plain steps."""
     path, base = agree_model if which == "agree" else (models["small"], np.random.default_rng(
         9).integers(0, pqfile.SMALL.vocab, 24))
     prompt = np.concatenate([base, base[:20], base]) if ngram else base

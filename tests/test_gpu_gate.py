@@ -1,6 +1,8 @@
-"""GPU parity: the adaptive policy's chain gate (libnmx.so nmx_top1_gate) against the oracle's
-top-1 softmax probability (the reference's top1_prob, engine/src/spec.c:89-92, compared with
-CONF_TAU as in engine/src/spec_adapt.c:56).
+"""GPU parity: the device form of the reference's chain gate (libnmx.so nmx_top1_gate: the
+top-1 softmax probability of a draft row, the reference's top1_prob, engine/src/spec.c:89-92,
+compared with CONF_TAU as in engine/src/spec_adapt.c:56) against the oracle's. The engine's own
+adaptive policy does not gate chains; the device ABI keeps the gate for callers of the
+reference's policy.
 
 Bar: the flag equals (oracle top1_prob(row) >= tau) for every row. The rows include ones whose
 probability lies within the kernel's double-precision error band around tau, where the decision
