@@ -140,6 +140,19 @@ int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
                        const float *d, const float *fsum, float *logits, const int32_t *drafts,
                        void *work, int32_t *out, int32_t *tok_dst);
 
+/* nmx_head_accept without the workspace argument: allocates nothing and takes no workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * partial argmax keys live in a static device array of NMX_HEAD_SCRATCH_BYTES per GPU (held
+ * until the process ends), so nmx_head_work_bytes(rows, n) must not exceed it (rows <= 2^20
+ * at n <= 16; larger shapes fail with an error). The caller passes inputs and outputs as for
+ * nmx_head_accept and gets the same results. Calls on one GPU share the array: calls that
+ * overlap in time on one GPU (two streams, two contexts) race; calls on one stream do not. */
+#define NMX_HEAD_SCRATCH_BYTES (512 * 1024)
+int nmx_head_accept_noalloc(nmx_ctx *ctx, const void *W, int rows, int cols, int n,
+                            const int8_t *q, const float *d, const float *fsum, float *logits,
+                            const int32_t *drafts, int32_t *out);
+
 /* ---- verify-step glue (the rest of one forward pass, engine/src/forward*.c) -------------
  * All enqueue on the context's stream; positions come from a device control block so a
  * captured HIP graph can be replayed at any position: ctl[0] = n_past at the start of the

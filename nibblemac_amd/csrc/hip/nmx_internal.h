@@ -62,6 +62,10 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
                   bool swiglu, nmx_a8 out);
 
 
+/* Resolve the device address of nmx_head_accept_noalloc's static scratch array for
+ * ctx->device (current on the calling thread), once per device; nmx_create calls it. */
+int nmx_head_scratch_init(nmx_ctx *ctx);
+
 /* [a, a + na) and [b, b + nb) overlap (byte ranges). */
 static inline bool nmx_overlap(const void *a, size_t na, const void *b, size_t nb) {
     const char *pa = (const char *)a, *pb = (const char *)b;

@@ -17,6 +17,8 @@
  *   - the 6-bit sub-scales / sub-mins of the lane's row are decoded from the 64-byte scale line
  *     once per superblock.
  * Several matrices that share one input run in one launch (segment table). */
+#include <mutex>
+
 #include "nmx_internal.h"
 #include "nmx_a8.h"
 #include "nmx_lanes.h"
@@ -782,6 +784,35 @@ size_t q4k_bytes(int rows, int cols) {
 
 } // namespace
 
+/* The partial argmax keys of nmx_head_accept_noalloc live in this array instead of a
+ * caller-provided workspace: one copy per device, at a device address that
+ * nmx_head_scratch_init resolves once per device (host code must never pass the array's own
+ * name to a kernel: on the host it only stands for the device symbol). Every call of the
+ * entry point on a device shares the copy; the keys of a call are all written by its head
+ * kernel before head_finish_k reads them, so nothing needs clearing between calls. */
+static __device__ __align__(256) unsigned long long scratch[NMX_HEAD_SCRATCH_BYTES / 8];
+
+namespace {
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+unsigned long long *g_scratch[SCRATCH_DEVICES]; /* device address of `scratch`, per device */
+} // namespace
+
+int nmx_head_scratch_init(nmx_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= SCRATCH_DEVICES)
+        return nmx_fail(ctx, "head scratch: device %d beyond %d", ctx->device, SCRATCH_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[ctx->device]) return 0;
+    int cur = -1;
+    NMX_HIP(ctx, hipGetDevice(&cur));
+    if (cur != ctx->device) return nmx_fail(ctx, "head scratch: device %d not current", ctx->device);
+    void *ptr = nullptr;
+    NMX_HIP(ctx, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr || (uintptr_t)ptr % 256) return nmx_fail(ctx, "head scratch: bad symbol address");
+    g_scratch[ctx->device] = (unsigned long long *)ptr;
+    return 0;
+}
+
 extern "C" {
 
 int nmx_quant_a8(nmx_ctx *ctx, const float *X, int n, int cols, int8_t *q, float *d,
@@ -867,6 +898,25 @@ int nmx_head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, cons
                     const float *d, const float *fsum, float *logits, const int32_t *drafts,
                     void *work, int32_t *out) {
     return nmx_head_accept_to(ctx, W, rows, cols, n, q, d, fsum, logits, drafts, work, out, nullptr);
+}
+
+int nmx_head_accept_noalloc(nmx_ctx *ctx, const void *W, int rows, int cols, int n,
+                            const int8_t *q, const float *d, const float *fsum, float *logits,
+                            const int32_t *drafts, int32_t *out) {
+    if (!ctx) return -1;
+    const size_t kb = nmx_head_work_bytes(rows, n);
+    if (kb > NMX_HEAD_SCRATCH_BYTES)
+        return nmx_fail(ctx, "nmx_head_accept_noalloc: rows=%d n=%d need %zu scratch bytes, above "
+                        "the %d of the static array (use nmx_head_accept with a workspace)",
+                        rows, n, kb, NMX_HEAD_SCRATCH_BYTES);
+    unsigned long long *keys = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (ctx->device >= 0 && ctx->device < SCRATCH_DEVICES) keys = g_scratch[ctx->device];
+    }
+    if (!keys) return nmx_fail(ctx, "nmx_head_accept_noalloc: head scratch not set up");
+    return nmx_head_accept_to(ctx, W, rows, cols, n, q, d, fsum, logits, drafts, keys, out,
+                              nullptr);
 }
 
 int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,

@@ -65,6 +65,12 @@ nmx_ctx *nmx_create(int device) {
     }
     snprintf(ctx->name, sizeof ctx->name, "%s (%s, %d CUs)", prop.name, prop.gcnArchName,
              prop.multiProcessorCount);
+    if (nmx_head_scratch_init(ctx)) {
+        nmx_fail(nullptr, "device %d setup: %s", device, ctx->err);
+        (void)hipStreamDestroy(ctx->stream);
+        free(ctx);
+        return nullptr;
+    }
     return ctx;
 }
 

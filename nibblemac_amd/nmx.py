@@ -94,6 +94,7 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_head_work_bytes": (_sz, [_i, _i]),
     "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_accept_to": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nmx_head_accept_noalloc": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_accept_commit": (_i, [_vp, _vp, _vp, _vp]),
     "nmx_accept_commit_mb": (_i, [_vp, _vp, _vp, _vp, _vp, _i]),
     "nmx_host_alloc": (_vp, [_vp, _sz]),
@@ -382,6 +383,13 @@ class Device:
             rc = self.lib.nmx_head_accept_to(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
                                              _p(logits), _p(drafts), _p(work), _p(out), _p(tok_dst))
         self.check(rc, "head_accept")
+
+    def head_accept_noalloc(self, W, rows: int, cols: int, n: int, q, d, fs, logits, drafts,
+                            out) -> None:
+        """nmx_head_accept_noalloc: the head with its scratch in the library's static array."""
+        self.check(self.lib.nmx_head_accept_noalloc(self.ctx, _p(W), rows, cols, n, _p(q), _p(d),
+                                                    _p(fs), _p(logits), _p(drafts), _p(out)),
+                   "head_accept_noalloc")
 
     def accept_commit(self, out, vt, ctl, mailbox=None, nvt: int = 0) -> None:
         """nmx_accept_commit, or nmx_accept_commit_mb writing the host mailbox."""
