@@ -47,7 +47,7 @@ K_DRAFT, DRAFT_VOCAB = 4, 32768
 N_PROMPT, N_GEN = 512, 128
 CPU_SHARE = 16                       # host threads of one GPU's share of the box
 ONE_PROMPT, ONE_GEN = 16, 5          # the bounded 1-thread sample
-TRAFFIC_FILE = ROOT / "profiles" / "q4k_head_n5_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "q4k_head_n5_fused_traffic.json"
 
 
 def log(msg: str) -> None:
@@ -172,7 +172,7 @@ def main() -> int:
                     help="only the in-path LM head launches (for counter runs)")
     ap.add_argument("--kernels-only", action="store_true", help="only the config 1-4 lines")
     ap.add_argument("--eager", action="store_true",
-                    help="with --head-only: stream launches instead of graph replays")
+                    help="with --head-only / --kernels-only: stream launches, not graph replays")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="with --head-only: a device copy of this size first (counter scale)")
     a = ap.parse_args()
@@ -186,6 +186,7 @@ def main() -> int:
         print(json.dumps({"roofline": roof}), flush=True)
         return 0
     if a.kernels_only:
+        kbench.EAGER = a.eager
         with Device(0) as dev:
             ks = kbench.run_all(dev)
         print(json.dumps({"kernels": ks}), flush=True)

@@ -86,7 +86,8 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     /* chain records: (dot, (D*s)*d, -(M*m), fsum) float4 [nb][nv][R]; the SwiGLU launch (64
      * rows) keeps ((float)dot, (D*s)*d) float2 [nb][nv][R] and -(M*m) [nb][R] to fit */
     int work = swiglu ? nb * nv * R * 8 + nb * R * 4 : nb * nv * R * 16;
-    const int nwork = nv * (4 * cm_stride4(cols) + 4) * 4;
+    /* the norm prologue: chain-major squares, then the summed rows [nv][cols] */
+    const int nwork = nv * (4 * cm_stride4(cols) + 4) * 4 + nv * cols * 4;
     if (norm && nwork > work) work = nwork;
     L.res = L.work + work;
     L.total = L.res + (swiglu ? nv * R * 4 : 0);
@@ -142,23 +143,22 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
             bf[u] = fs[gi];
         }
     }
-    float xv[NORM ? NV : 1][MT_NORM_CPT], wv[MT_NORM_CPT];
+    /* the norm inputs: x and add stay in separate registers until the weight loads below are
+     * issued (adding them here would wait for their memory round trip first) */
+    float xv[NORM ? NV : 1][MT_NORM_CPT], av[NORM ? NV : 1][MT_NORM_CPT];
     if constexpr (NORM) { /* rows v0 .. v0 + NV - 1 (+ add): thread columns c = tid + T j */
 #pragma unroll
         for (int j = 0; j < MT_NORM_CPT; j++) {
             const int cc = tid + T * j;
             const int ci = cc < cols ? cc : cols - 1;
-            wv[j] = 0.0f;
 #pragma unroll
-            for (int v = 0; v < NV; v++) xv[v][j] = 0.0f;
+            for (int v = 0; v < NV; v++) xv[v][j] = 0.0f, av[v][j] = 0.0f;
             if (T * j >= cols) continue; /* uniform: slot unused by every thread */
-            wv[j] = nm.w[ci];
 #pragma unroll
             for (int v = 0; v < NV; v++) xv[v][j] = nm.x[(size_t)(v0 + v) * nm.x_stride + ci];
             if (nm.add) {
 #pragma unroll
-                for (int v = 0; v < NV; v++)
-                    xv[v][j] = xv[v][j] + nm.add[(size_t)(v0 + v) * nm.add_stride + ci];
+                for (int v = 0; v < NV; v++) av[v][j] = nm.add[(size_t)(v0 + v) * nm.add_stride + ci];
             }
         }
     }
@@ -183,6 +183,17 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
         a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
 #pragma unroll
         for (int k = 0; k < 4; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
+    }
+
+    if constexpr (NORM) { /* the residual add, now that the weight loads are in flight */
+        if (nm.add) {
+#pragma unroll
+            for (int j = 0; j < MT_NORM_CPT; j++) {
+                if (T * j >= cols) continue;
+#pragma unroll
+                for (int v = 0; v < NV; v++) xv[v][j] = xv[v][j] + av[v][j];
+            }
+        }
     }
 
     /* ---- phase 0c: activations into LDS ---- */
@@ -228,6 +239,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
         /* RMSNorm (sumsq: 4 interleaved partial sums + tail, chain-major squares in LDS) */
         const int s4 = cm_stride4(cols), rsz = 4 * s4 + 4, m4 = cols >> 2;
         float *sq = (float *)(smem + L.work);
+        float *xs = sq + NV * rsz; /* the summed rows [NV][cols] */
 #pragma unroll
         for (int j = 0; j < MT_NORM_CPT; j++) {
             const int cc = tid + T * j;
@@ -236,24 +248,32 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
 #pragma unroll
             for (int v = 0; v < NV; v++) {
                 sq[v * rsz + ix] = xv[v][j] * xv[v][j];
+                xs[v * cols + cc] = xv[v][j];
                 if (nm.x_out && blockIdx.x == 0) nm.x_out[(size_t)(v0 + v) * nm.xo_stride + cc] = xv[v][j];
             }
         }
         __syncthreads();
-        if (tid < 4 * NV) { /* chain l of row v */
+        if (tid < 4 * NV) { /* chain l of row v, the next 32 terms' reads issued ahead */
             const float *ch = sq + (tid >> 2) * rsz + (tid & 3) * s4;
             float a = 0.0f;
             int m = 0;
-            for (; m + 32 <= m4; m += 32) {
-                float4 b[8];
+            if (m4 >= 32) {
+                float4 b[8], nb4[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + m + 4 * u);
+                for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + 4 * u);
+                for (; m + 32 <= m4; m += 32) {
+                    const int mn = m + 64 <= m4 ? m + 32 : m; /* past the end: a reread */
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    a = a + b[u].x;
-                    a = a + b[u].y;
-                    a = a + b[u].z;
-                    a = a + b[u].w;
+                    for (int u = 0; u < 8; u++) nb4[u] = *(const float4 *)(ch + mn + 4 * u);
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        a = a + b[u].x;
+                        a = a + b[u].y;
+                        a = a + b[u].z;
+                        a = a + b[u].w;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; u++) b[u] = nb4[u];
                 }
             }
             for (; m < m4; m++) a = a + ch[m];
@@ -265,21 +285,51 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
             red[tid] = t;
         }
         __syncthreads();
-        float rv[NV];
+        /* A8 of y = (x * r) * w: a lane pair per (32-column block, vector), 16 columns each;
+         * the block's max and code sum are taken over the pair (exact in any order: the same
+         * values as a half-wave's lane reductions), the divisions once per lane */
+        for (int e2 = tid; e2 < 2 * nb * NV; e2 += T) { /* T is a multiple of 64: pairs stay whole */
+            const int e = e2 >> 1, hf = e2 & 1;
+            const int b = e / NV, v = e - b * NV;
+            const float sv = (red[4 * v] + red[4 * v + 1]) + (red[4 * v + 2] + red[4 * v + 3]);
+            const float r = 1.0f / sqrtf((sv + red[4 * NV + v]) / (float)cols + nm.eps);
+            const float4 *xp = (const float4 *)(xs + v * cols + 32 * b + 16 * hf);
+            const float4 *wp = (const float4 *)(nm.w + 32 * b + 16 * hf);
+            float y[16];
 #pragma unroll
-        for (int v = 0; v < NV; v++) {
-            const float s = (red[4 * v] + red[4 * v + 1]) + (red[4 * v + 2] + red[4 * v + 3]);
-            rv[v] = 1.0f / sqrtf((s + red[4 * NV + v]) / (float)cols + nm.eps);
-        }
+            for (int u = 0; u < 4; u++) {
+                const float4 xx = xp[u], ww = wp[u];
+                y[4 * u] = (xx.x * r) * ww.x;
+                y[4 * u + 1] = (xx.y * r) * ww.y;
+                y[4 * u + 2] = (xx.z * r) * ww.z;
+                y[4 * u + 3] = (xx.w * r) * ww.w;
+            }
+            float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MT_NORM_CPT; j++) {
-            const int cc = tid + T * j;
-            if (T * j + (tid & ~31) >= cols) continue; /* whole half-wave past the row */
-            const int b = cc >> 5;
+            for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(y[i]));
+            amax = fmaxf(amax, __int_as_float(nmx_dpp<NMX_DPP_XOR1>(__float_as_int(amax))));
+            const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+            int sum = 0;
+            uint32_t pk[4];
 #pragma unroll
-            for (int v = 0; v < NV; v++) {
-                const float y = (xv[v][j] * rv[v]) * wv[j];
-                nmx_a8_store(y, aq + aq_off(b, NV) + v * 32, ad + b * NV + v, afs + b * NV + v);
+            for (int u = 0; u < 4; u++) {
+                uint32_t w4 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int c = (int)rintf(y[4 * u + i] * id);
+                    sum += c;
+                    const int cs = c > 127 ? 127 : c < -128 ? -128 : c;
+                    w4 |= ((uint32_t)cs & 0xffu) << (8 * i);
+                }
+                pk[u] = w4;
+            }
+            sum += nmx_dpp<NMX_DPP_XOR1>(sum);
+            *(int4 *)(aq + aq_off(b, NV) + v * 32 + 16 * hf) =
+                make_int4((int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]);
+            if (hf == 0) {
+                const float dd = amax / 127.0f;
+                ad[b * NV + v] = dd;
+                afs[b * NV + v] = dd * (float)sum;
             }
         }
     }
@@ -433,8 +483,21 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
  * A8 block). The other launches use chain records and R = 8 (else 4): measured on the verify
  * shapes (1024 .. 3584 columns, 5 vectors) this beat every larger R, since a small workgroup's
  * dot and chain phases are short and several workgroups share a CU. */
-int pick_rows(int cols, int nv, bool norm, bool swiglu, int *threads) {
+int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int count, int *threads) {
     const int nsb = cols >> 8;
+    if (norm && !swiglu) {
+        /* every workgroup redoes the norm prologue: the fewest rows per workgroup (a multiple
+         * of 4) whose workgroups fit the 256 CUs in one round */
+        for (int R = 4 * ((total_rows + 4 * 256 - 1) / (4 * 256)); R <= 64; R += 4) {
+            if (R * 256 < total_rows + count * R) continue; /* each segment rounds up */
+            const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
+            const int tt = t * MT_NORM_CPT < cols ? 64 * ((cols / MT_NORM_CPT + 63) / 64) : t;
+            if (tt > MT_NORM_THREADS || mt_layout(cols, nv, R, true, false).total > MT_LDS) break;
+            *threads = tt;
+            return R;
+        }
+        return 0;
+    }
     for (int R = swiglu ? 64 : 8; R >= 4; R >>= 1) {
         if (swiglu && R != 64) break;
         const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
@@ -489,7 +552,11 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
     const int passes = (n + MT_MAX_NV - 1) / MT_MAX_NV;
     int T = 0;
     const int nv_max = (n + passes - 1) / passes;
-    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, &T);
+    /* the fused norm reads its weight as float4 */
+    if (norm && ((uintptr_t)norm->w & 15)) return 1;
+    int total_rows = 0;
+    for (int s = 0; s < count; s++) total_rows += segs[s].rows;
+    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, total_rows, count, &T);
     if (!R) return 1;
     MtTab tab{};
     tab.count = count;

@@ -187,6 +187,7 @@ pinfer_ctx *pinfer_load(const char *path, const pinfer_params *params, int *err)
 void pinfer_free(pinfer_ctx *c) {
     if (!c) return;
     if (c->dev) {
+        nmx_sync(c->dev); /* nothing of the stream in flight when its graphs are destroyed */
         e_drop_graphs(c);
         nmx_host_free(c->dev, c->mbox);
         pinfer_checkpoint_clear(c);

@@ -109,7 +109,8 @@ static int seq_round_ng(pinfer_ctx *c, int ke) {
 
 static int graph_for(pinfer_ctx *c, int ke, int nv, int ng, nmx_graph **out) {
     nmx_graph **slot = ng ? &c->g_round_ng[ke] : &c->g_round[ke];
-    if (c->graph_nv != nv) {
+    if (c->graph_nv != nv) { /* a replay of the old graphs may still run: wait for it */
+        CK(nmx_sync(c->dev));
         e_drop_graphs(c);
         c->graph_nv = nv;
     }

@@ -31,8 +31,22 @@ def matvec_algo_bytes(rows: int, cols: int, n: int, out: bool = True) -> int:
     return q4k_bytes(rows, cols) + n * cols + 2 * 4 * n * (cols // 32) + (4 * n * rows if out else 0)
 
 
+EAGER = False  # stream launches instead of graph replays (profiler counter runs)
+
+
 def _time_graph(dev: Device, launches, reps: int) -> float:
-    """ms per replay of a graph of `launches` (captured once, replayed after one warm-up)."""
+    """ms per replay of a graph of `launches` (captured once, replayed after one warm-up), or
+    per round of stream launches when EAGER."""
+    if EAGER:
+        launches()
+        dev.sync()
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        for _ in range(reps):
+            launches()
+        dev.record(e1)
+        dev.sync()
+        return dev.elapsed_ms(e0, e1) / reps
     dev.graph_begin()
     launches()
     g = dev.graph_end()
@@ -44,7 +58,9 @@ def _time_graph(dev: Device, launches, reps: int) -> float:
         dev.graph_launch(g)
     dev.record(e1)
     dev.sync()
-    return dev.elapsed_ms(e0, e1) / reps
+    ms = dev.elapsed_ms(e0, e1) / reps
+    dev.graph_destroy(g)
+    return ms
 
 
 def _copies(dev: Device, host: np.ndarray, total_min: int, at_least: int = 1):
@@ -139,6 +155,12 @@ def config2_layer(dev: Device, n: int = 5, graphs: int = 10) -> dict:
         algo = wbytes + sum(n * c + 8 * n * (c // 32) + 4 * n * r for r, c in shapes.values())
         res[kind] = dict(_line(algo, us), weight_bytes=wbytes, algorithmic_bytes=algo,
                          launches_per_layer=4, copies=ncopy)
+        # the same over copies that fit the MALL (about 160 MB: above the L2s, below 256 MB)
+        full = layers
+        layers = full[:max(2, (160 << 20) // wbytes)]
+        us_m = _time_graph(dev, launches, graphs) / len(layers) * 1e3
+        res[kind]["mall_resident"] = dict(_line(algo, us_m), copies=len(layers))
+        layers = full
         for L in layers:
             for b in L.values():
                 b.free()

@@ -270,6 +270,9 @@ class Device:
             raise NmxError(f"graph end: {self.lib.nmx_error(self.ctx).decode()}")
         return g
 
+    def graph_destroy(self, g: int) -> None:
+        self.lib.nmx_graph_destroy(g)
+
     def graph_launch(self, g: int) -> None:
         self.check(self.lib.nmx_graph_launch(self.ctx, g), "graph launch")
 
