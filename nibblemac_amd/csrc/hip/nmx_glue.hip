@@ -722,52 +722,74 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
  * consecutive workgroups go to different XCDs (round-robin), so the workgroups reading one
  * slice share one XCD's L2. The scores row and the first PV_PT value rows are requested at
  * entry; each tile lands in LDS as w_p v_p[d] (the products the chain adds). Wave 0's lanes
- * run the chains (one per dimension), reading 3 batches of 8 positions ahead of the adds; while
- * wave 0 runs a tile's chains, waves 1-3 load the next PV_PT2 rows. */
-constexpr int PV_DS = 64;           /* output dims per workgroup: two A8 blocks */
-constexpr int PV_PT = 448;          /* positions of the first tile */
-constexpr int PV_PT2 = 192;         /* positions of each later tile (loaded by waves 1-3) */
+ * run the chains (one per dimension), reading batches of 8 positions ahead of the adds; while
+ * wave 0 runs a tile's chains, waves 1-3 load the next PV_PT2 rows. A dependent fp32 add costs
+ * 11-17 cycles in wave 0, so the chains bound the kernel; 32 dims per workgroup give twice
+ * the workgroups of 64, and a first tile of PV_PT positions keeps a workgroup's LDS under half
+ * of the CU's for contexts up to 1024 positions, so two workgroups share a CU and a 5-token
+ * verify pass (320 workgroups) runs in one round. */
+constexpr int PV_DS = 32;           /* output dims per workgroup: one A8 block */
+constexpr int PV_PT = 576;          /* positions of the first tile */
+constexpr int PV_PT2 = 384;         /* positions of each later tile (loaded by waves 1-3) */
 constexpr int PV_PER = PV_PT * (PV_DS / 4) / 256;    /* float4 loads per thread, first tile */
 constexpr int PV_PER2 = PV_PT2 * (PV_DS / 4) / 192;  /* per thread of waves 1-3, later tiles */
 
 /* acc += x[0] + ... + x[n-1] in order, x[i] = p[i * stride] in LDS, with the reads of 3
- * batches of 8 in flight ahead of the adds (at most 12 LDS reads outstanding). The scheduling
- * barriers keep each batch's reads where they are issued: left alone, the scheduler sinks
- * them to just before their adds, and every batch then waits the full LDS latency. */
+ * batches of 8 in flight ahead of the adds (at most 16 LDS reads outstanding). Each batch is
+ * four register pairs: two reads of one pair merge into one ds_read2 that lands in the pair
+ * itself, so the loop-carried batches need no register copies (with scalar batches the
+ * merged reads landed in fresh registers and were copied at the loop's end, which waited for
+ * every read in flight). The scheduling barriers keep each batch's reads where they are
+ * issued: left alone, the scheduler sinks them to just before their adds. */
+__device__ __forceinline__ void pv_load8(float2 (&X)[4], const float *p, int stride, int r) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) X[u] = make_float2(p[(r + 2 * u) * stride], p[(r + 2 * u + 1) * stride]);
+}
+
+__device__ __forceinline__ float pv_add8(float acc, const float2 (&X)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        acc = acc + X[u].x;
+        acc = acc + X[u].y;
+    }
+    return acc;
+}
+
 __device__ __forceinline__ float pv_chain(float acc, const float *p, int stride, int n) {
     int r = 0;
-    if (n >= 24) {
-        float A[8], B[8], C[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) A[u] = p[u * stride], B[u] = p[(8 + u) * stride];
-        for (; r + 24 <= n; r += 24) {
-            /* A = r .. r+7, B = r+8 .. r+15 loaded; reads past n are clamped (not used) */
-            const int c0 = r + 16, a0 = r + 24 + 8 <= n ? r + 24 : r, b0 = r + 32 + 8 <= n ? r + 32 : r;
-#pragma unroll
-            for (int u = 0; u < 8; u++) C[u] = p[(c0 + u) * stride];
+    if (n >= 32) {
+        float2 A[4], B[4], C[4], D[4];
+        pv_load8(A, p, stride, 0);
+        pv_load8(B, p, stride, 8);
+        pv_load8(C, p, stride, 16);
+        for (; r + 32 <= n; r += 32) {
+            /* A, B, C = rows r .. r+23 loaded; reads past n are clamped (not used) */
+            const int d0 = r + 24, a0 = r + 40 <= n ? r + 32 : r, b0 = r + 48 <= n ? r + 40 : r,
+                      c0 = r + 56 <= n ? r + 48 : r;
+            pv_load8(D, p, stride, d0);
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc = acc + A[u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) A[u] = p[(a0 + u) * stride];
+            acc = pv_add8(acc, A);
+            pv_load8(A, p, stride, a0);
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc = acc + B[u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) B[u] = p[(b0 + u) * stride];
+            acc = pv_add8(acc, B);
+            pv_load8(B, p, stride, b0);
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc = acc + C[u];
+            acc = pv_add8(acc, C);
+            pv_load8(C, p, stride, c0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_add8(acc, D);
         }
-        /* A holds r .. r+7 and B r+8 .. r+15 when those are in range */
+        /* A, B, C hold r .. r+23 when those are in range */
         if (r + 8 <= n) {
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc = acc + A[u];
+            acc = pv_add8(acc, A);
             r += 8;
             if (r + 8 <= n) {
-#pragma unroll
-                for (int u = 0; u < 8; u++) acc = acc + B[u];
+                acc = pv_add8(acc, B);
                 r += 8;
+                if (r + 8 <= n) {
+                    acc = pv_add8(acc, C);
+                    r += 8;
+                }
             }
         }
     }
