@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of speculative greedy decoding (draft k = 4, verify + commit) on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-kernels]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-kernels] [--no-accept]
                     [--head-only [--eager] [--copy-mib M]]
 
 Workload (config 5): a 0.8B-shaped Qwen3.5 hybrid (24 layers: 18 Gated DeltaNet + 6 gated full
@@ -19,7 +19,10 @@ stream it runs on. `kernels` holds configs 1-4 (nibblemac_amd/kbench.py). `cpu_b
 reference engine's own sources with the oracle's threaded Q4K operators
 (oracle/_ref/libpinfer_refq4k.so) on the host cores: the config-5 workload itself on the GPU
 box's CPU share (16 threads), its tokens checked against the GPU's, plus a 1-thread run on a
-bounded sample and the oracle's Q4K matvec of config 1 on 1 thread.
+bounded sample and the oracle's Q4K matvec of config 1 on 1 thread. With random weights the
+drafts are essentially never accepted; `accepting` times the same workload on the same weights
+with final norms that make the drafts agree (multi-token commits and deferred DeltaNet replays),
+its tokens checked against plain greedy decoding.
 """
 from __future__ import annotations
 
@@ -48,6 +51,38 @@ N_PROMPT, N_GEN = 512, 128
 CPU_SHARE = 16                       # host threads of one GPU's share of the box
 ONE_PROMPT, ONE_GEN = 16, 5          # the bounded 1-thread sample
 TRAFFIC_FILE = ROOT / "profiles" / "q4k_head_n5_fused_traffic.json"
+
+
+def accepting_leg(tmp: str, prompt: np.ndarray, steps: int) -> dict:
+    """The same workload on the same shape with final norms that make the MTP drafts agree
+    (pqfile.agreeing_norm) and an untied head whose rows past the draft vocabulary are
+    N(0, 0.002) (otherwise the same random-init weights), so that multi-token commits and the
+    deferred DeltaNet replays run inside the timed rounds. Its tokens are checked against plain
+    greedy decoding (k = 0) of the same model."""
+    w = pqfile.agreeing_norm(QWEN35_08B.hidden)
+    path = Path(tmp) / "qwen35_08b_shape_q4k_agree.pq"
+    pqfile.write_model(path, QWEN35_08B, seed=1, overrides={"norm.weight": w,
+                                                            "mtp.norm.weight": w},
+                       lm_head=(DRAFT_VOCAB, 0.002))
+    with Model(str(path), max_ctx=1024) as gpu:
+        plain, _, _, td0 = gpu.bench_generate(prompt, N_GEN, 0, DRAFT_VOCAB)
+        gpu.bench_generate(prompt, N_GEN, K_DRAFT, DRAFT_VOCAB)
+        dec, rounds, drafted, accepted = 0.0, 0, 0, 0
+        for _ in range(steps):
+            toks, st, _, td = gpu.bench_generate(prompt, N_GEN, K_DRAFT, DRAFT_VOCAB)
+            if toks != plain:
+                raise SystemExit("bench.py: accepting leg: speculative tokens differ from greedy")
+            dec, rounds = dec + td, rounds + st.rounds
+            drafted, accepted = drafted + st.drafted, accepted + st.accepted
+    leg = {"workload": "as config; final norms pqfile.agreeing_norm, untied head with rows "
+                       f">= {DRAFT_VOCAB} N(0, 0.002) (drafts agree)",
+           "tok_s": round(steps * (N_GEN - 1) / dec, 2), "steps": steps,
+           "rounds_per_step": rounds / steps, "drafted": drafted // steps,
+           "accepted": accepted // steps,
+           "tokens_per_pass": round(steps * (N_GEN - 1) / rounds, 3),
+           "ms_per_pass": round(dec / rounds * 1e3, 4),
+           "plain_k0_tok_s": round((N_GEN - 1) / td0, 2), "tokens_match_greedy": True}
+    return leg
 
 
 def log(msg: str) -> None:
@@ -168,6 +203,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 1-4 lines")
+    ap.add_argument("--no-accept", action="store_true", help="skip the accepting-drafts leg")
     ap.add_argument("--head-only", action="store_true",
                     help="only the in-path LM head launches (for counter runs)")
     ap.add_argument("--kernels-only", action="store_true", help="only the config 1-4 lines")
@@ -213,6 +249,10 @@ def main() -> int:
                     f"{(N_GEN - 1) / td:.1f} tok/s, rounds {st.rounds} accepted {st.accepted}")
             tps = a.steps * (N_GEN - 1) / dec
         cpu = None if a.no_cpu else cpu_baseline(path, (first, first_st), prompt)
+        accept = None
+        if not a.no_accept:
+            accept = accepting_leg(tmp, prompt, a.steps)
+            log(f"accepting leg: {json.dumps(accept)}")
     roof = head_roofline()
     log(f"head (in path, cold): {roof['us_per_launch']} us, {roof['achieved']} GB/s")
     kernels = None
@@ -238,7 +278,7 @@ def main() -> int:
                  "tokens_per_pass": round((N_GEN - 1) / rounds, 3) if rounds else None,
                  "ms_per_pass": round(dec / stats[0] * 1e3, 4) if stats[0] else None},
         "prefill_tok_s": round(a.steps * N_PROMPT / pre, 1),
-        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels,
+        "roofline": roof, "cpu_baseline": cpu, "accepting": accept, "kernels": kernels,
     }
     print(json.dumps(rec), flush=True)
     return 0

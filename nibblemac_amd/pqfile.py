@@ -23,11 +23,13 @@ ENTRY_FMT = "<80sII4IQQ8x"                 # one 128-byte directory entry
 F32, BF16, Q4K = 0, 1, 4
 
 
-def tensors(shape: Shape, seed: int, random_norms: bool, mtp: bool = True):
+def tensors(shape: Shape, seed: int, random_norms: bool, mtp: bool = True,
+            lm_head: tuple[int, float] | None = None):
     """(name, dtype, dims, producer) for every tensor the engine maps, in file order. Matrices
     are N(0, 0.02) packed as Q4K; norms 1 (or U(0.8, 1.2) with random_norms); conv weights
     U(-0.5, 0.5); A_log / dt_bias so that the decay exp(-exp(A_log) softplus(a + dt_bias))
-    stays in (0.9, 1) for |a| up to ~3."""
+    stays in (0.9, 1) for |a| up to ~3. lm_head = (rows, std): an untied output head whose
+    first `rows` rows are N(0, 0.02) and the others N(0, std)."""
     rng = np.random.default_rng(seed)
     H, F = shape.hidden, shape.ffn
     stream = [0]
@@ -82,6 +84,14 @@ def tensors(shape: Shape, seed: int, random_norms: bool, mtp: bool = True):
         vec(p + "linear_attn.conv1d.weight", [shape.conv_dim, shape.conv_k], -0.5, 0.5)
 
     mat("embed_tokens.weight", shape.vocab, H)
+    if lm_head:
+        hot, std = lm_head
+        if hot % 4 or not 0 < hot < shape.vocab:
+            raise ValueError(f"lm_head rows {hot}: a multiple of 4 inside the vocabulary")
+        s = 1 << 20  # streams of their own: every other tensor keeps its values
+        out.append(("lm_head.weight", Q4K, [shape.vocab, H], lambda s=s: np.concatenate(
+            [pqtool.gauss_q4k(seed, s, hot, H, 0.02),
+             pqtool.gauss_q4k(seed, s + 1, shape.vocab - hot, H, std)])))
     norm("norm.weight", H)
     for i in range(shape.layers):
         block(f"layers.{i}.", shape.is_full(i))
@@ -101,11 +111,12 @@ def nbytes(dtype: int, dims: list[int]) -> int:
 
 def write_model(path: str | os.PathLike, shape: Shape = QWEN35_08B, seed: int = 1,
                 random_norms: bool = False, mtp: bool = True,
-                overrides: dict[str, np.ndarray] | None = None) -> Path:
+                overrides: dict[str, np.ndarray] | None = None,
+                lm_head: tuple[int, float] | None = None) -> Path:
     """Write a synthetic model; returns the path. `overrides` replaces the values of named F32
-    tensors (same element count)."""
+    tensors (same element count); `lm_head` writes an untied output head (see tensors)."""
     path = Path(path)
-    ts = tensors(shape, seed, random_norms, mtp)
+    ts = tensors(shape, seed, random_norms, mtp, lm_head)
     for name, value in (overrides or {}).items():
         i = next((i for i, t in enumerate(ts) if t[0] == name), None)
         if i is None or ts[i][1] != F32:
@@ -122,7 +133,8 @@ def write_model(path: str | os.PathLike, shape: Shape = QWEN35_08B, seed: int = 
     hdr = struct.pack(HEADER_FMT, MAGIC, 1, len(ts), dir_off, data_off, 1, shape.hidden,
                       shape.layers, shape.vocab, shape.ffn, shape.n_heads, shape.n_kv,
                       shape.head_dim, shape.rot, shape.lin_k_heads, shape.lin_v_heads,
-                      shape.lin_k_dim, shape.lin_v_dim, shape.conv_k, mask, shape.eos_id, 1,
+                      shape.lin_k_dim, shape.lin_v_dim, shape.conv_k, mask, shape.eos_id,
+                      0 if lm_head else 1,
                       1 if mtp else 0, shape.rms_eps, shape.rope_theta)
     with path.open("wb") as f:
         f.write(hdr.ljust(4096, b"\0"))
@@ -135,6 +147,18 @@ def write_model(path: str | os.PathLike, shape: Shape = QWEN35_08B, seed: int = 
             assert data.nbytes == nbytes(dt, dims), name
             f.write(data.tobytes())
     return path
+
+
+def agreeing_norm(hidden: int, j: int = 2) -> np.ndarray:
+    """A final-norm weight vector that keeps (almost) only hidden coordinate j: the logits are
+    then about x_j * head[:, j], so the main model and the MTP head (both read through the same
+    head) pick one of the same two tokens, by the sign of their x_j, and MTP drafts are often
+    accepted. Pass it as the override of both "norm.weight" and "mtp.norm.weight". When the
+    drafts are restricted to the first rows of the head, write an untied head whose other rows
+    are small (write_model's lm_head), so that the main model's choice lies among them too."""
+    w = np.full(hidden, 1e-3, np.float32)
+    w[j] = 1.0
+    return w
 
 
 SMALL = replace(QWEN35_08B, hidden=256, layers=4, ffn=768, vocab=2048, n_heads=4, n_kv=2,

@@ -30,17 +30,6 @@ def dev():
     d.close()
 
 
-def agreeing_norm(hidden: int, j: int = 2) -> "np.ndarray":
-    """A final-norm weight vector that keeps (almost) only hidden coordinate j: the logits are
-    then about x_j * head[:, j], so the main model and the MTP head (both read through the same
-    head) pick one of the same two tokens, by the sign of their x_j."""
-    import numpy as np
-
-    w = np.full(hidden, 1e-3, np.float32)
-    w[j] = 1.0
-    return w
-
-
 @pytest.fixture(scope="session")
 def agree_model(tmp_path_factory):
     """(path, prompt): a small synthetic model (the 0.8B layer pattern) whose MTP drafts are
@@ -52,7 +41,7 @@ def agree_model(tmp_path_factory):
 
     from nibblemac_amd import pqfile
 
-    w = agreeing_norm(pqfile.SMALL.hidden)
+    w = pqfile.agreeing_norm(pqfile.SMALL.hidden)
     d = tmp_path_factory.mktemp("agree")
     path = pqfile.write_model(d / "agree.pq", pqfile.SMALL, seed=3, random_norms=True,
                               overrides={"norm.weight": w, "mtp.norm.weight": w})
