@@ -140,6 +140,15 @@ int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
                        const float *d, const float *fsum, float *logits, const int32_t *drafts,
                        void *work, int32_t *out, int32_t *tok_dst);
 
+/* nmx_head_accept followed by the commit of the accepted run in the same last kernel: what
+ * nmx_accept_commit_mb (mailbox != NULL, nvt >= n + 1) or nmx_accept_commit (mailbox NULL)
+ * does after it (engine/src/spec.c:340-351: the acceptance loop, then vt[a + 1] = bonus and
+ * e = a + 1), without the extra launch. No logits. */
+int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int n,
+                           const int8_t *q, const float *d, const float *fsum,
+                           const int32_t *drafts, void *work, int32_t *out, int32_t *vt,
+                           int32_t *ctl, int32_t *mailbox, int nvt);
+
 /* nmx_head_accept without the workspace argument: allocates nothing and takes no workspace.
  * No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The

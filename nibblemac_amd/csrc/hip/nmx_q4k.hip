@@ -342,18 +342,32 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
     }
 }
 
+/* The commit of the accepted run that head_finish_k can apply itself (engine/src/spec.c:
+ * 346-351): vt[a + 1] = bonus, ctl[1] = e = a + 1, and the host mailbox [a, bonus, vt[0..nvt)
+ * after the update] followed by mb[2 + nvt] = 1 with a system-scope release. vt NULL: none. */
+struct FinishCommit {
+    int32_t *vt, *ctl, *mb;
+    int nvt;
+};
+
 /* Argmax of every row from the per-workgroup partial keys, then the acceptance loop of the
  * reference (engine/src/spec.c:340-345): a = 0; g = argmax(row 0); while a < k and
- * drafts[a] == g: a++, g = argmax(row a). out = [a, g, argmax(row 0..n-1)]. One workgroup of
- * 1024 threads; every partial is loaded once, all loads issued before the reduction. */
+ * drafts[a] == g: a++, g = argmax(row a). out = [a, g, argmax(row 0..n-1)]; then the commit
+ * fc when given. One workgroup of 1024 threads; the drafts (and vt for the mailbox) are
+ * requested first, every partial is loaded once, all loads issued before the reduction, so
+ * the acceptance loop reads LDS only. */
 __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *__restrict__ keys,
                                                       int nblk, int n,
-                                                      const int32_t *__restrict__ drafts,
+                                                      const int32_t *drafts,
                                                       int32_t *__restrict__ out,
-                                                      int32_t *__restrict__ tok_dst) {
+                                                      int32_t *__restrict__ tok_dst,
+                                                      FinishCommit fc) {
     __shared__ unsigned long long red[16][8];
-    __shared__ int am[64];
+    __shared__ int am[64], sdr[64], svt[1024];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int dr = drafts && tid < n - 1 ? drafts[tid] : 0;
+    const int vv = fc.mb && tid < fc.nvt ? fc.vt[tid] : 0;
+    bool staged = false;
     for (int t0 = 0; t0 < n; t0 += 8) {
         unsigned long long k[8];
 #pragma unroll
@@ -372,6 +386,11 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
             k[j] = nmx_max_u64_wave(k[j]);
             if (lane == 0) red[wv][j] = k[j];
         }
+        if (!staged) { /* the keys' loads waited for these (issued first) */
+            if (tid < n - 1) sdr[tid] = dr;
+            if (tid < fc.nvt) svt[tid] = vv;
+            staged = true;
+        }
         __syncthreads();
         if (tid < 8 && t0 + tid < n) {
             unsigned long long m = red[0][tid];
@@ -382,7 +401,7 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
     }
     if (tid == 0) {
         int a = 0, g = am[0];
-        while (a < n - 1 && drafts[a] == g) {
+        while (a < n - 1 && sdr[a] == g) {
             a++;
             g = am[a];
         }
@@ -390,6 +409,16 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
         out[1] = g;
         for (int t = 0; t < n; t++) out[2 + t] = am[t];
         if (tok_dst) *tok_dst = g;
+        if (fc.vt) {
+            fc.vt[a + 1] = g;
+            fc.ctl[1] = a + 1;
+            if (fc.mb) {
+                fc.mb[0] = a;
+                fc.mb[1] = g;
+                for (int i = 0; i < fc.nvt; i++) fc.mb[2 + i] = i == a + 1 ? g : svt[i];
+                __hip_atomic_store(fc.mb + 2 + fc.nvt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
     }
 }
 
@@ -919,9 +948,9 @@ int nmx_head_accept_noalloc(nmx_ctx *ctx, const void *W, int rows, int cols, int
                               nullptr);
 }
 
-int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+static int head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
                        const float *d, const float *fsum, float *logits, const int32_t *drafts,
-                       void *work, int32_t *out, int32_t *tok_dst) {
+                       void *work, int32_t *out, int32_t *tok_dst, FinishCommit fc) {
     if (!ctx) return -1;
     if (!W || !q || !d || !fsum || !work || !out || (n > 1 && !drafts))
         return nmx_fail(ctx, "nmx_head_accept: NULL pointer");
@@ -946,9 +975,27 @@ int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
     const int blocks = (tab.total_waves + 3) / 4;
     unsigned long long *keys = (unsigned long long *)work;
     if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, keys)) return -1;
-    head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out, tok_dst);
+    head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out, tok_dst, fc);
     NMX_LAUNCHED(ctx, "head_finish");
     return 0;
+}
+
+int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                       const float *d, const float *fsum, float *logits, const int32_t *drafts,
+                       void *work, int32_t *out, int32_t *tok_dst) {
+    return head_accept(ctx, W, rows, cols, n, q, d, fsum, logits, drafts, work, out, tok_dst,
+                       FinishCommit{nullptr, nullptr, nullptr, 0});
+}
+
+int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int n,
+                           const int8_t *q, const float *d, const float *fsum,
+                           const int32_t *drafts, void *work, int32_t *out, int32_t *vt,
+                           int32_t *ctl, int32_t *mailbox, int nvt) {
+    if (!ctx) return -1;
+    if (!vt || !ctl || (mailbox && (nvt < n + 1 || nvt > 1024)))
+        return nmx_fail(ctx, "nmx_head_accept_commit: bad arguments");
+    return head_accept(ctx, W, rows, cols, n, q, d, fsum, nullptr, drafts, work, out, nullptr,
+                       FinishCommit{vt, ctl, mailbox, mailbox ? nvt : 0});
 }
 
 } /* extern "C" */

@@ -146,7 +146,9 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
         if ((rc = mlp_block(c, L, n, &r))) return rc;
     }
     CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->norm, n, H, c->rms_eps, s->xn, H, s->a_h));
-    CK(nmx_ctl_set(D, c->ctl, 2, 0)); /* every linear layer applied the pending rows */
+    /* every linear layer applied the pending rows: keep = 0, except after a logged pass, which
+     * the commit always follows and whose kernel sets keep = e - 1 itself */
+    if (!logged) CK(nmx_ctl_set(D, c->ctl, 2, 0));
     return PINFER_OK;
 }
 

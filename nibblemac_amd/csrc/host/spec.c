@@ -64,9 +64,9 @@ static float *m_ping(pinfer_ctx *c, int i) { return c->mbuf + (size_t)(1 + (i & 
 static int seq_verify(pinfer_ctx *c, int ke) {
     TRY(e_forward(c, c->vt, ke + 1, 1));
     e_scratch *sc = &c->s;
-    CK(nmx_head_accept(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
-                       NULL, c->vt + 1, c->hwork, c->hout));
-    CK(nmx_accept_commit_mb(c->dev, c->hout, c->vt, c->ctl, c->mbox, ke + 2));
+    CK(nmx_head_accept_commit(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d,
+                              sc->a_h.fs, c->vt + 1, c->hwork, c->hout, c->vt, c->ctl, c->mbox,
+                              ke + 2));
     return PINFER_OK;
 }
 

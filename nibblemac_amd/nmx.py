@@ -95,6 +95,8 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_accept_to": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_accept_noalloc": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nmx_head_accept_commit": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                    _vp, _vp, _i]),
     "nmx_accept_commit": (_i, [_vp, _vp, _vp, _vp]),
     "nmx_accept_commit_mb": (_i, [_vp, _vp, _vp, _vp, _vp, _i]),
     "nmx_host_alloc": (_vp, [_vp, _sz]),
@@ -393,6 +395,14 @@ class Device:
         self.check(self.lib.nmx_head_accept_noalloc(self.ctx, _p(W), rows, cols, n, _p(q), _p(d),
                                                     _p(fs), _p(logits), _p(drafts), _p(out)),
                    "head_accept_noalloc")
+
+    def head_accept_commit(self, W, rows: int, cols: int, n: int, q, d, fs, drafts, work, out,
+                           vt, ctl, mailbox=None, nvt: int = 0) -> None:
+        """nmx_head_accept_commit: the head, the acceptance and the commit of the accepted run
+        (vt, ctl and, when given, the host mailbox) in one launch sequence."""
+        self.check(self.lib.nmx_head_accept_commit(self.ctx, _p(W), rows, cols, n, _p(q), _p(d),
+                                                   _p(fs), _p(drafts), _p(work), _p(out), _p(vt),
+                                                   _p(ctl), mailbox, nvt), "head_accept_commit")
 
     def accept_commit(self, out, vt, ctl, mailbox=None, nvt: int = 0) -> None:
         """nmx_accept_commit, or nmx_accept_commit_mb writing the host mailbox."""

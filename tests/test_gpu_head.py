@@ -184,6 +184,62 @@ def test_accept_commit_mailbox(dev, a):
             b.free()
 
 
+@pytest.mark.parametrize("accept,mailbox", [(0, True), (2, True), (4, True), (3, False)])
+def test_head_accept_commit_equals_two_launches(dev, accept, mailbox):
+    """nmx_head_accept_commit (the accept commit inside the head's last kernel) against
+    nmx_head_accept + nmx_accept_commit(_mb) on the same inputs: out, vt, ctl and the mailbox
+    identical, the drafts being vt[1..k] as in the verify round."""
+    import ctypes
+
+    print(f"[case] head_accept_commit accept={accept} mailbox={mailbox}", flush=True)
+    rng = np.random.default_rng(70 + accept)
+    rows, cols, k = 32768, 1024, 4
+    n = k + 1
+    W = quantized_head(rng, rows, cols)
+    X = rng.standard_normal((n, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, n, threads=8)
+    am = np.array([oracle.argmax(ref[t]) for t in range(n)], np.int32)
+    vt0 = np.concatenate([[12345], planted_drafts(am, accept, k)]).astype(np.int32)
+    dW, dq, dd, dfs = dev.to_device(W), dev.to_device(q), dev.to_device(d), dev.to_device(fs)
+    nvt = k + 2
+    got = []
+    for fused in (False, True):
+        vt = dev.to_device(np.concatenate([vt0, [-1]]).astype(np.int32))
+        ctl = dev.to_device(np.full(16, 9, np.int32))
+        work = dev.zeros(dev.head_work_bytes(rows, n), np.uint8)
+        out = dev.zeros(2 + n, np.int32)
+        mb = dev.host_alloc((3 + nvt) * 4) if mailbox else None
+        try:
+            if mb:
+                view = (ctypes.c_int32 * (3 + nvt)).from_address(mb)
+                for i in range(3 + nvt):
+                    view[i] = -7
+                view[2 + nvt] = 0
+            if fused:
+                dev.head_accept_commit(dW, rows, cols, n, dq, dd, dfs, vt.ptr + 4, work, out, vt,
+                                       ctl, mailbox=mb, nvt=nvt if mb else 0)
+            else:
+                dev.head_accept(dW, rows, cols, n, dq, dd, dfs, None, vt.ptr + 4, work, out)
+                dev.accept_commit(out, vt, ctl, mailbox=mb, nvt=nvt)
+            dev.sync()
+            got.append((out.numpy(), vt.numpy(), ctl.numpy(), list(view) if mb else None))
+        finally:
+            if mb:
+                dev.host_free(mb)
+            for b in (vt, ctl, work, out):
+                b.free()
+    for b in (dW, dq, dd, dfs):
+        b.free()
+    (o0, v0, c0, m0), (o1, v1, c1, m1) = got
+    a_ref, bonus_ref, _ = oracle.accept(ref, vt0[1:])
+    assert o0[0] == a_ref == accept and o0[1] == bonus_ref
+    assert np.array_equal(o0, o1) and np.array_equal(v0, v1) and np.array_equal(c0, c1)
+    assert v1[accept + 1] == bonus_ref and c1[1] == accept + 1
+    if mailbox:
+        assert m0 == m1 and m1[-1] == 1 and m1[:2] == [accept, bonus_ref]
+
+
 def test_head_accept_to_writes_token(dev):
     """nmx_head_accept_to stores out[1] (the greedy token) at tok_dst as well."""
     rng = np.random.default_rng(5)
