@@ -228,9 +228,10 @@ __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >
  * whose A entries must be zero read the zero copy. Each block's operand reads are ordered
  * after the previous block's chain steps (an empty asm on the LDS offset), and each superblock's
  * weight loads after the last one's. Left alone, the compiler hoists every block's MFMAs and
- * holds all their results, which halves the waves per SIMD. */
-template <int NV, bool AMAX>
-__global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, int v0,
+ * holds all their results, which halves the waves per SIMD. WPG waves per workgroup share one
+ * table and one partial argmax key per vector. */
+template <int NV, bool AMAX, int WPG>
+__global__ __launch_bounds__(64 * WPG) void q4k_mvx_k(SegTable tab, int cols, int n, int v0,
                                                  const int8_t *__restrict__ q,
                                                  const float *__restrict__ d,
                                                  const float *__restrict__ fs,
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
     typedef int v16i __attribute__((ext_vector_type(16)));
     extern __shared__ __align__(16) uint8_t xt[];
     const int nb = cols >> 5, ent = nb * 2 * NV, tbytes = ent * 16;
-    const int wave_raw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wave_raw = blockIdx.x * WPG + (threadIdx.x >> 6);
     const bool wave_live = wave_raw < tab.total_waves; /* every wave reaches the barrier */
     const int wave = wave_live ? wave_raw : tab.total_waves - 1;
     const int lane = threadIdx.x & 63;
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
 #pragma unroll
     for (int k = 0; k < 8; k++) c[k] = tp[4 + 4 * k + i];
 
-    for (int e = threadIdx.x; e < ent; e += 256) {
+    for (int e = threadIdx.x; e < ent; e += 64 * WPG) {
         const int v = e % NV, bp = e / NV, h = bp & 1, blk = bp >> 1;
         const uint32_t *x = (const uint32_t *)(q + ((size_t)blk * n + v0 + v) * 32);
         *(uint4 *)(xt + (size_t)e * 16) = make_uint4(x[2 * h], x[4 + 2 * h], x[2 * h + 1], x[5 + 2 * h]);
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
         for (int v = 0; v < NV; v++) Y[(size_t)(v0 + v) * ystride + row] = acc[v];
     }
     if (AMAX) { /* as in q4k_mv_k */
-        __shared__ unsigned long long wkeys[4][MAX_NV];
+        __shared__ unsigned long long wkeys[WPG][MAX_NV];
         const int wv = threadIdx.x >> 6;
 #pragma unroll
         for (int v = 0; v < NV; v++) {
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(256) void q4k_mvx_k(SegTable tab, int cols, int n, 
         __syncthreads();
         if (threadIdx.x < NV) {
             unsigned long long key = wkeys[0][threadIdx.x];
-            for (int w = 1; w < 4; w++) key = wkeys[w][threadIdx.x] > key ? wkeys[w][threadIdx.x] : key;
+            for (int w = 1; w < WPG; w++) key = wkeys[w][threadIdx.x] > key ? wkeys[w][threadIdx.x] : key;
             amax_key[(size_t)(v0 + threadIdx.x) * gridDim.x + blockIdx.x] = key;
         }
     }
@@ -701,18 +702,51 @@ __global__ __launch_bounds__(256) void quant_a8_k(const float *__restrict__ X, i
     nmx_a8_store(x, q + (size_t)unit * 32, d + unit, fs + unit);
 }
 
+/* Waves per workgroup of the matrix-core matvec: 16 (one 1024-thread workgroup per CU: one
+ * activation table per CU instead of about four, and a quarter of the partial argmax keys for
+ * the reduction) once the row groups fill MVX_BIG_WAVES waves, else 4 (more CUs for smaller
+ * matrices). */
+constexpr int MVX_BIG_WAVES = 16 * 200;
+
+bool mvx_used(int nv, int cols, bool dots) { return nv >= 3 && !dots && (size_t)2 * nv * cols <= 65536; }
+
+/* Vectors of the next pass: n vectors in ceil(n / MAX_NV) passes of equal size (+-1), larger
+ * first, like the reference's VECTOR_PASSES (engine/src/kern_quant.c:258-274). */
+int pass_nv(int left) {
+    const int np = (left + MAX_NV - 1) / MAX_NV;
+    return (left + np - 1) / np;
+}
+
+/* Waves per workgroup of every pass of an n-vector row-per-lane launch: 16 only when every
+ * pass runs the matrix-core kernel on enough row groups, so the partial argmax keys of all
+ * passes have one layout ([vector][workgroups]). */
+int mv_wpg(const SegTable &tab, int n, int cols, bool dots) {
+    if (tab.total_waves < MVX_BIG_WAVES) return 4;
+    for (int v = 0; v < n;) {
+        const int nv = pass_nv(n - v);
+        if (!mvx_used(nv, cols, dots)) return 4;
+        v += nv;
+    }
+    return 16;
+}
+
 template <int NV>
 void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
-               const float *d, const float *fs, int32_t *dots, unsigned long long *am) {
-    const unsigned blocks = (unsigned)((tab.total_waves + 3) / 4);
+               const float *d, const float *fs, int32_t *dots, unsigned long long *am, int wpg) {
+    const unsigned blocks = (unsigned)((tab.total_waves + wpg - 1) / wpg);
     /* 3 or more vectors: the block dots on the matrix cores (bit-identical results; measured at
      * 248320 x 1024, 5 vectors: 30 us against 34-38 us), while its activation table fits in
      * the default 64 KB of LDS */
     if constexpr (NV >= 3) {
         const size_t xbytes = (size_t)2 * NV * cols;
-        if (!dots && xbytes <= 65536) {
-            if (am) q4k_mvx_k<NV, true><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
-            else q4k_mvx_k<NV, false><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+        if (mvx_used(NV, cols, dots != nullptr)) {
+            if (wpg == 16) {
+                if (am) q4k_mvx_k<NV, true, 16><<<blocks, 1024, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+                else q4k_mvx_k<NV, false, 16><<<blocks, 1024, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+            } else {
+                if (am) q4k_mvx_k<NV, true, 4><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+                else q4k_mvx_k<NV, false, 4><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
+            }
             return;
         }
     }
@@ -786,20 +820,20 @@ int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8
     }
     if (!am && total_rows < KSPLIT_MAX_ROWS && cols <= 16 * 2 * 256)
         return launch_ksplit(ctx, tab, tab.total_waves, cols, n, q, d, fs, dots);
-    /* n vectors in ceil(n / MAX_NV) passes of equal size (+-1), larger first, like the
-     * reference's VECTOR_PASSES (engine/src/kern_quant.c:258-274): every pass performs the same
-     * per-vector operations, so the result does not depend on the split. */
+    /* every pass performs the same per-vector operations, so the result does not depend on
+     * the split (pass_nv) */
+    const int wpg = mv_wpg(tab, n, cols, dots != nullptr);
     for (int v = 0; v < n;) {
-        const int left = n - v, np = (left + MAX_NV - 1) / MAX_NV, nv = (left + np - 1) / np;
+        const int nv = pass_nv(n - v);
         switch (nv) {
-        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
-        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am); break;
+        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
         }
         NMX_LAUNCHED(ctx, "q4k_mv");
         v += nv;
@@ -972,7 +1006,8 @@ static int head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
     tab.s[0] = Seg{(const uint8_t *)W, logits, rows, rows, 0, 0};
     tab.total_waves = (rows + 63) / 64;
     if ((uintptr_t)work % 8) return nmx_fail(ctx, "nmx_head_accept: work not 8-byte aligned");
-    const int blocks = (tab.total_waves + 3) / 4;
+    const int wpg = mv_wpg(tab, n, cols, false);
+    const int blocks = (tab.total_waves + wpg - 1) / wpg; /* launch_passes' workgroups */
     unsigned long long *keys = (unsigned long long *)work;
     if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, keys)) return -1;
     head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out, tok_dst, fc);
