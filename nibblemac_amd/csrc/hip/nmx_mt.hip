@@ -34,7 +34,8 @@ constexpr int MT_MAX_THREADS = 512; /* the SwiGLU launch (64 rows; the dots' VGP
 constexpr int MT_LDS = 159 * 1024; /* dynamic LDS per workgroup (gfx950: 160 KB) */
 constexpr int MT_NORM_CPT = 8; /* columns per thread in the norm prologue */
 constexpr int MT_NORM_THREADS = 512; /* the prologue keeps NV x MT_NORM_CPT values in VGPRs */
-constexpr int MT_REC_THREADS = 256;  /* record launches (8 or 4 rows): room for VGPR buffers */
+constexpr int MT_REC_THREADS = 1024; /* record launches of one-block units */
+constexpr int MT_REC4_THREADS = 256; /* record launches of 4-block units: room for VGPR buffers */
 
 struct MtTab {
     nmx_mt_seg s[NMX_MAX_SEGS];
@@ -94,8 +95,8 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     return L;
 }
 
-template <int NV, bool NORM, bool SWI>
-__global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_REC_THREADS) void q4k_mt_k(
+template <int NV, bool NORM, bool SWI, int BPU>
+__global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : BPU == 1 ? MT_REC_THREADS : MT_REC4_THREADS) void q4k_mt_k(
     MtTab tab, int cols, int n, int v0, int R, const int8_t *__restrict__ q,
     const float *__restrict__ d, const float *__restrict__ fs, nmx_norm_in nm,
     int8_t *__restrict__ oq, float *__restrict__ od, float *__restrict__ ofs) {
@@ -122,11 +123,14 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
     /* ---- phase 0a: first round of activation / norm-input loads, issued before the weight
      * loads so that waiting for them does not wait for the weights ---- */
     const int nq = nb * NV * 2, ns = nb * NV; /* 16-byte code halves; (block, vector) pairs */
-    int4 buf[8];
-    float bd[4], bf[4];
+    /* staged per thread and round: NQB code halves, NDB (d, fsum) pairs (wide workgroups of
+     * one-block units need fewer) */
+    constexpr int NQB = BPU == 1 ? 2 : 8, NDB = BPU == 1 ? 1 : 4;
+    int4 buf[NQB];
+    float bd[NDB], bf[NDB];
     if constexpr (!NORM) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < NQB; u++) {
             const int e = u * T + tid;
             buf[u] = make_int4(0, 0, 0, 0);
             if (e < nq) {
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < NDB; u++) {
             const int e = u * T + tid;
             const int b = e / NV, v = e - b * NV;
             const size_t gi = e < ns ? (size_t)b * n + v0 + v : 0;
@@ -163,10 +167,12 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
         }
     }
 
-    /* ---- phase 0b: weight unit loads: unit = (row u_r, half superblock u_h) ---- */
-    const bool has_unit = tid < R * 2 * nsb;
+    /* ---- phase 0b: weight unit loads: unit = (row u_r, BPU consecutive blocks u_h of one
+     * superblock half; UPS units per superblock) ---- */
+    constexpr int UPS = 8 / BPU;
+    const bool has_unit = tid < R * UPS * nsb;
     const int u_h = has_unit ? tid / R : 0, u_r = has_unit ? tid - u_h * R : 0;
-    const int u_sb = u_h >> 1, u_k0 = 4 * (u_h & 1);
+    const int u_sb = u_h / UPS, u_k0 = BPU * (u_h % UPS);
     int wseg = si, wrow;
     if (SWI) { /* rows [0, R/2) gate, [R/2, R) up, both at output index lg * R/2 + r mod R/2 */
         wseg = u_r < R / 2 ? 0 : 1;
@@ -178,11 +184,11 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
     const int lrow = wrow < wrows ? wrow : wrows - 1;
     const uint4 *p = (const uint4 *)(tab.s[wseg].W + ((size_t)(lrow >> 2) * nsb + u_sb) * 576);
     const int ti = lrow & 3;
-    uint4 a0 = {}, a1 = {}, a2 = {}, a3 = {}, c[4] = {};
+    uint4 a0 = {}, a1 = {}, a2 = {}, a3 = {}, c[BPU] = {};
     if (has_unit) {
         a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
 #pragma unroll
-        for (int k = 0; k < 4; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
+        for (int k = 0; k < BPU; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
     }
 
     if constexpr (NORM) { /* the residual add, now that the weight loads are in flight */
@@ -198,19 +204,19 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
 
     /* ---- phase 0c: activations into LDS ---- */
     if constexpr (!NORM) {
-        for (int r0 = 0; r0 * 8 * T < nq || r0 * 4 * T < ns; r0++) {
+        for (int r0 = 0; r0 * NQB * T < nq || r0 * NDB * T < ns; r0++) {
             if (r0 > 0) { /* rare: more than one round (very wide rows) */
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int e = (r0 * 8 + u) * T + tid;
+                for (int u = 0; u < NQB; u++) {
+                    const int e = (r0 * NQB + u) * T + tid;
                     if (e < nq) {
                         const int b = e / (2 * NV), rem = e - b * 2 * NV;
                         buf[u] = *(const int4 *)(q + ((size_t)b * n + v0 + (rem >> 1)) * 32 + 16 * (rem & 1));
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const int e = (r0 * 4 + u) * T + tid;
+                for (int u = 0; u < NDB; u++) {
+                    const int e = (r0 * NDB + u) * T + tid;
                     const int b = e / NV, v = e - b * NV;
                     const size_t gi = e < ns ? (size_t)b * n + v0 + v : 0;
                     bd[u] = d[gi];
@@ -218,16 +224,16 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int e = (r0 * 8 + u) * T + tid;
+            for (int u = 0; u < NQB; u++) {
+                const int e = (r0 * NQB + u) * T + tid;
                 if (e < nq) {
                     const int b = e / (2 * NV), rem = e - b * 2 * NV;
                     *(int4 *)(aq + aq_off(b, NV) + (rem >> 1) * 32 + 16 * (rem & 1)) = buf[u];
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int e = (r0 * 4 + u) * T + tid;
+            for (int u = 0; u < NDB; u++) {
+                const int e = (r0 * NDB + u) * T + tid;
                 if (e < ns) {
                     ad[e] = bd[u];
                     afs[e] = bf[u];
@@ -341,20 +347,25 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
         const uint32_t dw = (ti & 2) ? a0.y : a0.x, mw = (ti & 2) ? a0.w : a0.z;
         const float D = half_bits(dw >> (16 * (ti & 1)));
         const float M = half_bits(mw >> (16 * (ti & 1)));
-        int s6[4], m6[4];
-        decode6_half(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, u_h & 1, s6);
-        decode6_half(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, u_h & 1, m6);
-        const int blk0 = u_sb * 8 + u_k0;
-        /* the unit's 4 blocks x NV scales d and fsum (4 NV consecutive floats each, read as NV
-         * float4), then the activations block by block, the next block's 2 NV reads issued
-         * before the current block's dots */
-        float sdv[4 * NV], sfv[4 * NV];
+        int s6[4], m6[4]; /* the 4 blocks of the unit's superblock half */
+        decode6_half(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, u_k0 >> 2, s6);
+        decode6_half(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, u_k0 >> 2, m6);
+        const int blk0 = u_sb * 8 + u_k0, kh = u_k0 & 3; /* kh: first block within the half */
+        /* the unit's BPU blocks x NV scales d and fsum (BPU NV consecutive floats each; as NV
+         * float4 for 4-block units, 16-byte aligned), then the activations block by block, the
+         * next block's 2 NV reads issued before the current block's dots */
+        float sdv[BPU * NV], sfv[BPU * NV];
+        if constexpr (BPU == 4) {
 #pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const float4 x = *(const float4 *)(ad + blk0 * NV + 4 * i);
-            const float4 y = *(const float4 *)(afs + blk0 * NV + 4 * i);
-            sdv[4 * i] = x.x, sdv[4 * i + 1] = x.y, sdv[4 * i + 2] = x.z, sdv[4 * i + 3] = x.w;
-            sfv[4 * i] = y.x, sfv[4 * i + 1] = y.y, sfv[4 * i + 2] = y.z, sfv[4 * i + 3] = y.w;
+            for (int i = 0; i < NV; i++) {
+                const float4 x = *(const float4 *)(ad + blk0 * NV + 4 * i);
+                const float4 y = *(const float4 *)(afs + blk0 * NV + 4 * i);
+                sdv[4 * i] = x.x, sdv[4 * i + 1] = x.y, sdv[4 * i + 2] = x.z, sdv[4 * i + 3] = x.w;
+                sfv[4 * i] = y.x, sfv[4 * i + 1] = y.y, sfv[4 * i + 2] = y.z, sfv[4 * i + 3] = y.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < BPU * NV; i++) sdv[i] = ad[blk0 * NV + i], sfv[i] = afs[blk0 * NV + i];
         }
         int4 xa[NV][2], xn[NV][2];
 #pragma unroll
@@ -363,17 +374,17 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
             xa[v][0] = *(const int4 *)xb, xa[v][1] = *(const int4 *)(xb + 16);
         }
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < BPU; k++) {
             const int blk = blk0 + k;
-            if (k < 3) {
+            if (k < BPU - 1) {
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
                     const int8_t *xb = aq + aq_off(blk + 1, NV) + v * 32;
                     xn[v][0] = *(const int4 *)xb, xn[v][1] = *(const int4 *)(xb + 16);
                 }
             }
-            const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
-            const float of = M * (float)m6[k];
+            const float sc = D * (float)s6[kh + k]; /* exact: 6-bit x 11-bit mantissa */
+            const float of = M * (float)m6[kh + k];
             if constexpr (!REC) lof[blk * R + u_r] = -of;
             const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
             const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
@@ -396,7 +407,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
                 else
                     lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * sdv[k * NV + v]);
             }
-            if (k < 3) {
+            if (k < BPU - 1) {
 #pragma unroll
                 for (int v = 0; v < NV; v++) xa[v][0] = xn[v][0], xa[v][1] = xn[v][1];
             }
@@ -479,11 +490,17 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_
     }
 }
 
-/* Rows per workgroup for a pass of nv vectors. SwiGLU needs R = 64 (32 gate + 32 up rows = one
- * A8 block). The other launches use chain records and R = 8 (else 4): measured on the verify
- * shapes (1024 .. 3584 columns, 5 vectors) this beat every larger R, since a small workgroup's
- * dot and chain phases are short and several workgroups share a CU. */
-int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int count, int *threads) {
+/* Rows per workgroup for a pass of nv vectors, its threads and blocks per dot unit (*bpu).
+ * SwiGLU needs R = 64 (32 gate + 32 up rows = one A8 block). The other launches use chain
+ * records and R = 8 (else 4): measured on the verify shapes (1024 .. 3584 columns, 5 vectors)
+ * this beat every larger R, since a small workgroup's dot and chain phases are short and
+ * several workgroups share a CU. Without a norm prologue, each unit thread takes one block
+ * when the workgroup's units fit in 1024 threads, else 4 (at most 256 threads): a unit's blocks
+ * are one dependent sequence of LDS reads, dots and record stores, so more units shorten the
+ * dot phase. */
+int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int count, int *threads,
+              int *bpu) {
+    *bpu = 4;
     const int nsb = cols >> 8;
     if (norm && !swiglu) {
         /* every workgroup redoes the norm prologue: the fewest rows per workgroup (a multiple
@@ -500,8 +517,11 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
     }
     for (int R = swiglu ? 64 : 8; R >= 4; R >>= 1) {
         if (swiglu && R != 64) break;
-        const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
-        if (t > (norm ? MT_NORM_THREADS : swiglu ? MT_MAX_THREADS : MT_REC_THREADS)) continue;
+        if (!swiglu && !norm) *bpu = R * 8 * nsb <= MT_REC_THREADS ? 1 : 4;
+        const int units = R * (8 / *bpu) * nsb;
+        const int t = 64 * (((units > R * nv ? units : R * nv) + 63) / 64);
+        if (t > (norm ? MT_NORM_THREADS : swiglu ? MT_MAX_THREADS : *bpu == 1 ? MT_REC_THREADS : MT_REC4_THREADS))
+            continue;
         if (mt_layout(cols, nv, R, norm, swiglu).total > MT_LDS) continue;
         if (norm && cols > t * MT_NORM_CPT) continue;
         *threads = t;
@@ -510,18 +530,18 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
     return 0;
 }
 
-template <int NV, bool NORM, bool SWI>
+template <int NV, bool NORM, bool SWI, int BPU>
 int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
                const int8_t *q, const float *d, const float *fs, const nmx_norm_in &nm,
                nmx_a8 out) {
     static bool ready = false; /* idempotent: a racing second call sets the same value */
     if (!ready) {
-        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI>,
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI, BPU>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, MT_LDS));
         ready = true;
     }
     const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI).total;
-    q4k_mt_k<NV, NORM, SWI><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
+    q4k_mt_k<NV, NORM, SWI, BPU><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
         tab, cols, n, v0, R, q, d, fs, nm, out.q, out.d, out.fs);
     NMX_LAUNCHED(ctx, "q4k_mt");
     return 0;
@@ -529,13 +549,14 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
 
 template <int NV>
 int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
-              const int8_t *q, const float *d, const float *fs, const nmx_norm_in *nm, bool swiglu,
-              nmx_a8 out) {
+              int bpu, const int8_t *q, const float *d, const float *fs, const nmx_norm_in *nm,
+              bool swiglu, nmx_a8 out) {
     const nmx_norm_in none{};
-    if (nm && swiglu) return launch_one<NV, true, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
-    if (nm) return launch_one<NV, true, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
-    if (swiglu) return launch_one<NV, false, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
-    return launch_one<NV, false, false>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    if (nm && swiglu) return launch_one<NV, true, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (nm) return launch_one<NV, true, false, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (swiglu) return launch_one<NV, false, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    if (bpu == 1) return launch_one<NV, false, false, 1>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
+    return launch_one<NV, false, false, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
 }
 
 } // namespace
@@ -556,7 +577,8 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
     if (norm && ((uintptr_t)norm->w & 15)) return 1;
     int total_rows = 0;
     for (int s = 0; s < count; s++) total_rows += segs[s].rows;
-    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, total_rows, count, &T);
+    int bpu = 4;
+    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, total_rows, count, &T, &bpu);
     if (!R) return 1;
     MtTab tab{};
     tab.count = count;
@@ -575,14 +597,14 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
         const int Tn = T; /* the first (largest) pass's thread count covers every pass */
         int rc;
         switch (nv) {
-        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
-        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, q, d, fs, norm, swiglu, out); break;
+        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
         }
         if (rc) return rc;
         v0 += nv;
