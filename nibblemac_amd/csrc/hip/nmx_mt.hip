@@ -34,7 +34,7 @@ constexpr int MT_MAX_THREADS = 512; /* the SwiGLU launch (64 rows; the dots' VGP
 constexpr int MT_LDS = 159 * 1024; /* dynamic LDS per workgroup (gfx950: 160 KB) */
 constexpr int MT_NORM_CPT = 8; /* columns per thread in the norm prologue */
 constexpr int MT_NORM_THREADS = 512; /* the prologue keeps NV x MT_NORM_CPT values in VGPRs */
-constexpr int MT_REC_THREADS = 1024; /* record launches of one-block units */
+constexpr int MT_REC_THREADS = 1024; /* launches of 1- or 2-block units */
 constexpr int MT_REC4_THREADS = 256; /* record launches of 4-block units: room for VGPR buffers */
 
 struct MtTab {
@@ -96,7 +96,7 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
 }
 
 template <int NV, bool NORM, bool SWI, int BPU>
-__global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : BPU == 1 ? MT_REC_THREADS : MT_REC4_THREADS) void q4k_mt_k(
+__global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_REC4_THREADS) void q4k_mt_k(
     MtTab tab, int cols, int n, int v0, int R, const int8_t *__restrict__ q,
     const float *__restrict__ d, const float *__restrict__ fs, nmx_norm_in nm,
     int8_t *__restrict__ oq, float *__restrict__ od, float *__restrict__ ofs) {
@@ -104,6 +104,8 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : BPU
     __shared__ float red[5 * MT_MAX_NV];
     const int tid = threadIdx.x, T = blockDim.x;
     const int nb = cols >> 5, nsb = cols >> 8;
+    /* norm prologue columns per thread: wide workgroups of 1- or 2-block units need 2 */
+    constexpr int CPT = NORM && BPU < 4 ? 2 : MT_NORM_CPT;
     const MtLayout L = mt_layout(cols, NV, R, NORM, SWI);
     int8_t *aq = (int8_t *)(smem + L.aq);
     float *ad = (float *)(smem + L.ad), *afs = (float *)(smem + L.afs);
@@ -149,10 +151,10 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : BPU
     }
     /* the norm inputs: x and add stay in separate registers until the weight loads below are
      * issued (adding them here would wait for their memory round trip first) */
-    float xv[NORM ? NV : 1][MT_NORM_CPT], av[NORM ? NV : 1][MT_NORM_CPT];
+    float xv[NORM ? NV : 1][CPT], av[NORM ? NV : 1][CPT];
     if constexpr (NORM) { /* rows v0 .. v0 + NV - 1 (+ add): thread columns c = tid + T j */
 #pragma unroll
-        for (int j = 0; j < MT_NORM_CPT; j++) {
+        for (int j = 0; j < CPT; j++) {
             const int cc = tid + T * j;
             const int ci = cc < cols ? cc : cols - 1;
 #pragma unroll
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : BPU
     if constexpr (NORM) { /* the residual add, now that the weight loads are in flight */
         if (nm.add) {
 #pragma unroll
-            for (int j = 0; j < MT_NORM_CPT; j++) {
+            for (int j = 0; j < CPT; j++) {
                 if (T * j >= cols) continue;
 #pragma unroll
                 for (int v = 0; v < NV; v++) xv[v][j] = xv[v][j] + av[v][j];
@@ -247,7 +249,7 @@ __global__ __launch_bounds__(NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : BPU
         float *sq = (float *)(smem + L.work);
         float *xs = sq + NV * rsz; /* the summed rows [NV][cols] */
 #pragma unroll
-        for (int j = 0; j < MT_NORM_CPT; j++) {
+        for (int j = 0; j < CPT; j++) {
             const int cc = tid + T * j;
             if (cc >= cols) continue;
             const int ix = cc < 4 * m4 ? (cc & 3) * s4 + (cc >> 2) : 4 * s4 + (cc - 4 * m4);
@@ -507,11 +509,20 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
          * of 4) whose workgroups fit the 256 CUs in one round */
         for (int R = 4 * ((total_rows + 4 * 256 - 1) / (4 * 256)); R <= 64; R += 4) {
             if (R * 256 < total_rows + count * R) continue; /* each segment rounds up */
-            const int t = 64 * ((((2 * R * nsb) > (R * nv) ? 2 * R * nsb : R * nv) + 63) / 64);
-            const int tt = t * MT_NORM_CPT < cols ? 64 * ((cols / MT_NORM_CPT + 63) / 64) : t;
-            if (tt > MT_NORM_THREADS || mt_layout(cols, nv, R, true, false).total > MT_LDS) break;
-            *threads = tt;
-            return R;
+            if (mt_layout(cols, nv, R, true, false).total > MT_LDS) break;
+            /* 1- or 2-block units in up to 1024 threads (2 prologue columns per thread) when
+             * they fit, else 4-block units (8 columns per thread, up to 512 threads) */
+            for (int b = 1; b <= 4; b *= 2) {
+                const int units = R * (8 / b) * nsb;
+                const int t = 64 * (((units > R * nv ? units : R * nv) + 63) / 64);
+                const int cpt = b < 4 ? 2 : MT_NORM_CPT;
+                const int tt = t * cpt < cols ? 64 * ((cols / cpt + 63) / 64) : t;
+                if (tt > (b < 4 ? MT_REC_THREADS : MT_NORM_THREADS)) continue;
+                *threads = tt;
+                *bpu = b;
+                return R;
+            }
+            break;
         }
         return 0;
     }
@@ -553,6 +564,8 @@ int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v
               bool swiglu, nmx_a8 out) {
     const nmx_norm_in none{};
     if (nm && swiglu) return launch_one<NV, true, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (nm && bpu == 1) return launch_one<NV, true, false, 1>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (nm && bpu == 2) return launch_one<NV, true, false, 2>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm) return launch_one<NV, true, false, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (swiglu) return launch_one<NV, false, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
     if (bpu == 1) return launch_one<NV, false, false, 1>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);

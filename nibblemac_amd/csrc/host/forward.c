@@ -4,8 +4,9 @@
  * kernel on the context's stream. Nothing here touches the host copy of any activation, so a
  * sequence can be captured into a HIP graph; positions come from the control block c->ctl
  * (ctl[0] = n_past at the start of the pass). Residual adds are fused into the following
- * RMSNorm, SwiGLU into the gate/up matmul's epilogue, and every matmul input is A8-quantized
- * by the kernel that produces it. */
+ * RMSNorm, the RMSNorms into the prologue of the matmul that consumes them (input projections,
+ * gate/up), SwiGLU into the gate/up matmul's epilogue, and every other matmul input is
+ * A8-quantized by the kernel that produces it. */
 #include <math.h>
 #include <stdio.h>
 
@@ -40,32 +41,47 @@ typedef struct {
     const float *add; /* residual to add before the next norm (NULL: none) */
 } e_resid;
 
-/* RMSNorm of cur (+ add, the sum then current) into the A8 buffers a (the next matmul's
- * input). A separate launch: on gfx950 it costs less than the same norm as a matmul prologue
- * (nmx_q4k_matmul_norm), whose workgroups would each redo it. */
-static int norm_a8(pinfer_ctx *c, e_resid *r, const float *w, int n, nmx_a8 a) {
-    CK(nmx_rmsnorm_xo(c->dev, r->cur, c->H, r->add, c->H, r->add ? r->alt : NULL, c->H, w, n,
-                      c->H, c->rms_eps, NULL, 0, a));
+/* The norm input over the residual stream: cur (+ add, the sum written to alt) with weight w;
+ * resid_done then makes the sum current. */
+static nmx_norm_in resid_norm(const pinfer_ctx *c, const e_resid *r, const float *w) {
+    const nmx_norm_in in = {r->cur, c->H, r->add, c->H, r->add ? r->alt : NULL, c->H, w, c->rms_eps};
+    return in;
+}
+
+static void resid_done(e_resid *r) {
     if (r->add) {
         float *t = r->cur;
         r->cur = r->alt;
         r->alt = t;
         r->add = NULL;
     }
+}
+
+/* The input projections of a block: from the A8 rows in s->a_h, or (in != NULL) with the
+ * block's input RMSNorm as a prologue of the matmul's workgroups (nmx_q4k_matmul_norm: every
+ * workgroup redoes the norm of the n x H rows while its weight loads are in flight, one
+ * launch fewer; s->a_h is its fallback's buffer). */
+static int proj_in(pinfer_ctx *c, int count, const void *const *W, const int *R, float *const *Y,
+                   int n, const nmx_norm_in *in) {
+    e_scratch *s = &c->s;
+    if (in) CK(nmx_q4k_matmul_norm(c->dev, count, W, R, Y, R, c->H, n, in, s->a_h));
+    else CK(nmx_q4k_matmul_multi(c->dev, count, W, R, Y, R, c->H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
     return PINFER_OK;
 }
 
-/* Gated full attention (engine/src/forward_attn.c:231-266) on the normed rows (A8 in s->a_h):
- * q (query | gate per head), k, v in one launch; kc / vc: the block's caches; pos_off:
- * position of row 0 relative to ctl[0]. Output (o_proj) to s->out. */
-static int attn_block(pinfer_ctx *c, const e_layer *L, int n, void *kc, void *vc, int pos_off) {
+/* Gated full attention (engine/src/forward_attn.c:231-266) on the normed rows (A8 in s->a_h,
+ * or normed by the projection itself: in): q (query | gate per head), k, v in one launch;
+ * kc / vc: the block's caches; pos_off: position of row 0 relative to ctl[0]. Output (o_proj)
+ * to s->out. */
+static int attn_block(pinfer_ctx *c, const e_layer *L, int n, void *kc, void *vc, int pos_off,
+                      const nmx_norm_in *in) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H, hd = c->hd, qw = 2 * c->n_heads * hd, kvw = c->n_kv * hd;
     const void *W[3] = {L->q.w, L->k.w, L->v.w};
     const int R[3] = {qw, kvw, kvw};
     float *Y[3] = {s->ta, s->tb, s->tc};
-    CK(nmx_q4k_matmul_multi(D, 3, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
+    TRY(proj_in(c, 3, W, R, Y, n, in));
     nmx_attn_args a = {n, c->n_heads, c->n_kv, hd, c->rot, c->max_ctx, s->ta, s->tb, s->tc,
                        L->q_norm, L->k_norm, c->rms_eps, 1.0f / sqrtf((float)hd), c->rope_cos,
                        c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w, s->sc, c->kv_dtype};
@@ -96,10 +112,11 @@ static int mlp_block(pinfer_ctx *c, const e_layer *L, int n, e_resid *r) {
     return PINFER_OK;
 }
 
-/* Gated DeltaNet mixer (engine/src/forward_lin.c:94-133) on the normed rows (A8 in s->a_h).
- * logged: a verify pass (token 0 committed in place, tokens 1.. logged for the commit);
- * pending replays of the last commit are applied first (keep = ctl[2]). */
-static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged) {
+/* Gated DeltaNet mixer (engine/src/forward_lin.c:94-133) on the normed rows (A8 in s->a_h, or
+ * normed by the projection itself: in). logged: a verify pass (token 0 committed in place,
+ * tokens 1.. logged for the commit); pending replays of the last commit are applied first
+ * (keep = ctl[2]). */
+static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged, const nmx_norm_in *in) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H, C = c->conv_dim, vd = c->vd, nv = c->lv_heads, li = L->lin;
@@ -108,7 +125,7 @@ static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged) {
     const void *W[4] = {L->qkv.w, L->z.w, L->b.w, L->a.w};
     const int R[4] = {C, vd, nv, nv};
     float *Y[4] = {s->ta, s->tb, s->ba, s->aa};
-    CK(nmx_q4k_matmul_multi(D, 4, W, R, Y, R, H, n, s->a_h.q, s->a_h.d, s->a_h.fs));
+    TRY(proj_in(c, 4, W, R, Y, n, in));
     nmx_lin_pre_args p = {n, C, c->conv_k, c->lk_dim, c->kd, s->ta, C, s->conv,
                           c->conv_state + (size_t)li * (c->conv_k - 1) * C, L->conv_w,
                           logged ? c->xin + (size_t)li * c->cap * C : NULL,
@@ -138,11 +155,14 @@ int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
                       r.cur, H, NULL, 0, s->a_h, NULL, 0, NULL, NULL, 0, none));
     for (int l = 0; l < c->n_layers; l++) {
         const e_layer *L = &c->layers[l];
-        if (l > 0) TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
+        /* layer 0's input norm ran with the embedding; the others run in the projections */
+        const nmx_norm_in in = resid_norm(c, &r, L->in_norm);
+        const nmx_norm_in *pin = l > 0 ? &in : NULL;
         int rc = L->is_full ? attn_block(c, L, n, kv_of(c->kc, c, L->full),
-                                         kv_of(c->vc, c, L->full), 0)
-                            : lin_block(c, L, n, logged);
+                                         kv_of(c->vc, c, L->full), 0, pin)
+                            : lin_block(c, L, n, logged, pin);
         if (rc) return rc;
+        if (l > 0) resid_done(&r);
         if ((rc = mlp_block(c, L, n, &r))) return rc;
     }
     CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->norm, n, H, c->rms_eps, s->xn, H, s->a_h));
@@ -199,9 +219,10 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     e_resid r = {s->x, s->x2, NULL};
     CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H, NULL));
     const e_layer *L = &c->mtp;
-    TRY(norm_a8(c, &r, L->in_norm, n, s->a_h));
-    int rc = attn_block(c, L, n, c->mkc, c->mvc, pos_off);
+    const nmx_norm_in in = resid_norm(c, &r, L->in_norm);
+    int rc = attn_block(c, L, n, c->mkc, c->mvc, pos_off, &in);
     if (rc) return rc;
+    resid_done(&r);
     if ((rc = mlp_block(c, L, n, &r))) return rc;
     if (n == 1 && !head_row_dynamic) {
         /* one row: the final norm writes the MTP hidden and the head's A8 input itself */
