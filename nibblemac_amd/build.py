@@ -33,11 +33,15 @@ ARCH = "gfx950"
 
 # Device numerics: no contraction (the reference rounds every multiply and add separately
 # except where it calls fmaf), IEEE fp32 denormals, correctly rounded divide / sqrt (the
-# hipcc default, kept), and no packed-fp32 code generation.
+# hipcc default, kept), and no packed-fp32 code generation. Kernel arguments preloaded into
+# SGPRs (the leading pointer / integer arguments, up to 16 SGPRs; the code object keeps the
+# loading prologue for firmware without preloading), so a kernel's first memory requests do
+# not wait for a load from the argument segment.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero", "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{HIP_DIR}",
 ]
 C_FLAGS = ["-O2", "-std=c11", "-ffp-contract=off", "-fPIC", "-Wall", "-Wextra",

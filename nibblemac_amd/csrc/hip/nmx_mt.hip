@@ -95,14 +95,26 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     return L;
 }
 
+/* The leading arguments are the ones the first memory requests need, in 14 SGPRs: the
+ * library is built with kernel-argument preloading, so they arrive in SGPRs with the wave
+ * instead of through a load from the argument segment (about 0.2 us on this part). in0 / in1
+ * are the A8 codes and scales (q, d), or with NORM the norm input rows x and add; aux is the
+ * A8 fsum pointer, or with NORM the row strides of x (low 32 bits) and add (high); W0 / rows0
+ * the first segment's weights and rows; T the block size (blockDim lives in the argument
+ * segment). */
 template <int NV, bool NORM, bool SWI, int BPU>
 __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_REC4_THREADS) void q4k_mt_k(
-    MtTab tab, int cols, int n, int v0, int R, const int8_t *__restrict__ q,
-    const float *__restrict__ d, const float *__restrict__ fs, nmx_norm_in nm,
-    int8_t *__restrict__ oq, float *__restrict__ od, float *__restrict__ ofs) {
+    const void *__restrict__ in0, const void *__restrict__ in1, uint64_t aux,
+    const uint8_t *__restrict__ W0, int cols, int n, int v0, int R, int T, int rows0,
+    MtTab tab, nmx_norm_in nm, int8_t *__restrict__ oq, float *__restrict__ od,
+    float *__restrict__ ofs) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[5 * MT_MAX_NV];
-    const int tid = threadIdx.x, T = blockDim.x;
+    const int tid = threadIdx.x;
+    const int8_t *q = (const int8_t *)in0;
+    const float *d = (const float *)in1, *fs = (const float *)(uintptr_t)aux;
+    const float *nx = (const float *)in0, *nadd = (const float *)in1;
+    const int xs = (int)(uint32_t)aux, as = (int)(uint32_t)(aux >> 32);
     const int nb = cols >> 5, nsb = cols >> 8;
     /* norm prologue columns per thread: wide workgroups of 1- or 2-block units need 2 */
     constexpr int CPT = NORM && BPU < 4 ? 2 : MT_NORM_CPT;
@@ -114,13 +126,16 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     float2 *lp = (float2 *)(smem + L.work);  /* [nb][NV][R] ((float)dot, (D*s)*d) */
     float *lof = (float *)(lp + nb * NV * R); /* [nb][R] -(M*m) */
 
-    /* ---- segment and rows of this workgroup ---- */
+    /* ---- segment and rows of this workgroup (segment 0 from the preloaded arguments: its
+     * workgroups are the first ceil(rows0 / R); SwiGLU launches are one segment pair) ---- */
     const int g = blockIdx.x;
     int si = 0;
+    if (!SWI && g >= (rows0 + R - 1) / R) { /* uniform */
 #pragma unroll
-    for (int t = 1; t < NMX_MAX_SEGS; t++)
-        if (t < tab.count && g >= tab.g0[t]) si = t;
-    const int lg = g - tab.g0[si];
+        for (int t = 1; t < NMX_MAX_SEGS; t++)
+            if (t < tab.count && g >= tab.g0[t]) si = t;
+    }
+    const int lg = si == 0 ? g : g - tab.g0[si];
 
     /* ---- phase 0a: first round of activation / norm-input loads, issued before the weight
      * loads so that waiting for them does not wait for the weights ---- */
@@ -161,10 +176,10 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
             for (int v = 0; v < NV; v++) xv[v][j] = 0.0f, av[v][j] = 0.0f;
             if (T * j >= cols) continue; /* uniform: slot unused by every thread */
 #pragma unroll
-            for (int v = 0; v < NV; v++) xv[v][j] = nm.x[(size_t)(v0 + v) * nm.x_stride + ci];
-            if (nm.add) {
+            for (int v = 0; v < NV; v++) xv[v][j] = nx[(size_t)(v0 + v) * xs + ci];
+            if (nadd) {
 #pragma unroll
-                for (int v = 0; v < NV; v++) av[v][j] = nm.add[(size_t)(v0 + v) * nm.add_stride + ci];
+                for (int v = 0; v < NV; v++) av[v][j] = nadd[(size_t)(v0 + v) * as + ci];
             }
         }
     }
@@ -182,9 +197,10 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     } else {
         wrow = lg * R + u_r;
     }
-    const int wrows = tab.s[wseg].rows;
+    const int wrows = wseg == 0 ? rows0 : tab.s[wseg].rows;
     const int lrow = wrow < wrows ? wrow : wrows - 1;
-    const uint4 *p = (const uint4 *)(tab.s[wseg].W + ((size_t)(lrow >> 2) * nsb + u_sb) * 576);
+    const uint8_t *wbase = wseg == 0 ? W0 : tab.s[wseg].W;
+    const uint4 *p = (const uint4 *)(wbase + ((size_t)(lrow >> 2) * nsb + u_sb) * 576);
     const int ti = lrow & 3;
     uint4 a0 = {}, a1 = {}, a2 = {}, a3 = {}, c[BPU] = {};
     if (has_unit) {
@@ -194,7 +210,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     }
 
     if constexpr (NORM) { /* the residual add, now that the weight loads are in flight */
-        if (nm.add) {
+        if (nadd) {
 #pragma unroll
             for (int j = 0; j < CPT; j++) {
                 if (T * j >= cols) continue;
@@ -552,8 +568,13 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
         ready = true;
     }
     const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI).total;
+    const void *in0 = NORM ? (const void *)nm.x : (const void *)q;
+    const void *in1 = NORM ? (const void *)nm.add : (const void *)d;
+    const uint64_t aux = NORM ? ((uint64_t)(uint32_t)nm.add_stride << 32) | (uint32_t)nm.x_stride
+                              : (uint64_t)(uintptr_t)fs;
     q4k_mt_k<NV, NORM, SWI, BPU><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
-        tab, cols, n, v0, R, q, d, fs, nm, out.q, out.d, out.fs);
+        in0, in1, aux, (const uint8_t *)tab.s[0].W, cols, n, v0, R, T, tab.s[0].rows, tab, nm,
+        out.q, out.d, out.fs);
     NMX_LAUNCHED(ctx, "q4k_mt");
     return 0;
 }
