@@ -64,6 +64,7 @@ template <int DK4>
 __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[8 * 64];
+    __shared__ float spdec[MIX_TB]; /* decays of the pending batch (red serves the L2 norms) */
     constexpr int DK = DK4 * 4, PAD = DK4 + 4, ROW = 4 * PAD;
     const int n = a.n, dv = a.dv, heads = a.heads;
     const int h = blockIdx.x, tid = threadIdx.x, T = blockDim.x, c = tid & 3;
@@ -77,15 +78,9 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
     auto kidx = [](int i) { return (i / DK4) * PAD + i % DK4; }; /* rule layout of key i */
     const int n0 = n < MIX_TB ? n : MIX_TB; /* tokens whose inputs are requested at entry */
 
-    /* ==== every input of the first batch is requested here, before any of it is used ==== */
-    /* recurrence state of the quad's keys */
-    float *Sp = a.S + ((size_t)h * dv + j) * DK + c * DK4;
-    float s[DK4];
-#pragma unroll
-    for (int r = 0; r < DK4; r += 4) {
-        const float4 x = *(const float4 *)(Sp + r);
-        s[r] = x.x, s[r + 1] = x.y, s[r + 2] = x.z, s[r + 3] = x.w;
-    }
+    /* ==== every input of the first batch is requested here, before any of it is used; the
+     * recurrence state last, since loads complete in order and the state is needed only by
+     * the pending replay, which runs after the conv, gates and L2 norms ==== */
     /* pending rows of the first batch, up to the host's bound on keep: keys (x = e T + tid
      * over [pb0][DK]), deltas (over [pb0][dv]), decays (tid < pb0) */
     const int pb0 = a.keep < MIX_TB ? a.keep : MIX_TB;
@@ -136,6 +131,21 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         zq = *(const float4 *)(a.z + (size_t)t * a.z_stride + h * dv + jj);
     }
     if (w_on) wq = *(const float4 *)(a.w + 4 * tid);
+    /* recurrence state of the quad's keys */
+    float *Sp = a.S + ((size_t)h * dv + j) * DK + c * DK4;
+    float s[DK4];
+#pragma unroll
+    for (int r = 0; r < DK4; r += 4) {
+        const float4 x = *(const float4 *)(Sp + r);
+        s[r] = x.x, s[r + 1] = x.y, s[r + 2] = x.z, s[r + 3] = x.w;
+    }
+
+    /* pending rows to replay: the host's bound, or fewer from the device control block */
+    int keep = a.keep;
+    if (a.keep_dev) {
+        const int kd_ = *a.keep_dev;
+        keep = kd_ < keep ? kd_ : keep;
+    }
 
     /* ---- requested values that later phases read from LDS ---- */
 #pragma unroll
@@ -144,56 +154,10 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         if (uk < pb0) sp[uk * ROW + kidx(ik)] = pkey[e];
         if (ud < pb0) spd[x] = pdel[e];
     }
-    if (tid < pb0) red[tid] = pdec;
+    if (tid < pb0) spdec[tid] = pdec;
     if (z_on) *(float4 *)(sz + 4 * tid) = zq;
     if (w_on) *(float4 *)(sw + 4 * tid) = wq;
     __syncthreads();
-
-    /* ---- the deferred commit of the previous pass (matvec_ref.c:169-188 arithmetic) ---- */
-    int keep = a.keep;
-    if (a.keep_dev) {
-        const int kd_ = *a.keep_dev;
-        keep = kd_ < keep ? kd_ : keep;
-    }
-    for (int u0 = 0; u0 < keep; u0 += MIX_TB) {
-        const int nb = keep - u0 < MIX_TB ? keep - u0 : MIX_TB;
-        if (u0 > 0) { /* later batches (keep > MIX_TB) load here */
-            float kb[2], db[2], dc = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv, jd = x - ud * dv;
-                kb[e] = uk < nb ? a.pend[((size_t)(u0 + uk) * heads + h) * logw + ik] : 0.0f;
-                db[e] = ud < nb ? a.pend[((size_t)(u0 + ud) * heads + h) * logw + DK + jd] : 0.0f;
-            }
-            if (tid < nb) dc = a.pend[((size_t)(u0 + tid) * heads + h) * logw + DK + dv];
-            __syncthreads(); /* the previous batch is applied */
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv;
-                if (uk < nb) sp[uk * ROW + kidx(ik)] = kb[e];
-                if (ud < nb) spd[x] = db[e];
-            }
-            if (tid < nb) red[tid] = dc;
-            __syncthreads();
-        }
-#pragma unroll
-        for (int u = 0; u < MIX_TB; u++) {
-            if (u < nb) {
-                const float pdec_ = red[u], pdel_ = spd[u * dv + j];
-                const float *kk = sp + u * ROW + c * PAD;
-#pragma unroll
-                for (int r = 0; r < DK4; r++) {
-                    s[r] = s[r] * pdec_;
-                    s[r] = s[r] + kk[r] * pdel_;
-                }
-            }
-        }
-    }
-    const bool store_now = a.log0 && keep > 0;
-    if (store_now) {
-#pragma unroll
-        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
-    }
 
     /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv), one per thread ---- */
     if (conv_on) {
@@ -286,6 +250,49 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         }
     }
     __syncthreads();
+
+    /* ---- the deferred commit of the previous pass (matvec_ref.c:169-188 arithmetic): the
+     * state's rows, requested at entry, have arrived during the conv, gates and L2 norms;
+     * the first batch of pending rows is in LDS since the first barrier ---- */
+    for (int u0 = 0; u0 < keep; u0 += MIX_TB) {
+        const int nb = keep - u0 < MIX_TB ? keep - u0 : MIX_TB;
+        if (u0 > 0) { /* later batches (keep > MIX_TB) load here */
+            float kb[2], db[2], dc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv, jd = x - ud * dv;
+                kb[e] = uk < nb ? a.pend[((size_t)(u0 + uk) * heads + h) * logw + ik] : 0.0f;
+                db[e] = ud < nb ? a.pend[((size_t)(u0 + ud) * heads + h) * logw + DK + jd] : 0.0f;
+            }
+            if (tid < nb) dc = a.pend[((size_t)(u0 + tid) * heads + h) * logw + DK + dv];
+            __syncthreads(); /* the previous batch is applied */
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int x = e * T + tid, uk = x / DK, ik = x - uk * DK, ud = x / dv;
+                if (uk < nb) sp[uk * ROW + kidx(ik)] = kb[e];
+                if (ud < nb) spd[x] = db[e];
+            }
+            if (tid < nb) spdec[tid] = dc;
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < MIX_TB; u++) {
+            if (u < nb) {
+                const float pdec_ = spdec[u], pdel_ = spd[u * dv + j];
+                const float *kk = sp + u * ROW + c * PAD;
+#pragma unroll
+                for (int r = 0; r < DK4; r++) {
+                    s[r] = s[r] * pdec_;
+                    s[r] = s[r] + kk[r] * pdel_;
+                }
+            }
+        }
+    }
+    const bool store_now = a.log0 && keep > 0;
+    if (store_now) {
+#pragma unroll
+        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+    }
 
     /* ---- recurrence over the tokens (nmx_lin_rule arithmetic) ---- */
     for (int t = 0; t < n; t++) {
