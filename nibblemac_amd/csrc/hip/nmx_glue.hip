@@ -645,12 +645,22 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
     extern __shared__ float4 smem4[];
     const int hd = a.hd, rep = a.nh / a.nkv, rs = hd + 4;
     const int t = blockIdx.y, g = blockIdx.z, p0 = blockIdx.x * CP;
+    const int f4 = hd >> 2;
+    /* the first 4 query heads of the group, requested before the position is known (the K
+     * rows' addresses wait for it); staged into LDS once the K rows are */
+    float4 qa[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int f = u * 256 + threadIdx.x, hh = f / f4, c4 = f - hh * f4;
+        qa[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (f < 4 * f4 && hh < rep)
+            qa[u] = ((const float4 *)(a.q + ((size_t)t * a.nh + g * rep + hh) * 2 * hd))[c4];
+    }
     const int np = *a.pos + a.pos_off + t + 1;
     if (p0 >= np) return;
     const int rows = np - p0 < CP ? np - p0 : CP;
     float *ks = (float *)smem4;   /* [CP][rs] */
     float *qs = ks + CP * rs;     /* [4][hd] */
-    const int f4 = hd >> 2;
     const size_t R0 = (size_t)g * a.max_ctx + p0;
     const float *ksc = kv_scales<KVT>(a.kc, a);
     for (int f0 = 0; f0 < rows * f4; f0 += 4 * 256) {
@@ -676,11 +686,19 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
     const float *kr = ks + (live ? pl : 0) * rs + CPL * lp;
     for (int hb = 0; hb < rep; hb += 4) {
         __syncthreads(); /* K staged; previous heads' qs reads done */
-        for (int f = threadIdx.x; f < 4 * f4; f += 256) {
-            const int hh = f / f4, c4 = f - hh * f4;
-            if (hb + hh < rep)
-                *(float4 *)(qs + hh * hd + 4 * c4) =
-                    ((const float4 *)(a.q + ((size_t)t * a.nh + g * rep + hb + hh) * 2 * hd))[c4];
+        if (hb == 0) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int f = u * 256 + threadIdx.x, hh = f / f4, c4 = f - hh * f4;
+                if (f < 4 * f4 && hh < rep) *(float4 *)(qs + hh * hd + 4 * c4) = qa[u];
+            }
+        } else {
+            for (int f = threadIdx.x; f < 4 * f4; f += 256) {
+                const int hh = f / f4, c4 = f - hh * f4;
+                if (hb + hh < rep)
+                    *(float4 *)(qs + hh * hd + 4 * c4) =
+                        ((const float4 *)(a.q + ((size_t)t * a.nh + g * rep + hb + hh) * 2 * hd))[c4];
+            }
         }
         __syncthreads();
         const int h = hb + w;
