@@ -319,6 +319,13 @@ typedef struct {
 } nmx_attn_args;
 int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p);
 int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p);
+/* nmx_attn_prep followed by nmx_attn in two launches instead of three: the scores kernel
+ * normalises and rotates its own queries and the pass's new keys (rounded to the cache format
+ * and back) and stores the new K / V rows itself (the steps of forward_attn.c:231-266 and
+ * forward_kv.c:83-127). o, its A8, the scores and both caches equal those of the two calls
+ * bit for bit; q keeps the unrotated queries. hd = 256, at most 4 query heads per KV group
+ * and at most 8 tokens, else the two calls. */
+int nmx_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p);
 
 /* flag[0] = (top-1 probability of logits[0, n) >= tau): with mx = max (pf_softmax_max) and
  * s = sum of pf_expf(l_i - mx) in the reference's order (4 interleaved partial sums, tail,

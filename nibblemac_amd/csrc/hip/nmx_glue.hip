@@ -731,6 +731,196 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
     }
 }
 
+/* attn_prep_k and attn_score_k in one launch (nmx_attn_fused), for hd = 256 (a thread per
+ * element of a row) and at most 4 query heads per KV group. Each workgroup (chunk of CP
+ * positions, token t, group g) normalises and rotates the group's query heads of token t
+ * itself, and the keys of the pass's new positions in its chunk (tokens t' <= t), with the
+ * operations of attn_prep_k; the keys are rounded to the cache format and back, so each score
+ * equals the one read from the cache. The workgroup whose chunk holds token t's own position
+ * stores that K row and the V row (each (token, group) once; later passes and the P.V launch
+ * read them). The rotated queries are not written back: only the scores use them. */
+constexpr int QK_HD = 256;
+
+/* max |x| of a row of QK_HD values, one per thread, exact in any order */
+__device__ __forceinline__ float qk_row_amax(float x, float *amx, int slot) {
+    float m = fabsf(x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) amx[slot * 4 + (threadIdx.x >> 6)] = m;
+    return m;
+}
+
+template <int CP, int KVT>
+__global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc) {
+    constexpr int HD = QK_HD, LP = 64 / CP, CPL = 16 / LP, RS = HD + 4, F4 = HD / 4;
+    extern __shared__ float4 smem4[];
+    __shared__ float part[(4 + CP) * 4]; /* partial sums of squares, 4 per row */
+    __shared__ float rn[4 + CP];         /* 1 / rms of each row */
+    __shared__ float amx[(CP + 1) * 4];  /* int8 cache: per (row, wave) max |x| */
+    const int i = threadIdx.x, lane = i & 63, w = i >> 6;
+    const int rep = a.nh / a.nkv, h2 = a.rot / 2;
+    const int t = blockIdx.y, g = blockIdx.z, p0 = blockIdx.x * CP;
+    float *ks = (float *)smem4; /* [CP][RS] key rows of the chunk, as the cache gives them */
+    float *qs = ks + CP * RS;   /* [4][HD] rotated queries */
+    float *qw = qs + 4 * HD;    /* [4][HD] queries being normalised */
+    float *kw = qw + 4 * HD;    /* [CP][HD] new keys being normalised */
+    /* the queries first (their address does not wait for the position) */
+    float qv[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++)
+        qv[hh] = hh < rep ? a.q[((size_t)t * a.nh + g * rep + hh) * 2 * HD + i] : 0.0f;
+    const int pos0 = *a.pos + a.pos_off; /* position of token 0 */
+    const int np = pos0 + t + 1;
+    if (p0 >= np) return;
+    const int rows = np - p0 < CP ? np - p0 : CP;
+    const int nold = pos0 - p0 <= 0 ? 0 : pos0 - p0 < rows ? pos0 - p0 : rows;
+    const int nnew = rows - nold;
+    const bool own = np - p0 <= CP; /* token t's own position is row rows - 1 of the chunk */
+    const size_t R0 = (size_t)g * a.max_ctx + p0;
+    const float *ksc = kv_scales<KVT>(a.kc, a);
+    /* new keys and, for the own row, the values: raw inputs */
+    for (int r = nold; r < rows; r++)
+        kw[r * HD + i] = a.k_in[(size_t)(p0 + r - pos0) * a.nkv * HD + g * HD + i];
+    const float vv = own ? a.v_in[(size_t)t * a.nkv * HD + g * HD + i] : 0.0f;
+    /* the old rows from the cache */
+    for (int f0 = 0; f0 < nold * F4; f0 += 4 * 256) {
+        float4 b[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int f = f0 + u * 256 + i;
+            b[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (f < nold * F4) b[u] = kv_load4<KVT>(a.kc, R0 + f / F4, HD, 4 * (f % F4), ksc);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int f = f0 + u * 256 + i;
+            if (f < nold * F4) {
+                const int r = f / F4, c4 = f - r * F4;
+                *(float4 *)(ks + r * RS + 4 * c4) = b[u];
+            }
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) qw[hh * HD + i] = qv[hh];
+    __syncthreads();
+    /* RMSNorm of every row (attn_prep_k: 4 partial sums of squares over i = l (mod 4) in i
+     * order, combined (c0 + c1) + (c2 + c3), empty tail), rows 0-3 the queries, then the new
+     * keys */
+    for (int x = i; x < (4 + nnew) * 4; x += 256) {
+        const int j = x >> 2, l = x & 3;
+        const float *row = j < 4 ? qw + j * HD : kw + (nold + j - 4) * HD;
+        float c = 0.0f;
+#pragma unroll 8
+        for (int m = 0; m < HD / 4; m++) {
+            const float v = row[4 * m + l];
+            c = c + v * v;
+        }
+        part[x] = c;
+    }
+    __syncthreads();
+    for (int j = i; j < 4 + nnew; j += 256) {
+        const float *r4 = part + 4 * j;
+        const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
+        rn[j] = 1.0f / sqrtf(ss / (float)HD + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) qw[hh * HD + i] = (qw[hh * HD + i] * rn[hh]) * a.q_norm[i];
+    for (int r = nold; r < rows; r++)
+        kw[r * HD + i] = (kw[r * HD + i] * rn[4 + r - nold]) * a.k_norm[i];
+    __syncthreads();
+    /* RoPE over the first rot elements at each row's position */
+    auto rope = [&](const float *row, int p) {
+        if (i < h2) {
+            const float c = a.rcos[(size_t)p * h2 + i], s = a.rsin[(size_t)p * h2 + i];
+            return row[i] * c - row[i + h2] * s;
+        } else if (i < 2 * h2) {
+            const float c = a.rcos[(size_t)p * h2 + i - h2], s = a.rsin[(size_t)p * h2 + i - h2];
+            return row[i] * c + row[i - h2] * s;
+        }
+        return row[i];
+    };
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) qs[hh * HD + i] = rope(qw + hh * HD, pos0 + t);
+    for (int r = nold; r < rows; r++) ks[r * RS + i] = rope(kw + r * HD, p0 + r);
+    if constexpr (KVT == KV_I8) {
+        /* row maxima of the new keys (and of the own row's values) for their int8 codes */
+        __syncthreads(); /* the rotated keys are in ks */
+        for (int r = nold; r < rows; r++) (void)qk_row_amax(ks[r * RS + i], amx, r);
+        if (own) (void)qk_row_amax(vv, amx, CP);
+        __syncthreads();
+    }
+    const size_t Rown = (size_t)g * a.max_ctx + (np - 1);
+    for (int r = nold; r < rows; r++) {
+        const float x = ks[r * RS + i];
+        const bool st = own && r == rows - 1;
+        if constexpr (KVT == KV_F32) {
+            if (st) ((float *)a.kc)[Rown * HD + i] = x;
+        } else if constexpr (KVT == KV_F16) {
+            const uint32_t b = kv_half_bits(x);
+            ks[r * RS + i] = kv_half_value(b);
+            if (st) ((unsigned short *)a.kc)[Rown * HD + i] = (unsigned short)b;
+        } else {
+            float amax = 0.0f; /* kv_store's order */
+#pragma unroll
+            for (int ww = 0; ww < HD / 64; ww++) amax = fmaxf(amax, amx[4 * r + ww]);
+            const float inv = amax > 127.0f / 3.40282347e+38f ? 127.0f / amax : 0.0f;
+            const uint32_t q = kv_i8_code(x, inv);
+            const float scl = amax / 127.0f;
+            ks[r * RS + i] = (float)(int8_t)q * scl;
+            if (st) {
+                ((int8_t *)a.kc)[Rown * HD + i] = (int8_t)q;
+                if (i == 0) ((float *)((int8_t *)a.kc + (size_t)a.nkv * a.max_ctx * HD))[Rown] = scl;
+            }
+        }
+    }
+    if (own) { /* the value row: stored as attn_prep_k stores it */
+        if constexpr (KVT == KV_F32) {
+            ((float *)a.vc)[Rown * HD + i] = vv;
+        } else if constexpr (KVT == KV_F16) {
+            ((unsigned short *)a.vc)[Rown * HD + i] = (unsigned short)kv_half_bits(vv);
+        } else {
+            float amax = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < HD / 64; ww++) amax = fmaxf(amax, amx[4 * CP + ww]);
+            const float inv = amax > 127.0f / 3.40282347e+38f ? 127.0f / amax : 0.0f;
+            ((int8_t *)a.vc)[Rown * HD + i] = (int8_t)kv_i8_code(vv, inv);
+            if (i == 0) ((float *)((int8_t *)a.vc + (size_t)a.nkv * a.max_ctx * HD))[Rown] = amax / 127.0f;
+        }
+    }
+    __syncthreads(); /* ks and qs complete */
+    /* the scores, as attn_score_k (wave w takes query head w) */
+    const int pl = lane % CP, lp = lane / CP;
+    const bool live = pl < rows;
+    const float *kr = ks + (live ? pl : 0) * RS + CPL * lp;
+    if (w >= rep) return; /* uniform per wave; no barrier follows */
+    const float *qr = qs + w * HD + CPL * lp;
+    float c[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) c[j] = 0.0f;
+    for (int e = 0; e < HD; e += 16) {
+#pragma unroll
+        for (int j = 0; j < CPL; j += 4) {
+            const float4 kv = *(const float4 *)(kr + e + j);
+            const float4 qv4 = *(const float4 *)(qr + e + j);
+            c[j] = c[j] + qv4.x * kv.x;
+            c[j + 1] = c[j + 1] + qv4.y * kv.y;
+            c[j + 2] = c[j + 2] + qv4.z * kv.z;
+            c[j + 3] = c[j + 3] + qv4.w * kv.w;
+        }
+    }
+    float x;
+    if constexpr (LP == 2) {
+        x = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+    } else {
+        x = (c[0] + c[1]) + (c[2] + c[3]);
+        x = x + __shfl_xor(x, 16);
+    }
+    const float s = x + __shfl_xor(x, 32);
+    if (lp == 0 && live)
+        sc[((size_t)t * a.nh + g * rep + w) * a.max_ctx + p0 + pl] = (s + 0.0f) * a.scale;
+}
+
 /* Softmax and P.V (forward_attn.c:171-181, forward_ops.c:294-382, :360-382): max (exact in
  * any order: only its value is used, and exp(x - (+-0)) agrees), e_p = exp(s_p - max) with
  * 4 partial sums + tail, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] accumulated in p
@@ -1345,6 +1535,9 @@ void launch_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
 }
 
 template <int KVT>
+int launch_pv(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a);
+
+template <int KVT>
 int launch_attn(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
     const int cp = p->hd <= 256 ? 32 : 16;
     dim3 sgrid((unsigned)((p->max_ctx + cp - 1) / cp), (unsigned)p->n, (unsigned)p->nkv);
@@ -1352,6 +1545,11 @@ int launch_attn(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
     if (cp == 32) attn_score_k<32, KVT><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
     else attn_score_k<16, KVT><<<sgrid, 256, slds, ctx->stream>>>(a, p->scores);
     NMX_LAUNCHED(ctx, "attn_score");
+    return launch_pv<KVT>(ctx, p, a);
+}
+
+template <int KVT>
+int launch_pv(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
     const unsigned pgrid = (unsigned)((p->hd / PV_DS) * p->nh * p->n);
     const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + (size_t)PV_PT * PV_DS) * 4;
     static bool pv_ready = false; /* idempotent */
@@ -1371,9 +1569,43 @@ int launch_attn(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
     return 0;
 }
 
+/* attn_qk_k + the P.V launch of launch_attn; outside attn_qk_k's limits, and for passes of
+ * more than 8 tokens (prefill chunks: each of their workgroups would redo up to 32 key rows'
+ * norms, measured slower than the separate launch), the three launches */
+template <int KVT>
+int launch_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
+    if (p->hd != QK_HD || p->nh / p->nkv > 4 || p->n > 8) {
+        launch_attn_prep<KVT>(ctx, p, a);
+        NMX_LAUNCHED(ctx, "attn_prep");
+        return launch_attn<KVT>(ctx, p, a);
+    }
+    constexpr int CP = 32;
+    const size_t lds = ((size_t)CP * (QK_HD + 4) + 8 * (size_t)QK_HD + (size_t)CP * QK_HD) * 4;
+    static bool ready = false; /* idempotent */
+    if (!ready) {
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_qk_k<CP, KVT>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        ready = true;
+    }
+    dim3 grid((unsigned)((p->max_ctx + CP - 1) / CP), (unsigned)p->n, (unsigned)p->nkv);
+    attn_qk_k<CP, KVT><<<grid, 256, lds, ctx->stream>>>(a, p->scores);
+    NMX_LAUNCHED(ctx, "attn_qk");
+    return launch_pv<KVT>(ctx, p, a);
+}
+
 } // namespace
 
 extern "C" {
+
+int nmx_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p) {
+    if (!ctx) return -1;
+    Attn a;
+    if (attn_args(ctx, p, &a)) return -1;
+    if (!p->scores) return nmx_fail(ctx, "nmx_attn_fused: NULL scores workspace");
+    if (p->kv_dtype == KV_F16) return launch_attn_fused<KV_F16>(ctx, p, a);
+    if (p->kv_dtype == KV_I8) return launch_attn_fused<KV_I8>(ctx, p, a);
+    return launch_attn_fused<KV_F32>(ctx, p, a);
+}
 
 int nmx_attn_prep(nmx_ctx *ctx, const nmx_attn_args *p) {
     if (!ctx) return -1;

@@ -85,8 +85,7 @@ static int attn_block(pinfer_ctx *c, const e_layer *L, int n, void *kc, void *vc
     nmx_attn_args a = {n, c->n_heads, c->n_kv, hd, c->rot, c->max_ctx, s->ta, s->tb, s->tc,
                        L->q_norm, L->k_norm, c->rms_eps, 1.0f / sqrtf((float)hd), c->rope_cos,
                        c->rope_sin, kc, vc, c->ctl, pos_off, s->to, s->a_w, s->sc, c->kv_dtype};
-    CK(nmx_attn_prep(D, &a));
-    CK(nmx_attn(D, &a));
+    CK(nmx_attn_fused(D, &a)); /* prep + scores in one launch, then P.V */
     CK(nmx_q4k_matmul(D, L->o.w, H, c->n_heads * hd, n, s->a_w.q, s->a_w.d, s->a_w.fs, s->out,
                       H, NULL));
     return PINFER_OK;

@@ -64,6 +64,16 @@ class LinMixArgs(ctypes.Structure):
                 ("a8", A8)]
 
 
+class AttnArgs(ctypes.Structure):
+    """Mirror of nmx_attn_args (gated full attention over the KV caches)."""
+
+    _fields_ = [("n", _i), ("nh", _i), ("nkv", _i), ("hd", _i), ("rot", _i), ("max_ctx", _i),
+                ("q", _vp), ("k_in", _vp), ("v_in", _vp), ("q_norm", _vp), ("k_norm", _vp),
+                ("eps", ctypes.c_float), ("scale", ctypes.c_float), ("rope_cos", _vp),
+                ("rope_sin", _vp), ("kc", _vp), ("vc", _vp), ("pos", _vp), ("pos_off", _i),
+                ("o", _vp), ("a8", A8), ("scores", _vp), ("kv_dtype", _i)]
+
+
 _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_create": (_vp, [_i]),
     "nmx_create_error": (ctypes.c_char_p, []),
@@ -113,6 +123,9 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_lin_pre": (_i, [_vp, ctypes.POINTER(LinPreArgs)]),
     "nmx_lin_post": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp, _i, A8]),
     "nmx_lin_mix": (_i, [_vp, ctypes.POINTER(LinMixArgs)]),
+    "nmx_attn_prep": (_i, [_vp, ctypes.POINTER(AttnArgs)]),
+    "nmx_attn": (_i, [_vp, ctypes.POINTER(AttnArgs)]),
+    "nmx_attn_fused": (_i, [_vp, ctypes.POINTER(AttnArgs)]),
     "nmx_q4k_swiglu": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, ctypes.POINTER(NormIn),
                             _vp, A8, A8, _vp, _vp]),
     "nmx_top1_gate": (_i, [_vp, _vp, _i, ctypes.c_float, _vp]),
@@ -367,6 +380,16 @@ class Device:
         self.check(self.lib.nmx_lin_post(self.ctx, _p(o), o_stride, _p(z), z_stride, _p(w), n,
                                          heads, dv, eps, _p(y), y_stride,
                                          A8(*[_p(t) for t in a8])), "lin_post")
+
+    def attn_prep(self, args: "AttnArgs") -> None:
+        self.check(self.lib.nmx_attn_prep(self.ctx, ctypes.byref(args)), "attn_prep")
+
+    def attn(self, args: "AttnArgs") -> None:
+        self.check(self.lib.nmx_attn(self.ctx, ctypes.byref(args)), "attn")
+
+    def attn_fused(self, args: "AttnArgs") -> None:
+        """nmx_attn_fused: nmx_attn_prep + nmx_attn in two launches."""
+        self.check(self.lib.nmx_attn_fused(self.ctx, ctypes.byref(args)), "attn_fused")
 
     def lin_mix(self, args: "LinMixArgs") -> None:
         self.check(self.lib.nmx_lin_mix(self.ctx, ctypes.byref(args)), "lin_mix")
