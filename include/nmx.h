@@ -198,6 +198,16 @@ int nmx_rmsnorm_xo(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
 int nmx_rmsnorm_row(nmx_ctx *ctx, const float *x, int x_stride, const float *add,
                     int add_stride, const float *w, int cols, float eps, const int32_t *idx,
                     int off, int nrows, float *y, nmx_a8 a8);
+/* nmx_rmsnorm_row (row *idx + off of x (+ add), clamped to [0, nrows), normed with w into y,
+ * which may be NULL) followed by nmx_head_accept_to over that one row without drafts: the MTP
+ * draft head on its final norm (engine/src/mtp.c:88-100). The norm runs inside the head's
+ * workgroups (one launch fewer; y, out and tok_dst equal those of the two calls bit for bit)
+ * when cols is a multiple of 256 up to 1024 and x, add, w, y are 16-byte aligned rows; else
+ * the two calls, with a8_tmp (one cols-column A8 row) for the norm's output. */
+int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
+                           int x_stride, const float *add, int add_stride, const float *w,
+                           float eps, const int32_t *idx, int off, int nrows, float *y,
+                           void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp);
 
 int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
                      const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,

@@ -22,6 +22,7 @@
 #include "nmx_internal.h"
 #include "nmx_a8.h"
 #include "nmx_lanes.h"
+#include "nmx_rms.h"
 
 namespace {
 
@@ -350,6 +351,107 @@ struct FinishCommit {
     int32_t *vt, *ctl, *mb;
     int nvt;
 };
+
+/* The one-row head with its input's RMSNorm inside (nmx_head_row_accept_to): row *idx + off of
+ * x (+ add), clamped to [0, nrows), normed with w (rms4_load / rms4_finish: the arithmetic of
+ * nmx_rmsnorm_row) into y (written by workgroup 0) and into a one-vector A8 in LDS; then the
+ * dots of q4k_mv_k<1, false, true> with the activations read from LDS. The row's loads are
+ * requested before the first superblock's weights, so the norm runs while the weights are in
+ * flight. cols <= 1024. */
+struct HeadRow {
+    const float *x;
+    int x_stride;
+    const float *add;
+    int add_stride;
+    const float *w;
+    float eps;
+    const int32_t *idx;
+    int off, nrows;
+    float *y;
+};
+
+constexpr int MVR_MAX_COLS = 1024;
+
+__global__ __launch_bounds__(256) void q4k_mvr_k(SegTable tab, int cols, HeadRow hr,
+                                                 unsigned long long *__restrict__ amax_key) {
+    __shared__ __align__(16) int8_t s_q[MVR_MAX_COLS];
+    __shared__ float s_d[MVR_MAX_COLS / 32], s_fs[MVR_MAX_COLS / 32];
+    __shared__ __align__(16) float s_sq[4 * cm_stride(MVR_MAX_COLS) + 4];
+    __shared__ float s_red[8];
+    /* the norm's row first */
+    const int ri = *hr.idx + hr.off;
+    const size_t r = (size_t)(ri < 0 ? 0 : ri >= hr.nrows ? hr.nrows - 1 : ri);
+    float4 xv[1], av[1], wv[1];
+    rms4_load<1>(hr.x + r * hr.x_stride, hr.add ? hr.add + r * hr.add_stride : nullptr, hr.w, cols,
+                 xv, av, wv);
+
+    const int wave_raw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const bool wave_live = wave_raw < tab.total_waves;
+    const int wave = wave_live ? wave_raw : tab.total_waves - 1;
+    const int lane = threadIdx.x & 63;
+    const uint8_t *W = tab.s[0].W;
+    const int rows = tab.s[0].rows;
+    const int row_raw = wave * 64 + lane;
+    const bool valid = wave_live && row_raw < rows;
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const int i = row & 3, sh8 = 8 * i;
+    const int nsb = cols >> 8;
+    const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * nsb * SB_BYTES);
+    uint4 a0 = tp[0], a1 = tp[1], a2 = tp[2], a3 = tp[3], c[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) c[k] = tp[4 + 4 * k + i];
+
+    rms4_finish<1>(xv, av, wv, hr.add != nullptr, nullptr, cols, hr.eps,
+                   blockIdx.x == 0 ? hr.y : nullptr, s_q, s_d, s_fs, 1, 0, s_sq, s_red);
+    __syncthreads(); /* the A8 row is in LDS */
+
+    float acc = 0.0f;
+    for (int sb = 0; sb < nsb; sb++) {
+        const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
+        const float D = half_bits_to_float(dw >> (16 * (i & 1)));
+        const float M = half_bits_to_float(mw >> (16 * (i & 1)));
+        int s6[8], m6[8];
+        decode6(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, s6);
+        decode6(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, m6);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
+            const float of = M * (float)m6[k];
+            const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
+            const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
+            const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
+            const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
+            const int blk = sb * 8 + k;
+            const int4 x0 = *(const int4 *)(s_q + blk * 32), x1 = *(const int4 *)(s_q + blk * 32 + 16);
+            int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
+            dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
+            dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
+            dot = __builtin_amdgcn_sdot4(lo3, x0.w, dot, false);
+            dot = __builtin_amdgcn_sdot4(hi0, x1.x, dot, false);
+            dot = __builtin_amdgcn_sdot4(hi1, x1.y, dot, false);
+            dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
+            dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
+            acc = __builtin_fmaf((float)dot, sc * s_d[blk], acc);
+            acc = __builtin_fmaf(-of, s_fs[blk], acc);
+        }
+        if (sb + 1 < nsb) {
+            const uint4 *p = tp + (sb + 1) * (SB_BYTES / 16);
+            a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+#pragma unroll
+            for (int k = 0; k < 8; k++) c[k] = p[4 + 4 * k + i];
+        }
+    }
+    /* the argmax keys, as q4k_mv_k */
+    __shared__ unsigned long long wkeys[4];
+    const unsigned long long key = nmx_max_u64_wave(valid ? argmax_key(acc, row) : 0ull);
+    if (lane == 0) wkeys[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long k0 = wkeys[0];
+        for (int w = 1; w < 4; w++) k0 = wkeys[w] > k0 ? wkeys[w] : k0;
+        amax_key[blockIdx.x] = k0;
+    }
+}
 
 /* Argmax of every row from the per-workgroup partial keys, then the acceptance loop of the
  * reference (engine/src/spec.c:340-345): a = 0; g = argmax(row 0); while a < k and
@@ -1020,6 +1122,43 @@ int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
                        void *work, int32_t *out, int32_t *tok_dst) {
     return head_accept(ctx, W, rows, cols, n, q, d, fsum, logits, drafts, work, out, tok_dst,
                        FinishCommit{nullptr, nullptr, nullptr, 0});
+}
+
+int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
+                           int x_stride, const float *add, int add_stride, const float *w,
+                           float eps, const int32_t *idx, int off, int nrows, float *y,
+                           void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp) {
+    if (!ctx) return -1;
+    if (!W || !x || !w || !idx || !work || !out || nrows < 1 || x_stride < cols ||
+        (add && add_stride < cols))
+        return nmx_fail(ctx, "nmx_head_row_accept_to: bad arguments");
+    auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool fused = cols % 256 == 0 && cols <= MVR_MAX_COLS && rows > 0 && rows % 4 == 0 &&
+                       rows <= (1 << 22) && al(x) && al(w) && x_stride % 4 == 0 &&
+                       (!add || (al(add) && add_stride % 4 == 0)) && (!y || al(y)) &&
+                       (uintptr_t)work % 8 == 0;
+    if (!fused) { /* the norm, then the head on its A8 */
+        if (!a8_tmp.q || !a8_tmp.d || !a8_tmp.fs)
+            return nmx_fail(ctx, "nmx_head_row_accept_to: shape needs a8_tmp");
+        if (nmx_rmsnorm_row(ctx, x, x_stride, add, add_stride, w, cols, eps, idx, off, nrows, y,
+                            a8_tmp))
+            return -1;
+        return nmx_head_accept_to(ctx, W, rows, cols, 1, a8_tmp.q, a8_tmp.d, a8_tmp.fs, nullptr,
+                                  nullptr, work, out, tok_dst);
+    }
+    SegTable tab = {};
+    tab.count = 1;
+    tab.s[0] = Seg{(const uint8_t *)W, nullptr, rows, rows, 0, 0};
+    tab.total_waves = (rows + 63) / 64;
+    const int blocks = (tab.total_waves + 3) / 4;
+    unsigned long long *keys = (unsigned long long *)work;
+    q4k_mvr_k<<<blocks, 256, 0, ctx->stream>>>(
+        tab, cols, HeadRow{x, x_stride, add, add_stride, w, eps, idx, off, nrows, y}, keys);
+    NMX_LAUNCHED(ctx, "q4k_mvr");
+    head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, 1, nullptr, out, tok_dst,
+                                                FinishCommit{nullptr, nullptr, nullptr, 0});
+    NMX_LAUNCHED(ctx, "head_finish");
+    return 0;
 }
 
 int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int n,

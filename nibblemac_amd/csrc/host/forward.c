@@ -223,14 +223,23 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     if (rc) return rc;
     resid_done(&r);
     if ((rc = mlp_block(c, L, n, &r))) return rc;
+    const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
+    const int off = head_row_dynamic ? -1 : n - 1;
+    if (draft_dst && H <= 1024 && H % 256 == 0) {
+        /* the selected row's final norm (its MTP hidden to m_dst; a single row always to s->xn)
+         * inside the draft head's workgroups */
+        float *y = m_dst ? m_dst : n == 1 && !head_row_dynamic ? s->xn : NULL;
+        CK(nmx_head_row_accept_to(D, c->head.w, nv, H, r.cur, H, r.add, H, c->mtp_norm_out,
+                                  c->rms_eps, idx, off, n, y, c->hwork, c->hout2, draft_dst,
+                                  s->a_1));
+        return PINFER_OK;
+    }
     if (n == 1 && !head_row_dynamic) {
         /* one row: the final norm writes the MTP hidden and the head's A8 input itself */
         CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, 1, H, c->rms_eps,
                           m_dst ? m_dst : s->xn, H, draft_dst ? s->a_1 : none));
         return draft_dst ? head_a8(c, nv, draft_dst, 0) : PINFER_OK;
     }
-    const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
-    const int off = head_row_dynamic ? -1 : n - 1;
     if (H <= 1024 && H % 32 == 0 && (m_dst || draft_dst)) {
         /* only the selected row: its MTP hidden and the head's A8 input, one launch */
         CK(nmx_rmsnorm_row(D, r.cur, H, r.add, H, c->mtp_norm_out, H, c->rms_eps, idx, off, n,

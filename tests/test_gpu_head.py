@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
+from tests.test_gpu_q4k import assert_bits_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -257,3 +258,44 @@ def test_head_accept_to_writes_token(dev):
     assert list(out.numpy()) == [0, g, g] and list(tok.numpy()) == [-5, g]
     for b in (dW, dq, dd, dfs, work, out, tok):
         b.free()
+
+
+@pytest.mark.parametrize("case", [(0, 0, 1, 32768, True, True), (3, -1, 5, 32768, True, True),
+                                  (9, -1, 5, 10004, True, False), (0, -1, 5, 32768, False, True)],
+                         ids=["row0_of1", "row2_of5", "clamped_no_y", "below0_no_add"])
+def test_head_row_accept_equals_norm_then_head(dev, case):
+    """nmx_head_row_accept_to (the MTP draft head with its final RMSNorm inside the head's
+    workgroups) against nmx_rmsnorm_row + nmx_head_accept_to: the argmax, the draft written to
+    tok_dst and the normed row y bit for bit, for a device-selected row (clamped at both ends),
+    with and without the residual add and the y output."""
+    idx0, off, nrows, rows, with_add, want_y = case
+    cols, eps = 1024, 1e-6
+    print(f"[case] head_row_accept {case}", flush=True)
+    rng = np.random.default_rng(500 + idx0 + rows)
+    W = quantized_head(rng, rows, cols)
+    x = rng.standard_normal((nrows, cols)).astype(np.float32)
+    add = rng.standard_normal((nrows, cols)).astype(np.float32) if with_add else None
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    dW, dx, dw = dev.to_device(W), dev.to_device(x), dev.to_device(w)
+    dadd = dev.to_device(add) if with_add else None
+    didx = dev.to_device(np.array([idx0], np.int32))
+    nb = cols // 32
+    a8 = (dev.zeros((nb, 1, 32), np.int8), dev.zeros((nb, 1), np.float32),
+          dev.zeros((nb, 1), np.float32))
+    y_ref = dev.zeros((1, cols), np.float32)
+    dev.rmsnorm_row(dx, nrows, cols, dw, eps, didx, off, add=dadd, y=y_ref, a8=a8)
+    work_ref = dev.zeros(dev.head_work_bytes(rows, 1), np.uint8)
+    out_ref, tok_ref = dev.zeros(3, np.int32), dev.zeros(1, np.int32)
+    dev.head_accept(dW, rows, cols, 1, *a8, None, None, work_ref, out_ref, tok_dst=tok_ref)
+    y = dev.zeros((1, cols), np.float32)
+    work = dev.zeros(dev.head_work_bytes(rows, 1), np.uint8)
+    out, tok = dev.zeros(3, np.int32), dev.zeros(1, np.int32)
+    dev.head_row_accept_to(dW, rows, cols, dx, nrows, dw, eps, didx, off, work, out, tok,
+                           add=dadd, y=y if want_y else None)
+    dev.sync()
+    assert_bits_equal(out.numpy(), out_ref.numpy(), "out")
+    assert_bits_equal(tok.numpy(), tok_ref.numpy(), "draft token")
+    if want_y:
+        assert_bits_equal(y.numpy(), y_ref.numpy(), "y")
+    else:
+        assert not y.numpy().any(), "y written without being asked for"
