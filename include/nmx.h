@@ -203,11 +203,14 @@ int nmx_rmsnorm_row(nmx_ctx *ctx, const float *x, int x_stride, const float *add
  * draft head on its final norm (engine/src/mtp.c:88-100). The norm runs inside the head's
  * workgroups (one launch fewer; y, out and tok_dst equal those of the two calls bit for bit)
  * when cols is a multiple of 256 up to 1024 and x, add, w, y are 16-byte aligned rows; else
- * the two calls, with a8_tmp (one cols-column A8 row) for the norm's output. */
+ * the two calls, with a8_tmp (one cols-column A8 row) for the norm's output. advance (a
+ * control block, may be NULL): nmx_ctl_advance(advance) after the head, done by its last
+ * kernel (a round ending with the MTP pass over the committed rows). */
 int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
                            int x_stride, const float *add, int add_stride, const float *w,
                            float eps, const int32_t *idx, int off, int nrows, float *y,
-                           void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp);
+                           void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp,
+                           int32_t *advance);
 
 int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
                      const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,

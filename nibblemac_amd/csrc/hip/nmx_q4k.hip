@@ -350,6 +350,7 @@ __global__ __launch_bounds__(64 * WPG) void q4k_mvx_k(SegTable tab, int cols, in
 struct FinishCommit {
     int32_t *vt, *ctl, *mb;
     int nvt;
+    int32_t *adv; /* not NULL: adv[0] += adv[1] last (a round's n_past += e) */
 };
 
 /* The one-row head with its input's RMSNorm inside (nmx_head_row_accept_to): row *idx + off of
@@ -522,6 +523,7 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
                 __hip_atomic_store(fc.mb + 2 + fc.nvt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
+        if (fc.adv) fc.adv[0] = fc.adv[0] + fc.adv[1];
     }
 }
 
@@ -1121,13 +1123,14 @@ int nmx_head_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
                        const float *d, const float *fsum, float *logits, const int32_t *drafts,
                        void *work, int32_t *out, int32_t *tok_dst) {
     return head_accept(ctx, W, rows, cols, n, q, d, fsum, logits, drafts, work, out, tok_dst,
-                       FinishCommit{nullptr, nullptr, nullptr, 0});
+                       FinishCommit{nullptr, nullptr, nullptr, 0, nullptr});
 }
 
 int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
                            int x_stride, const float *add, int add_stride, const float *w,
                            float eps, const int32_t *idx, int off, int nrows, float *y,
-                           void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp) {
+                           void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp,
+                           int32_t *advance) {
     if (!ctx) return -1;
     if (!W || !x || !w || !idx || !work || !out || nrows < 1 || x_stride < cols ||
         (add && add_stride < cols))
@@ -1143,8 +1146,10 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
         if (nmx_rmsnorm_row(ctx, x, x_stride, add, add_stride, w, cols, eps, idx, off, nrows, y,
                             a8_tmp))
             return -1;
-        return nmx_head_accept_to(ctx, W, rows, cols, 1, a8_tmp.q, a8_tmp.d, a8_tmp.fs, nullptr,
-                                  nullptr, work, out, tok_dst);
+        if (nmx_head_accept_to(ctx, W, rows, cols, 1, a8_tmp.q, a8_tmp.d, a8_tmp.fs, nullptr,
+                               nullptr, work, out, tok_dst))
+            return -1;
+        return advance ? nmx_ctl_advance(ctx, advance) : 0;
     }
     SegTable tab = {};
     tab.count = 1;
@@ -1156,7 +1161,7 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
         tab, cols, HeadRow{x, x_stride, add, add_stride, w, eps, idx, off, nrows, y}, keys);
     NMX_LAUNCHED(ctx, "q4k_mvr");
     head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, 1, nullptr, out, tok_dst,
-                                                FinishCommit{nullptr, nullptr, nullptr, 0});
+                                                FinishCommit{nullptr, nullptr, nullptr, 0, advance});
     NMX_LAUNCHED(ctx, "head_finish");
     return 0;
 }
@@ -1169,7 +1174,7 @@ int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int 
     if (!vt || !ctl || (mailbox && (nvt < n + 1 || nvt > 1024)))
         return nmx_fail(ctx, "nmx_head_accept_commit: bad arguments");
     return head_accept(ctx, W, rows, cols, n, q, d, fsum, nullptr, drafts, work, out, nullptr,
-                       FinishCommit{vt, ctl, mailbox, mailbox ? nvt : 0});
+                       FinishCommit{vt, ctl, mailbox, mailbox ? nvt : 0, nullptr});
 }
 
 } /* extern "C" */

@@ -165,7 +165,7 @@ struct pinfer_ctx {
 int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged);
 int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits);
 int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst);
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst, int advance);
 int e_set_pos(pinfer_ctx *c, int pos);
 
 /* spec.c */

@@ -199,9 +199,10 @@ int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits) {
 /* The MTP draft head (engine/src/mtp.c:60-100) over n rows: h_dev [n][H] final-normed
  * hiddens, tok_dev [n] the tokens that follow them, positions ctl[0] + pos_off + i. The
  * selected row (n - 1, or ctl[1] - 1 when head_row_dynamic) gives the draft (argmax over the
- * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL). */
+ * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL). advance:
+ * ctl[0] += ctl[1] at the end (folded into the draft head's last kernel where it can be). */
 int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst) {
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst, int advance) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H;
@@ -231,23 +232,25 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
         float *y = m_dst ? m_dst : n == 1 && !head_row_dynamic ? s->xn : NULL;
         CK(nmx_head_row_accept_to(D, c->head.w, nv, H, r.cur, H, r.add, H, c->mtp_norm_out,
                                   c->rms_eps, idx, off, n, y, c->hwork, c->hout2, draft_dst,
-                                  s->a_1));
+                                  s->a_1, advance ? c->ctl : NULL));
         return PINFER_OK;
     }
     if (n == 1 && !head_row_dynamic) {
         /* one row: the final norm writes the MTP hidden and the head's A8 input itself */
         CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, 1, H, c->rms_eps,
                           m_dst ? m_dst : s->xn, H, draft_dst ? s->a_1 : none));
-        return draft_dst ? head_a8(c, nv, draft_dst, 0) : PINFER_OK;
-    }
-    if (H <= 1024 && H % 32 == 0 && (m_dst || draft_dst)) {
+        if (draft_dst) TRY(head_a8(c, nv, draft_dst, 0));
+    } else if (H <= 1024 && H % 32 == 0 && (m_dst || draft_dst)) {
         /* only the selected row: its MTP hidden and the head's A8 input, one launch */
         CK(nmx_rmsnorm_row(D, r.cur, H, r.add, H, c->mtp_norm_out, H, c->rms_eps, idx, off, n,
                            m_dst, draft_dst ? s->a_1 : none));
-        return draft_dst ? head_a8(c, nv, draft_dst, 0) : PINFER_OK;
+        if (draft_dst) TRY(head_a8(c, nv, draft_dst, 0));
+    } else {
+        CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn,
+                          H, none));
+        if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));
+        if (draft_dst) TRY(head_row(c, idx, off, nv, draft_dst, 0));
     }
-    CK(nmx_rmsnorm_xo(D, r.cur, H, r.add, H, NULL, 0, c->mtp_norm_out, n, H, c->rms_eps, s->xn, H,
-                      none));
-    if (m_dst) CK(nmx_select_row(D, s->xn, H, idx, off, H, m_dst));
-    return draft_dst ? head_row(c, idx, off, nv, draft_dst, 0) : PINFER_OK;
+    if (advance) CK(nmx_ctl_advance(D, c->ctl));
+    return PINFER_OK;
 }

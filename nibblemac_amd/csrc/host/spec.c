@@ -85,16 +85,16 @@ static int commit_lin_cur(pinfer_ctx *c, int redo) {
 /* One MTP round of ke drafts (engine/src/spec.c:303-365): the chain d2..dk, the verify, the
  * commit of e = ctl[1], the MTP head over the committed rows (its hidden of row e - 1 and the
  * next d1; the pass reads the verify's final-normed rows, s.xn, which at hidden <= 1024 it
- * never writes, and otherwise writes only after its last read), n_past += e. */
+ * never writes, and otherwise writes only after its last read), n_past += e (done by the
+ * pass's last kernel). */
 static int seq_round(pinfer_ctx *c, int ke, int nv) {
     for (int s = 1; s < ke; s++) {
         const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
-        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s)));
+        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), 0));
     }
     TRY(seq_verify(c, ke));
     TRY(commit_lin_cur(c, 0));
-    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c)));
-    CK(nmx_ctl_advance(c->dev, c->ctl));
+    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c), 1));
     return PINFER_OK;
 }
 
@@ -212,7 +212,7 @@ static int prefill(pinfer_ctx *c, const int32_t *prompt, int n, int use_mtp, int
             CK(nmx_upload(c->dev, c->tok, next, (size_t)nb * sizeof(int32_t)));
             if (last) CK(nmx_copy_d2d(c->dev, c->tok + nb - 1, c->vt, sizeof(int32_t)));
             TRY(e_mtp_forward(c, c->hbuf, c->tok, nb, 0, 0, nv, last ? c->vt + 1 : NULL,
-                              last ? m_cur(c) : NULL));
+                              last ? m_cur(c) : NULL, 0));
         }
         c->n_past += nb;
     }
@@ -247,7 +247,7 @@ static int flush_pending(pinfer_ctx *c, e_pending *pd, int nv) {
     if (pd->n == 0) return PINFER_OK;
     CK(nmx_upload(c->dev, c->tok, pd->tok, (size_t)pd->n * sizeof(int32_t)));
     TRY(e_set_pos(c, pd->pos));
-    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c)));
+    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c), 0));
     c->mtp_rows = pd->pos + pd->n;
     pd->n = 0;
     TRY(e_set_pos(c, c->n_past));

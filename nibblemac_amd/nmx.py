@@ -105,7 +105,7 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_accept_to": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_row_accept_to": (_i, [_vp, _vp, _i, _i, _vp, _i, _vp, _i, _vp, ctypes.c_float, _vp,
-                                    _i, _i, _vp, _vp, _vp, _vp, A8]),
+                                    _i, _i, _vp, _vp, _vp, _vp, A8, _vp]),
     "nmx_head_accept_noalloc": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_accept_commit": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _i]),
@@ -416,13 +416,14 @@ class Device:
 
     def head_row_accept_to(self, W, rows: int, cols: int, x, nrows: int, w, eps: float, idx,
                            off: int, work, out, tok_dst, *, add=None, y=None,
-                           a8_tmp=(None, None, None)) -> None:
+                           a8_tmp=(None, None, None), advance=None) -> None:
         """nmx_head_row_accept_to: the one-row head on the RMSNorm of row idx[0] + off of
-        contiguous rows x [nrows][cols] (+ add), the norm inside the head's workgroups."""
+        contiguous rows x [nrows][cols] (+ add), the norm inside the head's workgroups;
+        advance (int32 control block): advance[0] += advance[1] after the head."""
         self.check(self.lib.nmx_head_row_accept_to(self.ctx, _p(W), rows, cols, _p(x), cols,
                                                    _p(add), cols, _p(w), eps, _p(idx), off, nrows,
                                                    _p(y), _p(work), _p(out), _p(tok_dst),
-                                                   A8(*[_p(t) for t in a8_tmp])),
+                                                   A8(*[_p(t) for t in a8_tmp]), _p(advance)),
                    "head_row_accept_to")
 
     def head_accept_noalloc(self, W, rows: int, cols: int, n: int, q, d, fs, logits, drafts,

@@ -267,7 +267,8 @@ def test_head_row_accept_equals_norm_then_head(dev, case):
     """nmx_head_row_accept_to (the MTP draft head with its final RMSNorm inside the head's
     workgroups) against nmx_rmsnorm_row + nmx_head_accept_to: the argmax, the draft written to
     tok_dst and the normed row y bit for bit, for a device-selected row (clamped at both ends),
-    with and without the residual add and the y output."""
+    with and without the residual add and the y output; with a control block to advance
+    (n_past += e by the head's last kernel) on the cases that keep y."""
     idx0, off, nrows, rows, with_add, want_y = case
     cols, eps = 1024, 1e-6
     print(f"[case] head_row_accept {case}", flush=True)
@@ -290,9 +291,13 @@ def test_head_row_accept_equals_norm_then_head(dev, case):
     y = dev.zeros((1, cols), np.float32)
     work = dev.zeros(dev.head_work_bytes(rows, 1), np.uint8)
     out, tok = dev.zeros(3, np.int32), dev.zeros(1, np.int32)
+    ctl0 = np.array([1000 + idx0, 3 + idx0, 77], np.int32)
+    dctl = dev.to_device(ctl0) if want_y else None
     dev.head_row_accept_to(dW, rows, cols, dx, nrows, dw, eps, didx, off, work, out, tok,
-                           add=dadd, y=y if want_y else None)
+                           add=dadd, y=y if want_y else None, advance=dctl)
     dev.sync()
+    if want_y:
+        assert dctl.numpy().tolist() == [ctl0[0] + ctl0[1], ctl0[1], 77], "control block"
     assert_bits_equal(out.numpy(), out_ref.numpy(), "out")
     assert_bits_equal(tok.numpy(), tok_ref.numpy(), "draft token")
     if want_y:
