@@ -292,6 +292,18 @@ int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int
                         float *const *Y, const int *y_stride, int cols, int n,
                         const nmx_norm_in *in, nmx_a8 a8_tmp);
 
+/* The MTP head's fc projection on its input pair (engine/src/mtp.c:60-75): Y[n][rows] = W a
+ * (W rows x 2 H) with a the A8 of [rmsnorm(embedding rows tok[0..n) of the Q4K matrix E, w_emb)
+ * | rmsnorm(h, w_hid)], equal bit for bit to nmx_embed_norm (both halves' A8 into one 2 H-column
+ * buffer) followed by nmx_q4k_matmul. The embedding and both norms run inside the matmul's
+ * workgroups (one launch) when n <= 8, H is a multiple of 256, h, w_emb and w_hid are 16-byte
+ * aligned and the shape fits; otherwise a8_tmp (n x 2 H A8, the two calls; H <= 1024) is
+ * used. */
+int nmx_q4k_matmul_embed_norm(nmx_ctx *ctx, const void *W, int rows, float *Y, int y_stride,
+                              int n, int H, const void *E, int vocab, const int32_t *tok,
+                              const float *w_emb, const float *h, int h_stride,
+                              const float *w_hid, float eps, nmx_a8 a8_tmp);
+
 /* The SwiGLU MLP input (engine/src/forward.c:49-58, forward_ops.c:98-110): h = silu(Wg a) *
  * (Wu a) for a = the A8 input (q, d, fsum) or, when in is not NULL, the A8 of rmsnorm(in);
  * h is written as A8 to out (and as floats [n][ffn] to y if not NULL). Fused into one launch

@@ -54,12 +54,24 @@ struct nmx_mt_seg {
     int ystride;
 };
 
+/* The MTP head's fc input as a norm prologue: the embedding rows tok[] of the Q4K matrix E
+ * normed with w_emb, then the rows of h (row stride h_stride, 16-byte aligned) normed with
+ * norm->w; eps is norm->eps. */
+struct nmx_mt_pair {
+    const uint8_t *E;
+    const int32_t *tok;
+    const float *w_emb;
+    const float *h;
+    int h_stride;
+};
+
 /* Small-row Q4K matmul with every vector of a pass in one workgroup (nmx_mt.hip), optionally
- * with the RMSNorm + A8 prologue (norm) and the SwiGLU + A8 epilogue (swiglu: segments gate,
- * up). Returns 0, -1 on a launch error, or 1 when the shape is outside its limits. */
+ * with the RMSNorm + A8 prologue (norm; with pair, the MTP input pair of norms) and the
+ * SwiGLU + A8 epilogue (swiglu: segments gate, up). Returns 0, -1 on a launch error, or 1
+ * when the shape is outside its limits. */
 int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int n,
                   const int8_t *q, const float *d, const float *fs, const nmx_norm_in *norm,
-                  bool swiglu, nmx_a8 out);
+                  bool swiglu, nmx_a8 out, const nmx_mt_pair *pair = nullptr);
 
 
 /* Resolve the device address of nmx_head_accept_noalloc's static scratch array for

@@ -43,6 +43,13 @@ struct MtTab {
     int count;
 };
 
+/* The PAIR prologue's embedding half: the Q4K embedding E and its norm weight (the other half's
+ * weight and eps come in nmx_norm_in). */
+struct MtPair {
+    const uint8_t *E;
+    const float *w0;
+};
+
 __device__ __forceinline__ float half_bits(uint32_t h) {
     const unsigned short b = (unsigned short)h;
     _Float16 f;
@@ -67,6 +74,29 @@ __device__ __forceinline__ void decode6_half(uint32_t L0, uint32_t L1, uint32_t 
     }
 }
 
+/* The 32 values of 32-column block b of Q4K row `row` (cols columns), as the embedding
+ * kernels compute them (dequantised (D s) q - M m, engine/src/kern_act.c:47-88): the
+ * superblock's 64-byte scale line and the row's 16 code bytes in five 16-byte loads. */
+__device__ __forceinline__ void q4k_block32(const uint8_t *__restrict__ E, int row, int cols, int b,
+                                            float out[32]) {
+    const int sb = b >> 3, k = b & 7, i = row & 3;
+    const uint4 *p = (const uint4 *)(E + ((size_t)(row >> 2) * (cols >> 8) + sb) * 576);
+    const uint4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3], cw = p[4 + 4 * k + i];
+    int s6[4], m6[4];
+    decode6_half(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, 8 * i, k >> 2, s6);
+    decode6_half(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, 8 * i, k >> 2, m6);
+    const float D = half_bits(((i & 2) ? a0.y : a0.x) >> (16 * (i & 1)));
+    const float M = half_bits(((i & 2) ? a0.w : a0.z) >> (16 * (i & 1)));
+    const float dd = D * (float)s6[k & 3], mm = M * (float)m6[k & 3];
+    const uint32_t w[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        out[j] = dd * (float)(byte & 15u) - mm;
+        out[16 + j] = dd * (float)(byte >> 4) - mm;
+    }
+}
+
 /* Byte offset of block b's NV x 32 activation codes in LDS: 16 bytes of padding per
  * superblock, so the units of different superblocks read different banks. */
 __host__ __device__ constexpr int aq_off(int b, int nv) { return b * nv * 32 + (b >> 3) * 16; }
@@ -77,7 +107,8 @@ struct MtLayout {
     int aq, ad, afs, work, res, total;
 };
 
-__host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm, bool swiglu) {
+__host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm, bool swiglu,
+                                              bool pair = false) {
     const int nb = cols >> 5;
     MtLayout L{};
     L.aq = 0;
@@ -87,8 +118,10 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     /* chain records: (dot, (D*s)*d, -(M*m), fsum) float4 [nb][nv][R]; the SwiGLU launch (64
      * rows) keeps ((float)dot, (D*s)*d) float2 [nb][nv][R] and -(M*m) [nb][R] to fit */
     int work = swiglu ? nb * nv * R * 8 + nb * R * 4 : nb * nv * R * 16;
-    /* the norm prologue: chain-major squares, then the summed rows [nv][cols] */
-    const int nwork = nv * (4 * cm_stride4(cols) + 4) * 4 + nv * cols * 4;
+    /* the norm prologue: chain-major squares, then the summed rows [nv][cols] (PAIR: 2 nv rows
+     * of cols / 2) */
+    const int nr = pair ? 2 * nv : nv, rc = pair ? cols / 2 : cols;
+    const int nwork = nr * (4 * cm_stride4(rc) + 4) * 4 + nr * rc * 4;
     if (norm && nwork > work) work = nwork;
     L.res = L.work + work;
     L.total = L.res + (swiglu ? nv * R * 4 : 0);
@@ -101,19 +134,24 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
  * are the A8 codes and scales (q, d), or with NORM the norm input rows x and add; aux is the
  * A8 fsum pointer, or with NORM the row strides of x (low 32 bits) and add (high); W0 / rows0
  * the first segment's weights and rows; T the block size (blockDim lives in the argument
- * segment). */
-template <int NV, bool NORM, bool SWI, int BPU>
+ * segment).
+ * PAIR (with NORM): the MTP head's fc input (engine/src/mtp.c:60-75), activation row v =
+ * [rmsnorm(embedding row tok[v0 + v] of pr.E, pr.w0) | rmsnorm(row v0 + v of h, nm.w)], each
+ * half cols / 2 columns (a multiple of 256, so no A8 block straddles them); in0 = h, in1 =
+ * tok, aux = h's row stride; T >= cols / 8 (one float4 of each half per thread). */
+template <int NV, bool NORM, bool SWI, int BPU, bool PAIR = false>
 __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_MAX_THREADS : MT_REC4_THREADS) void q4k_mt_k(
     const void *__restrict__ in0, const void *__restrict__ in1, uint64_t aux,
     const uint8_t *__restrict__ W0, int cols, int n, int v0, int R, int T, int rows0,
     MtTab tab, nmx_norm_in nm, int8_t *__restrict__ oq, float *__restrict__ od,
-    float *__restrict__ ofs) {
+    float *__restrict__ ofs, MtPair pr) {
+    static_assert(!PAIR || (NORM && !SWI), "PAIR is a norm prologue of a plain matmul");
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float red[5 * MT_MAX_NV];
+    __shared__ float red[(PAIR ? 10 : 5) * MT_MAX_NV];
     const int tid = threadIdx.x;
     const int8_t *q = (const int8_t *)in0;
     const float *d = (const float *)in1, *fs = (const float *)(uintptr_t)aux;
-    const float *nx = (const float *)in0, *nadd = (const float *)in1;
+    const float *nx = (const float *)in0, *nadd = PAIR ? nullptr : (const float *)in1;
     const int xs = (int)(uint32_t)aux, as = (int)(uint32_t)(aux >> 32);
     const int nb = cols >> 5, nsb = cols >> 8;
     /* norm prologue columns per thread: wide workgroups of 1- or 2-block units need 2 */
@@ -166,8 +204,20 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     }
     /* the norm inputs: x and add stay in separate registers until the weight loads below are
      * issued (adding them here would wait for their memory round trip first) */
-    float xv[NORM ? NV : 1][CPT], av[NORM ? NV : 1][CPT];
-    if constexpr (NORM) { /* rows v0 .. v0 + NV - 1 (+ add): thread columns c = tid + T j */
+    constexpr bool NX = NORM && !PAIR;
+    float xv[NX ? NV : 1][CPT], av[NX ? NV : 1][CPT];
+    /* PAIR: float4 tid of each h row, and thread (v, b) = (tid / nbh, tid % nbh) decodes block
+     * b of embedding row tok[v0 + v] (its token now, its loads after the weights') */
+    const int m4h = cols >> 3, mi = tid < m4h ? tid : m4h - 1, nbh = cols >> 6;
+    const int ev = tid / nbh, eb = tid - ev * nbh;
+    int etok = 0;
+    float4 h4[PAIR ? NV : 1];
+    if constexpr (PAIR) {
+        etok = ((const int32_t *)in1)[v0 + (ev < NV ? ev : NV - 1)];
+#pragma unroll
+        for (int v = 0; v < NV; v++) h4[v] = ((const float4 *)(nx + (size_t)(v0 + v) * xs))[mi];
+    }
+    if constexpr (NX) { /* rows v0 .. v0 + NV - 1 (+ add): thread columns c = tid + T j */
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
             const int cc = tid + T * j;
@@ -209,7 +259,11 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
         for (int k = 0; k < BPU; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
     }
 
-    if constexpr (NORM) { /* the residual add, now that the weight loads are in flight */
+    float ev32[PAIR ? 32 : 1];
+    if constexpr (PAIR) {
+        if (ev < NV) q4k_block32(pr.E, etok, cols >> 1, eb, ev32);
+    }
+    if constexpr (NX) { /* the residual add, now that the weight loads are in flight */
         if (nadd) {
 #pragma unroll
             for (int j = 0; j < CPT; j++) {
@@ -260,10 +314,42 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
         }
     }
     if constexpr (NORM) {
-        /* RMSNorm (sumsq: 4 interleaved partial sums + tail, chain-major squares in LDS) */
-        const int s4 = cm_stride4(cols), rsz = 4 * s4 + 4, m4 = cols >> 2;
+        /* RMSNorm (sumsq: 4 interleaved partial sums + tail, chain-major squares in LDS) of NR
+         * rows of rc columns: the NV input rows, or (PAIR) the NV embedding rows then the NV h
+         * rows, each cols / 2 wide */
+        constexpr int NR = PAIR ? 2 * NV : NV;
+        const int rc = PAIR ? cols >> 1 : cols;
+        const int s4 = cm_stride4(rc), rsz = 4 * s4 + 4, m4 = rc >> 2;
         float *sq = (float *)(smem + L.work);
-        float *xs = sq + NV * rsz; /* the summed rows [NV][cols] */
+        float *xs = sq + NR * rsz; /* the summed rows [NR][rc] */
+        if constexpr (PAIR) {
+            if (tid < m4h) { /* h rows (rows NV..): float4 tid = terms tid of the four chains */
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const float4 x = h4[v];
+                    float *sr = sq + (NV + v) * rsz + tid;
+                    sr[0] = x.x * x.x;
+                    sr[s4] = x.y * x.y;
+                    sr[2 * s4] = x.z * x.z;
+                    sr[3 * s4] = x.w * x.w;
+                    *(float4 *)(xs + (NV + v) * rc + 4 * tid) = x;
+                }
+            }
+            if (ev < NV) { /* embedding block eb of row ev: terms 8 eb .. 8 eb + 7 of chain l are
+                            * its values l, l + 4, .., l + 28 */
+                float *sr = sq + ev * rsz + 8 * eb;
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const float *e = ev32 + l;
+                    *(float4 *)(sr + l * s4) = make_float4(e[0] * e[0], e[4] * e[4], e[8] * e[8], e[12] * e[12]);
+                    *(float4 *)(sr + l * s4 + 4) = make_float4(e[16] * e[16], e[20] * e[20], e[24] * e[24], e[28] * e[28]);
+                }
+                float *xr = xs + ev * rc + 32 * eb;
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    *(float4 *)(xr + 4 * u) = make_float4(ev32[4 * u], ev32[4 * u + 1], ev32[4 * u + 2], ev32[4 * u + 3]);
+            }
+        } else {
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
             const int cc = tid + T * j;
@@ -276,8 +362,9 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                 if (nm.x_out && blockIdx.x == 0) nm.x_out[(size_t)(v0 + v) * nm.xo_stride + cc] = xv[v][j];
             }
         }
+        }
         __syncthreads();
-        if (tid < 4 * NV) { /* chain l of row v, the next 32 terms' reads issued ahead */
+        if (tid < 4 * NR) { /* chain l of row v, the next 32 terms' reads issued ahead */
             const float *ch = sq + (tid >> 2) * rsz + (tid & 3) * s4;
             float a = 0.0f;
             int m = 0;
@@ -302,10 +389,10 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
             }
             for (; m < m4; m++) a = a + ch[m];
             red[tid] = a;
-        } else if (tid < 5 * NV) { /* the cols % 4 tail of row v */
-            const int v = tid - 4 * NV;
+        } else if (tid < 5 * NR) { /* the rc % 4 tail of row v */
+            const int v = tid - 4 * NR;
             float t = 0.0f;
-            for (int i = 4 * m4; i < cols; i++) t = t + sq[v * rsz + 4 * s4 + (i - 4 * m4)];
+            for (int i = 4 * m4; i < rc; i++) t = t + sq[v * rsz + 4 * s4 + (i - 4 * m4)];
             red[tid] = t;
         }
         __syncthreads();
@@ -315,10 +402,18 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
         for (int e2 = tid; e2 < 2 * nb * NV; e2 += T) { /* T is a multiple of 64: pairs stay whole */
             const int e = e2 >> 1, hf = e2 & 1;
             const int b = e / NV, v = e - b * NV;
-            const float sv = (red[4 * v] + red[4 * v + 1]) + (red[4 * v + 2] + red[4 * v + 3]);
-            const float r = 1.0f / sqrtf((sv + red[4 * NV + v]) / (float)cols + nm.eps);
-            const float4 *xp = (const float4 *)(xs + v * cols + 32 * b + 16 * hf);
-            const float4 *wp = (const float4 *)(nm.w + 32 * b + 16 * hf);
+            int vr = v, bc = b; /* normed row and its block */
+            const float *wr = nm.w;
+            if constexpr (PAIR) {
+                const int half = b >= (nb >> 1) ? 1 : 0;
+                vr = half * NV + v;
+                bc = b - half * (nb >> 1);
+                wr = half ? nm.w : pr.w0;
+            }
+            const float sv = (red[4 * vr] + red[4 * vr + 1]) + (red[4 * vr + 2] + red[4 * vr + 3]);
+            const float r = 1.0f / sqrtf((sv + red[4 * NR + vr]) / (float)rc + nm.eps);
+            const float4 *xp = (const float4 *)(xs + vr * rc + 32 * bc + 16 * hf);
+            const float4 *wp = (const float4 *)(wr + 32 * bc + 16 * hf);
             float y[16];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -517,7 +612,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
  * are one dependent sequence of LDS reads, dots and record stores, so more units shorten the
  * dot phase. */
 int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int count, int *threads,
-              int *bpu) {
+              int *bpu, bool pair = false) {
     *bpu = 4;
     const int nsb = cols >> 8;
     if (norm && !swiglu) {
@@ -525,13 +620,14 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
          * of 4) whose workgroups fit the 256 CUs in one round */
         for (int R = 4 * ((total_rows + 4 * 256 - 1) / (4 * 256)); R <= 64; R += 4) {
             if (R * 256 < total_rows + count * R) continue; /* each segment rounds up */
-            if (mt_layout(cols, nv, R, true, false).total > MT_LDS) break;
+            if (mt_layout(cols, nv, R, true, false, pair).total > MT_LDS) break;
             /* 1- or 2-block units in up to 1024 threads (2 prologue columns per thread) when
-             * they fit, else 4-block units (8 columns per thread, up to 512 threads) */
-            for (int b = 1; b <= 4; b *= 2) {
+             * they fit, else 4-block units (8 columns per thread, up to 512 threads); PAIR:
+             * one-block units, a float4 of each half per thread */
+            for (int b = 1; b <= (pair ? 1 : 4); b *= 2) {
                 const int units = R * (8 / b) * nsb;
                 const int t = 64 * (((units > R * nv ? units : R * nv) + 63) / 64);
-                const int cpt = b < 4 ? 2 : MT_NORM_CPT;
+                const int cpt = pair ? 8 : b < 4 ? 2 : MT_NORM_CPT;
                 const int tt = t * cpt < cols ? 64 * ((cols / cpt + 63) / 64) : t;
                 if (tt > (b < 4 ? MT_REC_THREADS : MT_NORM_THREADS)) continue;
                 *threads = tt;
@@ -557,24 +653,31 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
     return 0;
 }
 
-template <int NV, bool NORM, bool SWI, int BPU>
+template <int NV, bool NORM, bool SWI, int BPU, bool PAIR = false>
 int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
                const int8_t *q, const float *d, const float *fs, const nmx_norm_in &nm,
-               nmx_a8 out) {
+               nmx_a8 out, const nmx_mt_pair *pair = nullptr) {
     static bool ready = false; /* idempotent: a racing second call sets the same value */
     if (!ready) {
-        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI, BPU>,
+        NMX_HIP(ctx, hipFuncSetAttribute((const void *)q4k_mt_k<NV, NORM, SWI, BPU, PAIR>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, MT_LDS));
         ready = true;
     }
-    const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI).total;
+    const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI, PAIR).total;
     const void *in0 = NORM ? (const void *)nm.x : (const void *)q;
     const void *in1 = NORM ? (const void *)nm.add : (const void *)d;
-    const uint64_t aux = NORM ? ((uint64_t)(uint32_t)nm.add_stride << 32) | (uint32_t)nm.x_stride
-                              : (uint64_t)(uintptr_t)fs;
-    q4k_mt_k<NV, NORM, SWI, BPU><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
+    uint64_t aux = NORM ? ((uint64_t)(uint32_t)nm.add_stride << 32) | (uint32_t)nm.x_stride
+                        : (uint64_t)(uintptr_t)fs;
+    MtPair pr{nullptr, nullptr};
+    if (PAIR) {
+        in0 = pair->h;
+        in1 = pair->tok;
+        aux = (uint32_t)pair->h_stride;
+        pr = MtPair{pair->E, pair->w_emb};
+    }
+    q4k_mt_k<NV, NORM, SWI, BPU, PAIR><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
         in0, in1, aux, (const uint8_t *)tab.s[0].W, cols, n, v0, R, T, tab.s[0].rows, tab, nm,
-        out.q, out.d, out.fs);
+        out.q, out.d, out.fs, pr);
     NMX_LAUNCHED(ctx, "q4k_mt");
     return 0;
 }
@@ -582,8 +685,9 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
 template <int NV>
 int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
               int bpu, const int8_t *q, const float *d, const float *fs, const nmx_norm_in *nm,
-              bool swiglu, nmx_a8 out) {
+              bool swiglu, nmx_a8 out, const nmx_mt_pair *pair) {
     const nmx_norm_in none{};
+    if (pair) return launch_one<NV, true, false, 1, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out, pair);
     if (nm && swiglu) return launch_one<NV, true, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm && bpu == 1) return launch_one<NV, true, false, 1>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm && bpu == 2) return launch_one<NV, true, false, 2>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
@@ -597,11 +701,14 @@ int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v
 
 int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int n,
                   const int8_t *q, const float *d, const float *fs, const nmx_norm_in *norm,
-                  bool swiglu, nmx_a8 out) {
+                  bool swiglu, nmx_a8 out, const nmx_mt_pair *pair) {
     /* more rows than one pass: the row-per-lane / K-split kernels read the weights once for
      * all of them (prefill chunks) */
     if (count < 1 || count > NMX_MAX_SEGS || cols % 256 || n < 1 || n > MT_MAX_NV) return 1;
     if (swiglu && (count != 2 || segs[0].rows != segs[1].rows || segs[0].rows % 32)) return 1;
+    if (pair && (!norm || swiglu || cols % 512 || (uintptr_t)pair->w_emb & 15 ||
+                 (uintptr_t)pair->h & 15 || pair->h_stride % 4))
+        return 1;
     /* equal-size passes of at most MT_MAX_NV vectors, larger first: every pass performs the
      * same per-vector operations, so the split does not change any result */
     const int passes = (n + MT_MAX_NV - 1) / MT_MAX_NV;
@@ -612,7 +719,8 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
     int total_rows = 0;
     for (int s = 0; s < count; s++) total_rows += segs[s].rows;
     int bpu = 4;
-    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, total_rows, count, &T, &bpu);
+    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, total_rows, count, &T, &bpu,
+                            pair != nullptr);
     if (!R) return 1;
     MtTab tab{};
     tab.count = count;
@@ -631,14 +739,14 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
         const int Tn = T; /* the first (largest) pass's thread count covers every pass */
         int rc;
         switch (nv) {
-        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
-        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out); break;
+        case 8: rc = launch_nv<8>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        case 7: rc = launch_nv<7>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        case 6: rc = launch_nv<6>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        case 5: rc = launch_nv<5>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        case 4: rc = launch_nv<4>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        case 3: rc = launch_nv<3>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        case 2: rc = launch_nv<2>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
+        default: rc = launch_nv<1>(ctx, tab, groups, cols, n, v0, R, Tn, bpu, q, d, fs, norm, swiglu, out, pair); break;
         }
         if (rc) return rc;
         v0 += nv;
@@ -688,6 +796,39 @@ int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int
         return -1;
     return nmx_q4k_matmul_multi(ctx, count, W, rows, Y, y_stride, cols, n, a8_tmp.q, a8_tmp.d,
                                 a8_tmp.fs);
+}
+
+int nmx_q4k_matmul_embed_norm(nmx_ctx *ctx, const void *W, int rows, float *Y, int y_stride,
+                              int n, int H, const void *E, int vocab, const int32_t *tok,
+                              const float *w_emb, const float *h, int h_stride,
+                              const float *w_hid, float eps, nmx_a8 a8_tmp) {
+    if (!ctx) return -1;
+    if (!W || !Y || !E || !tok || !w_emb || !h || !w_hid || rows <= 0 || rows % 4 ||
+        y_stride < rows || H < 256 || H % 256 || H > 32768 || vocab <= 0 || vocab % 4 ||
+        n < 1 || n > 4096 || h_stride < H)
+        return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: bad arguments");
+    if (nmx_overlap(Y, ((size_t)(n - 1) * y_stride + rows) * 4, h,
+                    ((size_t)(n - 1) * h_stride + H) * 4))
+        return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: Y aliases h");
+    if (n <= MT_MAX_NV && rows < 32768) {
+        const nmx_norm_in nm{nullptr, 0, nullptr, 0, nullptr, 0, w_hid, eps};
+        const nmx_mt_pair pr{(const uint8_t *)E, tok, w_emb, h, h_stride};
+        const nmx_mt_seg seg{(const uint8_t *)W, Y, rows, y_stride};
+        const int rc = nmx_mt_matmul(ctx, 1, &seg, 2 * H, n, nullptr, nullptr, nullptr, &nm, false,
+                                     nmx_a8{}, &pr);
+        if (rc <= 0) return rc;
+    }
+    /* the two calls: both halves' A8 blocks into a8_tmp ([block][n][32], the embedding's
+     * blocks first), then the matmul */
+    if (!a8_tmp.q || !a8_tmp.d || !a8_tmp.fs)
+        return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: shape needs the a8_tmp buffers");
+    const size_t hb = (size_t)(H / 32) * n;
+    const nmx_a8 a1 = {a8_tmp.q + hb * 32, a8_tmp.d + hb, a8_tmp.fs + hb};
+    if (nmx_embed_norm(ctx, E, vocab, tok, n, H, eps, w_emb, nullptr, 0, nullptr, 0, a8_tmp, h,
+                       h_stride, w_hid, nullptr, 0, a1))
+        return -1;
+    return nmx_q4k_matmul(ctx, W, rows, 2 * H, n, a8_tmp.q, a8_tmp.d, a8_tmp.fs, Y, y_stride,
+                          nullptr);
 }
 
 int nmx_q4k_swiglu(nmx_ctx *ctx, const void *Wg, const void *Wu, int ffn, int cols, int n,

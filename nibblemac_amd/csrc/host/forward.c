@@ -207,17 +207,25 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     e_scratch *s = &c->s;
     const int H = c->H;
     const nmx_a8 none = {NULL, NULL, NULL};
-    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)], the embedding and
-     * both norms in one launch: each norm writes the A8 blocks of its half of the 2H row
-     * (blocks [0, H/32) and [H/32, 2H/32) of the [block][n][32] layout); a block never
-     * straddles the halves (H % 32 == 0) */
-    const size_t hb = (size_t)(H / 32) * n;
-    const nmx_a8 a8_emb = s->a_w, a8_hid = {s->a_w.q + hb * 32, s->a_w.d + hb, s->a_w.fs + hb};
-    CK(nmx_embed_norm(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps, c->mtp_norm_emb, s->emb,
-                      H, s->cat, 2 * H, a8_emb, h_dev, H, c->mtp_norm_hid, s->cat + H, 2 * H,
-                      a8_hid));
+    /* fc input [pre_fc_norm_embedding(embed(tok)) | pre_fc_norm_hidden(h)]: each norm gives
+     * the A8 blocks of its half of the 2H row (blocks [0, H/32) and [H/32, 2H/32)); a block
+     * never straddles the halves (H % 32 == 0). At most 8 rows, the embedding and both norms
+     * run inside the fc matmul's workgroups; else one launch for them, then the matmul */
     e_resid r = {s->x, s->x2, NULL};
-    CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H, NULL));
+    if (n <= 8 && H % 256 == 0 && H <= 1024) {
+        /* the embedding and both norms inside the fc matmul's workgroups */
+        CK(nmx_q4k_matmul_embed_norm(D, c->mtp_fc.w, H, r.cur, H, n, H, c->embed.w, c->vocab,
+                                     tok_dev, c->mtp_norm_emb, h_dev, H, c->mtp_norm_hid,
+                                     c->rms_eps, s->a_w));
+    } else {
+        const size_t hb = (size_t)(H / 32) * n;
+        const nmx_a8 a8_emb = s->a_w, a8_hid = {s->a_w.q + hb * 32, s->a_w.d + hb, s->a_w.fs + hb};
+        CK(nmx_embed_norm(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps, c->mtp_norm_emb,
+                          s->emb, H, s->cat, 2 * H, a8_emb, h_dev, H, c->mtp_norm_hid, s->cat + H,
+                          2 * H, a8_hid));
+        CK(nmx_q4k_matmul(D, c->mtp_fc.w, H, 2 * H, n, s->a_w.q, s->a_w.d, s->a_w.fs, r.cur, H,
+                          NULL));
+    }
     const e_layer *L = &c->mtp;
     const nmx_norm_in in = resid_norm(c, &r, L->in_norm);
     int rc = attn_block(c, L, n, c->mkc, c->mvc, pos_off, &in);

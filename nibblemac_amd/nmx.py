@@ -120,6 +120,8 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_rmsnorm_xo": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _i,
                             A8]),
     "nmx_silu_mul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, A8]),
+    "nmx_q4k_matmul_embed_norm": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp, _vp, _vp,
+                                       _i, _vp, ctypes.c_float, A8]),
     "nmx_q4k_matmul_norm": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, ctypes.POINTER(NormIn),
                                  A8]),
     "nmx_lin_pre": (_i, [_vp, ctypes.POINTER(LinPreArgs)]),
@@ -339,6 +341,16 @@ class Device:
                                            _p(xo0), cols, _p(y0), cols, A8(*[_p(t) for t in a0]),
                                            _p(x1), cols, _p(w1), _p(y1), cols,
                                            A8(*[_p(t) for t in a1])), "embed_norm")
+
+    def q4k_matmul_embed_norm(self, W, rows: int, Y, n: int, H: int, E, vocab: int, tok, w_emb,
+                              h, w_hid, eps: float, a8_tmp=(None, None, None)) -> None:
+        """nmx_q4k_matmul_embed_norm on contiguous rows: Y [n][rows] = W x A8 of
+        [rmsnorm(embed(tok), w_emb) | rmsnorm(h, w_hid)]."""
+        self.check(self.lib.nmx_q4k_matmul_embed_norm(self.ctx, _p(W), rows, _p(Y), rows, n, H,
+                                                      _p(E), vocab, _p(tok), _p(w_emb), _p(h),
+                                                      H, _p(w_hid), eps,
+                                                      A8(*[_p(t) for t in a8_tmp])),
+                   "q4k_matmul_embed_norm")
 
     def silu_mul(self, gate, up, n: int, cols: int, y=None, a8=(None, None, None)) -> None:
         self.check(self.lib.nmx_silu_mul(self.ctx, _p(gate), _p(up), cols, n, cols, _p(y),

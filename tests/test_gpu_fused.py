@@ -190,6 +190,41 @@ def test_embed_norm(dev, cols, n):
             assert_bits_equal(got.numpy(), ref, f"{what} A8 {part}")
 
 
+@pytest.mark.parametrize("H,n", [(1024, 1), (1024, 5), (1024, 8), (256, 3), (512, 13)])
+def test_matmul_embed_norm(dev, H, n):
+    """nmx_q4k_matmul_embed_norm (the MTP head's fc projection with its embedding and both input
+    norms inside the matmul's workgroups; 13 rows take the two-call path) against
+    nmx_embed_norm + nmx_q4k_matmul bit for bit, and against the oracle: the Q4K product of the
+    A8 of [restated norm of the oracle's embedding rows | restated norm of h]."""
+    print(f"[case] matmul_embed_norm H={H} n={n}", flush=True)
+    rng = np.random.default_rng(7 * H + n)
+    vocab, rows = 512, H
+    E = oracle.q4k_quantize((rng.standard_normal((vocab, H)) * 0.02).astype(np.float32))
+    W = gaussian_q4k(rng, rows, 2 * H)
+    tok = rng.integers(0, vocab, n).astype(np.int32)
+    h = rng.standard_normal((n, H)).astype(np.float32)
+    w_emb, w_hid = (rng.uniform(0.5, 1.5, H).astype(np.float32) for _ in range(2))
+    dE, dW, dtok, dh = dev.to_device(E), dev.to_device(W), dev.to_device(tok), dev.to_device(h)
+    dwe, dwh = dev.to_device(w_emb), dev.to_device(w_hid)
+    # separate: both halves' A8 into one 2H-column buffer, then the matmul
+    a8 = a8_bufs(dev, n, 2 * H)
+    hb = H // 32   # the h half's blocks start at block hb of [block][n][32]
+    a1 = (a8[0].offset(hb * n * 32), a8[1].offset(hb * n * 4), a8[2].offset(hb * n * 4))
+    dev.embed_norm(dE, vocab, dtok, n, H, EPS, dwe, a0=a8, x1=dh, w1=dwh, a1=a1)
+    Yref = dev.zeros((n, rows), np.float32)
+    dev.q4k_matmul(dW, rows, 2 * H, n, *a8, Yref)
+    Y = dev.zeros((n, rows), np.float32)
+    dev.q4k_matmul_embed_norm(dW, rows, Y, n, H, dE, vocab, dtok, dwe, dh, dwh, EPS,
+                              a8_tmp=a8_bufs(dev, n, 2 * H))
+    dev.sync()
+    assert_bits_equal(Y.numpy(), Yref.numpy(), "fused against separate")
+    emb = np.stack([oracle.q4k_get_row(E, vocab, H, int(t)) for t in tok])
+    act = np.concatenate([rmsnorm_restated(emb, w_emb, EPS), rmsnorm_restated(h, w_hid, EPS)],
+                         axis=1)
+    q, d, fs = oracle.quant_a8(act)
+    assert_bits_equal(Y.numpy(), oracle.q4k_matmul(W, rows, 2 * H, q, d, fs, n), "oracle")
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("sel,want_y", [((0, 0), True), ((4, -1), True), ((2, 2), True),
                                          ((9, -1), True), ((3, -1), False)])
