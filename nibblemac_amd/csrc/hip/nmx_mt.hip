@@ -641,12 +641,13 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
     for (int R = swiglu ? 64 : 8; R >= 4; R >>= 1) {
         if (swiglu && R != 64) break;
         if (!swiglu && !norm) *bpu = R * 8 * nsb <= MT_REC_THREADS ? 1 : 4;
+        if (swiglu) *bpu = R * 4 * nsb <= MT_REC_THREADS ? 2 : 4;
         const int units = R * (8 / *bpu) * nsb;
         const int t = 64 * (((units > R * nv ? units : R * nv) + 63) / 64);
-        if (t > (norm ? MT_NORM_THREADS : swiglu ? MT_MAX_THREADS : *bpu == 1 ? MT_REC_THREADS : MT_REC4_THREADS))
+        if (t > (*bpu < 4 ? MT_REC_THREADS : norm ? MT_NORM_THREADS : swiglu ? MT_MAX_THREADS : MT_REC4_THREADS))
             continue;
         if (mt_layout(cols, nv, R, norm, swiglu).total > MT_LDS) continue;
-        if (norm && cols > t * MT_NORM_CPT) continue;
+        if (norm && cols > t * (*bpu < 4 ? 2 : MT_NORM_CPT)) continue;
         *threads = t;
         return R;
     }
@@ -688,10 +689,12 @@ int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v
               bool swiglu, nmx_a8 out, const nmx_mt_pair *pair) {
     const nmx_norm_in none{};
     if (pair) return launch_one<NV, true, false, 1, true>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out, pair);
+    if (nm && swiglu && bpu == 2) return launch_one<NV, true, true, 2>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm && swiglu) return launch_one<NV, true, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm && bpu == 1) return launch_one<NV, true, false, 1>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm && bpu == 2) return launch_one<NV, true, false, 2>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
     if (nm) return launch_one<NV, true, false, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, *nm, out);
+    if (swiglu && bpu == 2) return launch_one<NV, false, true, 2>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
     if (swiglu) return launch_one<NV, false, true, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
     if (bpu == 1) return launch_one<NV, false, false, 1>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
     return launch_one<NV, false, false, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
