@@ -612,14 +612,19 @@ __device__ __forceinline__ float qk_row_amax(float x, float *amx, int slot) {
 }
 
 template <int CP, int KVT>
-__global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc) {
+__global__ __launch_bounds__(256) void attn_qk_k(const float *__restrict__ q_in,
+                                                 const int32_t *__restrict__ posp,
+                                                 const float *__restrict__ k_in,
+                                                 const float *__restrict__ v_in, void *kc,
+                                                 int nh, int nkv, int pos_off, int max_ctx,
+                                                 Attn a, float *__restrict__ sc) {
     constexpr int HD = QK_HD, LP = 64 / CP, CPL = 16 / LP, RS = HD + 4, F4 = HD / 4;
     extern __shared__ float4 smem4[];
     __shared__ float part[(4 + CP) * 4]; /* partial sums of squares, 4 per row */
     __shared__ float rn[4 + CP];         /* 1 / rms of each row */
     __shared__ float amx[(CP + 1) * 4];  /* int8 cache: per (row, wave) max |x| */
     const int i = threadIdx.x, lane = i & 63, w = i >> 6;
-    const int rep = a.nh / a.nkv, h2 = a.rot / 2;
+    const int rep = nh / nkv, h2 = a.rot / 2;
     const int t = blockIdx.y, g = blockIdx.z, p0 = blockIdx.x * CP;
     float *ks = (float *)smem4; /* [CP][RS] key rows of the chunk, as the cache gives them */
     float *qs = ks + CP * RS;   /* [4][HD] rotated queries */
@@ -629,20 +634,20 @@ __global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc)
     float qv[4];
 #pragma unroll
     for (int hh = 0; hh < 4; hh++)
-        qv[hh] = hh < rep ? a.q[((size_t)t * a.nh + g * rep + hh) * 2 * HD + i] : 0.0f;
-    const int pos0 = *a.pos + a.pos_off; /* position of token 0 */
+        qv[hh] = hh < rep ? q_in[((size_t)t * nh + g * rep + hh) * 2 * HD + i] : 0.0f;
+    const int pos0 = *posp + pos_off; /* position of token 0 */
     const int np = pos0 + t + 1;
     if (p0 >= np) return;
     const int rows = np - p0 < CP ? np - p0 : CP;
     const int nold = pos0 - p0 <= 0 ? 0 : pos0 - p0 < rows ? pos0 - p0 : rows;
     const int nnew = rows - nold;
     const bool own = np - p0 <= CP; /* token t's own position is row rows - 1 of the chunk */
-    const size_t R0 = (size_t)g * a.max_ctx + p0;
-    const float *ksc = kv_scales<KVT>(a.kc, a);
+    const size_t R0 = (size_t)g * max_ctx + p0;
+    const float *ksc = kv_scales<KVT>(kc, a);
     /* new keys and, for the own row, the values: raw inputs */
     for (int r = nold; r < rows; r++)
-        kw[r * HD + i] = a.k_in[(size_t)(p0 + r - pos0) * a.nkv * HD + g * HD + i];
-    const float vv = own ? a.v_in[(size_t)t * a.nkv * HD + g * HD + i] : 0.0f;
+        kw[r * HD + i] = k_in[(size_t)(p0 + r - pos0) * nkv * HD + g * HD + i];
+    const float vv = own ? v_in[(size_t)t * nkv * HD + g * HD + i] : 0.0f;
     /* the old rows from the cache */
     for (int f0 = 0; f0 < nold * F4; f0 += 4 * 256) {
         float4 b[4];
@@ -650,7 +655,7 @@ __global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc)
         for (int u = 0; u < 4; u++) {
             const int f = f0 + u * 256 + i;
             b[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (f < nold * F4) b[u] = kv_load4<KVT>(a.kc, R0 + f / F4, HD, 4 * (f % F4), ksc);
+            if (f < nold * F4) b[u] = kv_load4<KVT>(kc, R0 + f / F4, HD, 4 * (f % F4), ksc);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -711,16 +716,16 @@ __global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc)
         if (own) (void)qk_row_amax(vv, amx, CP);
         __syncthreads();
     }
-    const size_t Rown = (size_t)g * a.max_ctx + (np - 1);
+    const size_t Rown = (size_t)g * max_ctx + (np - 1);
     for (int r = nold; r < rows; r++) {
         const float x = ks[r * RS + i];
         const bool st = own && r == rows - 1;
         if constexpr (KVT == KV_F32) {
-            if (st) ((float *)a.kc)[Rown * HD + i] = x;
+            if (st) ((float *)kc)[Rown * HD + i] = x;
         } else if constexpr (KVT == KV_F16) {
             const uint32_t b = kv_half_bits(x);
             ks[r * RS + i] = kv_half_value(b);
-            if (st) ((unsigned short *)a.kc)[Rown * HD + i] = (unsigned short)b;
+            if (st) ((unsigned short *)kc)[Rown * HD + i] = (unsigned short)b;
         } else {
             float amax = 0.0f; /* kv_store's order */
 #pragma unroll
@@ -730,8 +735,8 @@ __global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc)
             const float scl = amax / 127.0f;
             ks[r * RS + i] = (float)(int8_t)q * scl;
             if (st) {
-                ((int8_t *)a.kc)[Rown * HD + i] = (int8_t)q;
-                if (i == 0) ((float *)((int8_t *)a.kc + (size_t)a.nkv * a.max_ctx * HD))[Rown] = scl;
+                ((int8_t *)kc)[Rown * HD + i] = (int8_t)q;
+                if (i == 0) ((float *)((int8_t *)kc + (size_t)nkv * max_ctx * HD))[Rown] = scl;
             }
         }
     }
@@ -746,7 +751,7 @@ __global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc)
             for (int ww = 0; ww < HD / 64; ww++) amax = fmaxf(amax, amx[4 * CP + ww]);
             const float inv = amax > 127.0f / 3.40282347e+38f ? 127.0f / amax : 0.0f;
             ((int8_t *)a.vc)[Rown * HD + i] = (int8_t)kv_i8_code(vv, inv);
-            if (i == 0) ((float *)((int8_t *)a.vc + (size_t)a.nkv * a.max_ctx * HD))[Rown] = amax / 127.0f;
+            if (i == 0) ((float *)((int8_t *)a.vc + (size_t)nkv * max_ctx * HD))[Rown] = amax / 127.0f;
         }
     }
     __syncthreads(); /* ks and qs complete */
@@ -779,7 +784,7 @@ __global__ __launch_bounds__(256) void attn_qk_k(Attn a, float *__restrict__ sc)
     }
     const float s = x + __shfl_xor(x, 32);
     if (lp == 0 && live)
-        sc[((size_t)t * a.nh + g * rep + w) * a.max_ctx + p0 + pl] = (s + 0.0f) * a.scale;
+        sc[((size_t)t * nh + g * rep + w) * max_ctx + p0 + pl] = (s + 0.0f) * a.scale;
 }
 
 /* Softmax and P.V (forward_attn.c:171-181, forward_ops.c:294-382, :360-382): max (exact in
@@ -867,20 +872,23 @@ __device__ __forceinline__ float pv_chain(float acc, const float *p, int stride,
 }
 
 template <int KVT>
-__global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict__ sc) {
+__global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
+                                                 const int32_t *__restrict__ posp,
+                                                 const void *vc, int pos_off, int max_ctx,
+                                                 int nh, int nkv, int hd_, Attn a) {
     extern __shared__ float4 smem4[];
     __shared__ float red[8];
     constexpr int F4 = PV_DS / 4;
-    const int hd = a.hd, rep = a.nh / a.nkv, S = (hd / PV_DS) * a.nkv;
+    const int hd = hd_, rep = nh / nkv, S = (hd / PV_DS) * nkv;
     const int tid = threadIdx.x, sl = blockIdx.x % S, k = blockIdx.x / S;
     const int d0 = (sl % (hd / PV_DS)) * PV_DS, g = sl / (hd / PV_DS);
     const int h = g * rep + k % rep, t = k / rep;
-    const int np = *a.pos + a.pos_off + t + 1;
+    const int np = *posp + pos_off + t + 1;
     float *att = (float *)smem4;                    /* [max_ctx] */
-    float *vt = att + ((a.max_ctx + 3) & ~3);       /* [PV_PT][PV_DS] */
-    const float *srow = sc + ((size_t)t * a.nh + h) * a.max_ctx;
-    const size_t R0 = (size_t)g * a.max_ctx;
-    const float *vsc = kv_scales<KVT>(a.vc, a);
+    float *vt = att + ((max_ctx + 3) & ~3);       /* [PV_PT][PV_DS] */
+    const float *srow = sc + ((size_t)t * nh + h) * max_ctx;
+    const size_t R0 = (size_t)g * max_ctx;
+    const float *vsc = kv_scales<KVT>(vc, a);
     /* the scores row, then the first tile's values (element f = u 256 + tid: float4 f % F4 of
      * row f / F4) */
     float bs[4];
@@ -895,7 +903,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     for (int u = 0; u < PV_PER; u++) {
         const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
         vb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < rows0) vb[u] = kv_load4<KVT>(a.vc, R0 + r, hd, d0 + 4 * c4, vsc);
+        if (r < rows0) vb[u] = kv_load4<KVT>(vc, R0 + r, hd, d0 + 4 * c4, vsc);
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -951,7 +959,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
             for (int u = 0; u < PV_PER2; u++) {
                 const int f = u * 192 + f0, r = f / F4, c4 = f - r * F4;
                 nb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (r < rows2) nb[u] = kv_load4<KVT>(a.vc, R0 + next + r, hd, d0 + 4 * c4, vsc);
+                if (r < rows2) nb[u] = kv_load4<KVT>(vc, R0 + next + r, hd, d0 + 4 * c4, vsc);
             }
         }
         if (tid < PV_DS) o = pv_chain(o, vt + tid, PV_DS, rows);
@@ -974,10 +982,10 @@ __global__ __launch_bounds__(256) void attn_pv_k(Attn a, const float *__restrict
     }
     if (tid < PV_DS) {
         const int d = d0 + tid;
-        const float *qrow = a.q + ((size_t)t * a.nh + h) * 2 * hd;
+        const float *qrow = a.q + ((size_t)t * nh + h) * 2 * hd;
         o = o * nmx_sigmoid(qrow[hd + d]);
         const int col = h * hd + d;
-        a.o[(size_t)t * a.nh * hd + col] = o;
+        a.o[(size_t)t * nh * hd + col] = o;
         if (a.aq) a8_block(o, col >> 5, t, a.n, a.aq, a.ad, a.afs);
     }
 }
@@ -1424,7 +1432,8 @@ int launch_pv(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
         const size_t llds = ((size_t)PV_SEG + (size_t)PV_PT2 * PV_DS) * 4;
         attn_pv_long_k<KVT><<<pgrid, 256, llds, ctx->stream>>>(a, p->scores);
     } else {
-        attn_pv_k<KVT><<<pgrid, 256, plds, ctx->stream>>>(a, p->scores);
+        attn_pv_k<KVT><<<pgrid, 256, plds, ctx->stream>>>(p->scores, a.pos, a.vc, a.pos_off, a.max_ctx,
+                                                           a.nh, a.nkv, a.hd, a);
     }
     NMX_LAUNCHED(ctx, "attn_pv");
     return 0;
@@ -1449,7 +1458,8 @@ int launch_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
         ready = true;
     }
     dim3 grid((unsigned)((p->max_ctx + CP - 1) / CP), (unsigned)p->n, (unsigned)p->nkv);
-    attn_qk_k<CP, KVT><<<grid, 256, lds, ctx->stream>>>(a, p->scores);
+    attn_qk_k<CP, KVT><<<grid, 256, lds, ctx->stream>>>(a.q, a.pos, a.k_in, a.v_in, a.kc, a.nh, a.nkv,
+                                                        a.pos_off, a.max_ctx, a, p->scores);
     NMX_LAUNCHED(ctx, "attn_qk");
     return launch_pv<KVT>(ctx, p, a);
 }
