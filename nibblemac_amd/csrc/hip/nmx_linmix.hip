@@ -61,15 +61,18 @@ __host__ __device__ constexpr int mix_lds_floats(int n, int dk, int dv) {
 }
 
 template <int DK4>
-__global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
+__global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
+    const float *__restrict__ raw, const float *__restrict__ z_in, const float *__restrict__ a_in,
+    const float *__restrict__ b_in, int raw_stride, int z_stride, int g_stride, int kdim, int rep,
+    int dv_, int n_, LinMix a) {
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[8 * 64];
     __shared__ float spdec[MIX_TB]; /* decays of the pending batch (red serves the L2 norms) */
     constexpr int DK = DK4 * 4, PAD = DK4 + 4, ROW = 4 * PAD;
-    const int n = a.n, dv = a.dv, heads = a.heads;
-    const int h = blockIdx.x, tid = threadIdx.x, T = blockDim.x, c = tid & 3;
+    const int n = n_, dv = dv_, heads = a.heads;
+    const int h = blockIdx.x, tid = threadIdx.x, T = 4 * dv, c = tid & 3; /* the launch's size */
     const int j = tid >> 2; /* value column of the quad (T = 4 dv) */
-    const int kh = h / a.rep, kd = a.kd;
+    const int kh = h / rep, kd = kdim;
     const size_t logw = (size_t)DK + dv + 1;
     const bool logged = a.log != nullptr;
     float *sq = sm, *sk = sq + n * ROW, *sv = sk + n * ROW, *so = sv + n * dv;
@@ -110,25 +113,25 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
 #pragma unroll
     for (int u = 0; u < MIX_TB; u++) {
         cx[u] = 0.0f;
-        if (conv_on && u < n0) cx[u] = a.raw[(size_t)u * a.raw_stride + gc];
+        if (conv_on && u < n0) cx[u] = raw[(size_t)u * raw_stride + gc];
     }
     /* gate items of the last wave, which owns no channel (y = tid - (T - 64)): item y < n is the
      * decay of token y, item n <= y < 2 n the beta of token y - n */
     const int gy = tid - (T - 64);
     float ga = 0.0f, gA = 0.0f, gdt = 0.0f;
     if (gy >= 0 && gy < n) {
-        ga = a.a_in[(size_t)gy * a.g_stride + h];
+        ga = a_in[(size_t)gy * g_stride + h];
         gA = a.A ? a.A[h] : a.A_log[h];
         gdt = a.dt_bias[h];
     } else if (gy >= n && gy < 2 * n) {
-        ga = a.b_in[(size_t)(gy - n) * a.g_stride + h];
+        ga = b_in[(size_t)(gy - n) * g_stride + h];
     }
     /* z of the first tokens and the norm weight, as float4 (x4 = tid over [n0][dv / 4]) */
     const bool z_on = 4 * tid < n0 * dv, w_on = 4 * tid < dv;
     float4 zq = make_float4(0.f, 0.f, 0.f, 0.f), wq = zq;
     if (z_on) {
         const int t = (4 * tid) / dv, jj = 4 * tid - t * dv;
-        zq = *(const float4 *)(a.z + (size_t)t * a.z_stride + h * dv + jj);
+        zq = *(const float4 *)(z_in + (size_t)t * z_stride + h * dv + jj);
     }
     if (w_on) wq = *(const float4 *)(a.w + 4 * tid);
     /* recurrence state of the quad's keys */
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
             if (t0 > 0) {
 #pragma unroll
                 for (int u = 0; u < MIX_TB; u++)
-                    xt[u] = u < nb ? a.raw[(size_t)(t0 + u) * a.raw_stride + gc] : 0.0f;
+                    xt[u] = u < nb ? raw[(size_t)(t0 + u) * raw_stride + gc] : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < MIX_TB; u++) {
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
         for (int x = gy; x < 2 * n; x += 64) {
             const bool first = x == gy;
             if (x < n) {
-                const float av = first ? ga : a.a_in[(size_t)x * a.g_stride + h];
+                const float av = first ? ga : a_in[(size_t)x * g_stride + h];
                 const float Ai = first ? gA : a.A ? a.A[h] : a.A_log[h];
                 const float dt = first ? gdt : a.dt_bias[h];
                 const float A = a.A ? Ai : -nmx_gate_expf(Ai);
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
                 sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf(sp_));
                 sdec[x] = nmx_gate_expf(A * sp_);
             } else {
-                const float b = first ? ga : a.b_in[(size_t)(x - n) * a.g_stride + h];
+                const float b = first ? ga : b_in[(size_t)(x - n) * g_stride + h];
                 sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf(-b));
             }
         }
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(LinMix a) {
     for (int x = tid; x < n * dv; x += T) { /* a 32-lane half-wave holds one A8 block */
         const int t = x / dv, jj = x - t * dv;
         const float ov = so[t * dv + jj];
-        const float gz = nmx_silu(t < n0 ? sz[x] : a.z[(size_t)t * a.z_stride + h * dv + jj]);
+        const float gz = nmx_silu(t < n0 ? sz[x] : z_in[(size_t)t * z_stride + h * dv + jj]);
         float yv = (ov * srn[2 * n + t]) * sw[jj];
         yv = yv * gz;
         const int col = h * dv + jj;
@@ -370,7 +373,8 @@ int launch_mix(nmx_ctx *ctx, const LinMix &m, size_t lds) {
                                          hipFuncAttributeMaxDynamicSharedMemorySize, MIX_LDS));
         ready = true;
     }
-    lin_mix_k<DK4><<<dim3((unsigned)m.heads), dim3((unsigned)(4 * m.dv)), lds, ctx->stream>>>(m);
+    lin_mix_k<DK4><<<dim3((unsigned)m.heads), dim3((unsigned)(4 * m.dv)), lds, ctx->stream>>>(
+        m.raw, m.z, m.a_in, m.b_in, m.raw_stride, m.z_stride, m.g_stride, m.kd, m.rep, m.dv, m.n, m);
     NMX_LAUNCHED(ctx, "lin_mix");
     return 0;
 }
