@@ -358,40 +358,33 @@ struct FinishCommit {
  * nmx_rmsnorm_row) into y (written by workgroup 0) and into a one-vector A8 in LDS; then the
  * dots of q4k_mv_k<1, false, true> with the activations read from LDS. The row's loads are
  * requested before the first superblock's weights, so the norm runs while the weights are in
- * flight. cols <= 1024. */
-struct HeadRow {
-    const float *x;
-    int x_stride;
-    const float *add;
-    int add_stride;
-    const float *w;
-    float eps;
-    const int32_t *idx;
-    int off, nrows;
-    float *y;
-};
-
+ * flight. cols <= 1024; W has rows rows. The leading 16 SGPRs of arguments are what the first
+ * requests need (preloaded with the wave). */
 constexpr int MVR_MAX_COLS = 1024;
 
-__global__ __launch_bounds__(256) void q4k_mvr_k(SegTable tab, int cols, HeadRow hr,
+__global__ __launch_bounds__(256) void q4k_mvr_k(const int32_t *__restrict__ idx,
+                                                 const float *__restrict__ x,
+                                                 const float *__restrict__ add,
+                                                 const float *__restrict__ w,
+                                                 const uint8_t *__restrict__ W, int off, int nrows,
+                                                 int x_stride, int add_stride, int cols, int rows,
+                                                 float eps, float *__restrict__ y,
                                                  unsigned long long *__restrict__ amax_key) {
     __shared__ __align__(16) int8_t s_q[MVR_MAX_COLS];
     __shared__ float s_d[MVR_MAX_COLS / 32], s_fs[MVR_MAX_COLS / 32];
     __shared__ __align__(16) float s_sq[4 * cm_stride(MVR_MAX_COLS) + 4];
     __shared__ float s_red[8];
     /* the norm's row first */
-    const int ri = *hr.idx + hr.off;
-    const size_t r = (size_t)(ri < 0 ? 0 : ri >= hr.nrows ? hr.nrows - 1 : ri);
+    const int ri = *idx + off;
+    const size_t r = (size_t)(ri < 0 ? 0 : ri >= nrows ? nrows - 1 : ri);
     float4 xv[1], av[1], wv[1];
-    rms4_load<1>(hr.x + r * hr.x_stride, hr.add ? hr.add + r * hr.add_stride : nullptr, hr.w, cols,
-                 xv, av, wv);
+    rms4_load<1>(x + r * x_stride, add ? add + r * add_stride : nullptr, w, cols, xv, av, wv);
 
+    const int total_waves = (rows + 63) / 64;
     const int wave_raw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const bool wave_live = wave_raw < tab.total_waves;
-    const int wave = wave_live ? wave_raw : tab.total_waves - 1;
+    const bool wave_live = wave_raw < total_waves;
+    const int wave = wave_live ? wave_raw : total_waves - 1;
     const int lane = threadIdx.x & 63;
-    const uint8_t *W = tab.s[0].W;
-    const int rows = tab.s[0].rows;
     const int row_raw = wave * 64 + lane;
     const bool valid = wave_live && row_raw < rows;
     const int row = row_raw < rows ? row_raw : rows - 1;
@@ -402,8 +395,8 @@ __global__ __launch_bounds__(256) void q4k_mvr_k(SegTable tab, int cols, HeadRow
 #pragma unroll
     for (int k = 0; k < 8; k++) c[k] = tp[4 + 4 * k + i];
 
-    rms4_finish<1>(xv, av, wv, hr.add != nullptr, nullptr, cols, hr.eps,
-                   blockIdx.x == 0 ? hr.y : nullptr, s_q, s_d, s_fs, 1, 0, s_sq, s_red);
+    rms4_finish<1>(xv, av, wv, add != nullptr, nullptr, cols, eps, blockIdx.x == 0 ? y : nullptr,
+                   s_q, s_d, s_fs, 1, 0, s_sq, s_red);
     __syncthreads(); /* the A8 row is in LDS */
 
     float acc = 0.0f;
@@ -1151,14 +1144,10 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
             return -1;
         return advance ? nmx_ctl_advance(ctx, advance) : 0;
     }
-    SegTable tab = {};
-    tab.count = 1;
-    tab.s[0] = Seg{(const uint8_t *)W, nullptr, rows, rows, 0, 0};
-    tab.total_waves = (rows + 63) / 64;
-    const int blocks = (tab.total_waves + 3) / 4;
+    const int blocks = ((rows + 63) / 64 + 3) / 4;
     unsigned long long *keys = (unsigned long long *)work;
-    q4k_mvr_k<<<blocks, 256, 0, ctx->stream>>>(
-        tab, cols, HeadRow{x, x_stride, add, add_stride, w, eps, idx, off, nrows, y}, keys);
+    q4k_mvr_k<<<blocks, 256, 0, ctx->stream>>>(idx, x, add, w, (const uint8_t *)W, off, nrows,
+                                                x_stride, add_stride, cols, rows, eps, y, keys);
     NMX_LAUNCHED(ctx, "q4k_mvr");
     head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, 1, nullptr, out, tok_dst,
                                                 FinishCommit{nullptr, nullptr, nullptr, 0, advance});
