@@ -212,6 +212,17 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
                            void *work, int32_t *out, int32_t *tok_dst, nmx_a8 a8_tmp,
                            int32_t *advance);
 
+/* The first kernel of nmx_head_row_accept_to alone, for its fused shapes (cols a multiple of
+ * 256 up to 1024, 16-byte aligned rows): the normed row to y (may be NULL) and the argmax over
+ * the rows of W left as nmx_head_row_nkeys(rows) partial keys in keys (8-byte aligned), for a
+ * consumer that resolves the token itself (nmx_q4k_matmul_embed_norm, nmx_embed_norm_keys):
+ * one launch fewer than a head with its own reduction. No reference counterpart of its own:
+ * the reference's draft head (engine/src/mtp.c:88-100) split at the argmax. */
+int nmx_head_row_keys(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
+                      int x_stride, const float *add, int add_stride, const float *w, float eps,
+                      const int32_t *idx, int off, int nrows, float *y, void *keys);
+int nmx_head_row_nkeys(int rows);
+
 int nmx_rmsnorm_pair(nmx_ctx *ctx, int n, int cols, float eps, const float *x0, int x0_stride,
                      const float *w0, float *y0, int y0_stride, nmx_a8 a0, const float *x1,
                      int x1_stride, const float *w1, float *y1, int y1_stride, nmx_a8 a1);
@@ -224,6 +235,14 @@ int nmx_embed_norm(nmx_ctx *ctx, const void *E, int vocab, const int32_t *tok, i
                    float eps, const float *w0, float *xo0, int xo0_stride, float *y0, int y0_stride,
                    nmx_a8 a0, const float *x1, int x1_stride, const float *w1, float *y1,
                    int y1_stride, nmx_a8 a1);
+
+/* nmx_embed_norm with one set (no second norm, no y0) whose row n - 1 takes its token from the
+ * nkeys partial argmax keys of nmx_head_row_keys (written to tok[n - 1]) instead of reading it:
+ * the verify pass's first norm on a draft that no separate reduction resolved. cols a multiple
+ * of 256 up to 1024, 16-byte aligned rows. */
+int nmx_embed_norm_keys(nmx_ctx *ctx, const void *E, int vocab, int32_t *tok, int n, int cols,
+                        float eps, const float *w, float *xo, int xo_stride, nmx_a8 a8,
+                        const void *keys, int nkeys);
 
 /* Gated DeltaNet pre (engine/src/forward_lin.c:36-67): causal conv + SiLU per channel with the
  * conv state, q/k L2 norm (+ q scale), beta = sigmoid(b), decay = exp(A softplus(a + dt_bias)).
@@ -298,11 +317,13 @@ int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int
  * buffer) followed by nmx_q4k_matmul. The embedding and both norms run inside the matmul's
  * workgroups (one launch) when n <= 8, H is a multiple of 256, h, w_emb and w_hid are 16-byte
  * aligned and the shape fits; otherwise a8_tmp (n x 2 H A8, the two calls; H <= 1024) is
- * used. */
+ * used. tok_keys (may be NULL; one row, the fused shape): the token is the argmax of the nkeys
+ * partial keys of nmx_head_row_keys, written to tok[0] (the draft lands in the token row). */
 int nmx_q4k_matmul_embed_norm(nmx_ctx *ctx, const void *W, int rows, float *Y, int y_stride,
-                              int n, int H, const void *E, int vocab, const int32_t *tok,
+                              int n, int H, const void *E, int vocab, int32_t *tok,
                               const float *w_emb, const float *h, int h_stride,
-                              const float *w_hid, float eps, nmx_a8 a8_tmp);
+                              const float *w_hid, float eps, nmx_a8 a8_tmp,
+                              const void *tok_keys, int nkeys);
 
 /* The SwiGLU MLP input (engine/src/forward.c:49-58, forward_ops.c:98-110): h = silu(Wg a) *
  * (Wu a) for a = the A8 input (q, d, fsum) or, when in is not NULL, the A8 of rmsnorm(in);

@@ -180,6 +180,9 @@ struct RmsSet {
     const int32_t *tok;
     float *xo;            /* optional: the rows (as read or decoded) written here */
     int xo_stride;
+    const unsigned long long *keys; /* optional, with E: row n - 1's token is the argmax of */
+    int nkeys;                      /* these partial keys, written to tok_w[n - 1] */
+    int32_t *tok_w;
 };
 
 template <int P4>
@@ -188,8 +191,19 @@ __global__ __launch_bounds__(256) void rmsnorm4_pair_k(RmsSet s0, RmsSet s1, int
     extern __shared__ float sq[];
     __shared__ float red[8];
     const RmsSet &s = blockIdx.y ? s1 : s0;
+    const int row = blockIdx.x;
+    if (s.keys && row == n - 1) { /* uniform: the token from the keys, by every wave */
+        const int tk = nmx_keys_token(s.keys, s.nkeys);
+        if (threadIdx.x == 0) s.tok_w[row] = tk;
+        float4 v[P4], a[P4], wv[P4];
+        rms4_load<P4>(nullptr, nullptr, s.w, cols, v, a, wv, s.E, tk);
+        rms4_finish<P4>(v, a, wv, false, s.xo ? s.xo + (size_t)row * s.xo_stride : nullptr, cols,
+                        eps, s.y ? s.y + (size_t)row * s.y_stride : nullptr, s.q, s.d, s.fs, n,
+                        row, sq, red);
+        return;
+    }
     rms4_row<P4>(s.x, s.x_stride, nullptr, 0, s.xo, s.xo_stride, s.w, cols, eps, s.y, s.y_stride,
-                 s.q, s.d, s.fs, n, blockIdx.x, sq, red, s.E, s.tok);
+                 s.q, s.d, s.fs, n, row, sq, red, s.E, s.tok);
 }
 
 /* ---- Gated DeltaNet pre (engine/src/forward_lin.c:36-67): per channel the causal conv over
@@ -1324,6 +1338,24 @@ int nmx_embed_norm(nmx_ctx *ctx, const void *E, int vocab, const int32_t *tok, i
     const RmsSet s1{x1, x1_stride, w1, y1, y1_stride, a1.q, a1.d, a1.fs, nullptr, nullptr, nullptr, 0};
     const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
     rmsnorm4_pair_k<1><<<dim3((unsigned)n, x1 ? 2 : 1), 256, lds, ctx->stream>>>(s0, s1, cols, eps, n);
+    NMX_LAUNCHED(ctx, "embed_norm");
+    return 0;
+}
+
+int nmx_embed_norm_keys(nmx_ctx *ctx, const void *E, int vocab, int32_t *tok, int n, int cols,
+                        float eps, const float *w, float *xo, int xo_stride, nmx_a8 a8,
+                        const void *keys, int nkeys) {
+    if (!ctx) return -1;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (!E || !tok || !w || !keys || nkeys < 1 || (uintptr_t)keys % 8 || vocab <= 0 ||
+        vocab % 4 || cols % 256 || cols < 256 || cols > 1024 || n < 1 || n > 4096 || !al16(w) ||
+        (xo && (xo_stride < cols || !al16(xo) || xo_stride % 4)) || (a8.q && (!a8.d || !a8.fs)))
+        return nmx_fail(ctx, "nmx_embed_norm_keys: bad arguments");
+    const RmsSet s0{nullptr, 0, w, nullptr, 0, a8.q, a8.d, a8.fs, (const uint8_t *)E, tok, xo,
+                    xo_stride, (const unsigned long long *)keys, nkeys, tok};
+    const RmsSet s1{};
+    const size_t lds = ((size_t)4 * cm_stride(cols) + 4) * 4;
+    rmsnorm4_pair_k<1><<<dim3((unsigned)n, 1), 256, lds, ctx->stream>>>(s0, s1, cols, eps, n);
     NMX_LAUNCHED(ctx, "embed_norm");
     return 0;
 }

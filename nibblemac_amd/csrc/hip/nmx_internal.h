@@ -59,10 +59,12 @@ struct nmx_mt_seg {
  * norm->w; eps is norm->eps. */
 struct nmx_mt_pair {
     const uint8_t *E;
-    const int32_t *tok;
+    int32_t *tok;
     const float *w_emb;
     const float *h;
     int h_stride;
+    const unsigned long long *keys; /* optional (one row): the token from nkeys argmax keys */
+    int nkeys;
 };
 
 /* Small-row Q4K matmul with every vector of a pass in one workgroup (nmx_mt.hip), optionally

@@ -77,6 +77,24 @@ __device__ __forceinline__ unsigned long long nmx_max_u64_wave(unsigned long lon
     return ((unsigned long long)hi0 << 32) | lo0;
 }
 
+/* The row of the greatest of nk argmax keys (order-preserving value bits over the complemented
+ * row index, so the greatest key is the first maximum): what head_finish_k resolves for one
+ * vector. Every lane of the calling wave gets it; the first 256 keys are requested together. */
+__device__ __forceinline__ int nmx_keys_token(const unsigned long long *keys, int nk) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long k[4], m = 0ull;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = lane + 64 * u;
+        k[u] = keys[i < nk ? i : nk - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) m = k[u] > m ? k[u] : m;
+    for (int i = lane + 256; i < nk; i += 64) m = keys[i] > m ? keys[i] : m;
+    m = nmx_max_u64_wave(m);
+    return (int)(0xffffffffu - (uint32_t)(m & 0xffffffffull));
+}
+
 template <int DK4>
 __device__ __forceinline__ float nmx_quad_chain(const float (&p)[DK4]) {
     float carry = 0.0f;

@@ -44,10 +44,13 @@ struct MtTab {
 };
 
 /* The PAIR prologue's embedding half: the Q4K embedding E and its norm weight (the other half's
- * weight and eps come in nmx_norm_in). */
+ * weight and eps come in nmx_norm_in); keys (one row): its token is the argmax of the nkeys
+ * partial keys instead of tok[v0], and workgroup 0 writes it to tok[v0]. */
 struct MtPair {
     const uint8_t *E;
     const float *w0;
+    const unsigned long long *keys;
+    int nkeys;
 };
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
@@ -213,7 +216,14 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     int etok = 0;
     float4 h4[PAIR ? NV : 1];
     if constexpr (PAIR) {
-        etok = ((const int32_t *)in1)[v0 + (ev < NV ? ev : NV - 1)];
+        if (pr.keys) { /* one row: every wave with a decoding thread, all its lanes */
+            if ((tid & ~63) < NV * nbh) {
+                etok = nmx_keys_token(pr.keys, pr.nkeys);
+                if (blockIdx.x == 0 && tid == 0) ((int32_t *)in1)[v0] = etok;
+            }
+        } else {
+            etok = ((const int32_t *)in1)[v0 + (ev < NV ? ev : NV - 1)];
+        }
 #pragma unroll
         for (int v = 0; v < NV; v++) h4[v] = ((const float4 *)(nx + (size_t)(v0 + v) * xs))[mi];
     }
@@ -669,12 +679,12 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
     const void *in1 = NORM ? (const void *)nm.add : (const void *)d;
     uint64_t aux = NORM ? ((uint64_t)(uint32_t)nm.add_stride << 32) | (uint32_t)nm.x_stride
                         : (uint64_t)(uintptr_t)fs;
-    MtPair pr{nullptr, nullptr};
+    MtPair pr{nullptr, nullptr, nullptr, 0};
     if (PAIR) {
         in0 = pair->h;
         in1 = pair->tok;
         aux = (uint32_t)pair->h_stride;
-        pr = MtPair{pair->E, pair->w_emb};
+        pr = MtPair{pair->E, pair->w_emb, pair->keys, pair->nkeys};
     }
     q4k_mt_k<NV, NORM, SWI, BPU, PAIR><<<dim3((unsigned)groups), dim3((unsigned)T), lds, ctx->stream>>>(
         in0, in1, aux, (const uint8_t *)tab.s[0].W, cols, n, v0, R, T, tab.s[0].rows, tab, nm,
@@ -710,7 +720,7 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
     if (count < 1 || count > NMX_MAX_SEGS || cols % 256 || n < 1 || n > MT_MAX_NV) return 1;
     if (swiglu && (count != 2 || segs[0].rows != segs[1].rows || segs[0].rows % 32)) return 1;
     if (pair && (!norm || swiglu || cols % 512 || (uintptr_t)pair->w_emb & 15 ||
-                 (uintptr_t)pair->h & 15 || pair->h_stride % 4))
+                 (uintptr_t)pair->h & 15 || pair->h_stride % 4 || (pair->keys && n != 1)))
         return 1;
     /* equal-size passes of at most MT_MAX_NV vectors, larger first: every pass performs the
      * same per-vector operations, so the split does not change any result */
@@ -802,20 +812,23 @@ int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int
 }
 
 int nmx_q4k_matmul_embed_norm(nmx_ctx *ctx, const void *W, int rows, float *Y, int y_stride,
-                              int n, int H, const void *E, int vocab, const int32_t *tok,
+                              int n, int H, const void *E, int vocab, int32_t *tok,
                               const float *w_emb, const float *h, int h_stride,
-                              const float *w_hid, float eps, nmx_a8 a8_tmp) {
+                              const float *w_hid, float eps, nmx_a8 a8_tmp,
+                              const void *tok_keys, int nkeys) {
     if (!ctx) return -1;
     if (!W || !Y || !E || !tok || !w_emb || !h || !w_hid || rows <= 0 || rows % 4 ||
         y_stride < rows || H < 256 || H % 256 || H > 32768 || vocab <= 0 || vocab % 4 ||
-        n < 1 || n > 4096 || h_stride < H)
+        n < 1 || n > 4096 || h_stride < H ||
+        (tok_keys && (n != 1 || nkeys < 1 || (uintptr_t)tok_keys % 8)))
         return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: bad arguments");
     if (nmx_overlap(Y, ((size_t)(n - 1) * y_stride + rows) * 4, h,
                     ((size_t)(n - 1) * h_stride + H) * 4))
         return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: Y aliases h");
     if (n <= MT_MAX_NV && rows < 32768) {
         const nmx_norm_in nm{nullptr, 0, nullptr, 0, nullptr, 0, w_hid, eps};
-        const nmx_mt_pair pr{(const uint8_t *)E, tok, w_emb, h, h_stride};
+        const nmx_mt_pair pr{(const uint8_t *)E, tok, w_emb, h, h_stride,
+                             (const unsigned long long *)tok_keys, nkeys};
         const nmx_mt_seg seg{(const uint8_t *)W, Y, rows, y_stride};
         const int rc = nmx_mt_matmul(ctx, 1, &seg, 2 * H, n, nullptr, nullptr, nullptr, &nm, false,
                                      nmx_a8{}, &pr);
@@ -823,6 +836,7 @@ int nmx_q4k_matmul_embed_norm(nmx_ctx *ctx, const void *W, int rows, float *Y, i
     }
     /* the two calls: both halves' A8 blocks into a8_tmp ([block][n][32], the embedding's
      * blocks first), then the matmul */
+    if (tok_keys) return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: keys need the fused shape");
     if (!a8_tmp.q || !a8_tmp.d || !a8_tmp.fs)
         return nmx_fail(ctx, "nmx_q4k_matmul_embed_norm: shape needs the a8_tmp buffers");
     const size_t hb = (size_t)(H / 32) * n;

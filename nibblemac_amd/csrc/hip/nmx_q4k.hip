@@ -1155,6 +1155,27 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
     return 0;
 }
 
+int nmx_head_row_nkeys(int rows) { return rows > 0 ? ((rows + 63) / 64 + 3) / 4 : 0; }
+
+int nmx_head_row_keys(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
+                      int x_stride, const float *add, int add_stride, const float *w, float eps,
+                      const int32_t *idx, int off, int nrows, float *y, void *keys) {
+    if (!ctx) return -1;
+    auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (!W || !x || !w || !idx || !keys || nrows < 1 || x_stride < cols ||
+        (add && add_stride < cols))
+        return nmx_fail(ctx, "nmx_head_row_keys: bad arguments");
+    if (cols % 256 || cols > MVR_MAX_COLS || rows <= 0 || rows % 4 || rows > (1 << 22) || !al(x) ||
+        !al(w) || x_stride % 4 || (add && (!al(add) || add_stride % 4)) || (y && !al(y)) ||
+        (uintptr_t)keys % 8)
+        return nmx_fail(ctx, "nmx_head_row_keys: shape outside the fused kernel (cols %d)", cols);
+    q4k_mvr_k<<<nmx_head_row_nkeys(rows), 256, 0, ctx->stream>>>(
+        idx, x, add, w, (const uint8_t *)W, off, nrows, x_stride, add_stride, cols, rows, eps, y,
+        (unsigned long long *)keys);
+    NMX_LAUNCHED(ctx, "q4k_mvr");
+    return 0;
+}
+
 int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int n,
                            const int8_t *q, const float *d, const float *fsum,
                            const int32_t *drafts, void *work, int32_t *out, int32_t *vt,

@@ -232,7 +232,7 @@ static int eval_chunks(pinfer_ctx *c, const int32_t *tokens, int n, int want_log
         const int nb = n - t0 < E_MAX_BATCH ? n - t0 : E_MAX_BATCH;
         if (nmx_upload(c->dev, c->tok, tokens + t0, (size_t)nb * 4)) return PINFER_E_ARG;
         int rc = e_set_pos(c, c->n_past);
-        if (rc == PINFER_OK) rc = e_forward(c, c->tok, nb, 0);
+        if (rc == PINFER_OK) rc = e_forward(c, c->tok, nb, 0, 0);
         if (rc != PINFER_OK) return rc;
         c->keep = 0;
         if (t0 + nb == n && want_logits) {

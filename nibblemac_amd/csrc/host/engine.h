@@ -162,10 +162,17 @@ struct pinfer_ctx {
 };
 
 /* forward.c */
-int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged);
+int e_forward(pinfer_ctx *c, int32_t *tok_dev, int n, int logged, int keys_last);
 int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits);
-int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst, int advance);
+int e_mtp_forward(pinfer_ctx *c, const float *h_dev, int32_t *tok_dev, int n, int pos_off,
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst, int advance,
+                  int keys_io);
+/* e_keys_ok: the draft heads and their consumers can pass a draft as argmax keys in c->hwork
+ * (keys_io of e_mtp_forward: E_KEYS_IN = the one input token from the keys, written to
+ * tok_dev[0]; E_KEYS_OUT = the draft left as keys, draft_dst unused; keys_last of e_forward:
+ * row n - 1's token from the keys, written to tok_dev[n - 1]). */
+enum { E_KEYS_IN = 1, E_KEYS_OUT = 2 };
+int e_keys_ok(const pinfer_ctx *c);
 int e_set_pos(pinfer_ctx *c, int pos);
 
 /* spec.c */

@@ -141,17 +141,24 @@ static int lin_block(pinfer_ctx *c, const e_layer *L, int n, int logged, const n
     return PINFER_OK;
 }
 
+int e_keys_ok(const pinfer_ctx *c) { return c->H % 256 == 0 && c->H <= 1024; }
+
 /* n tokens (device ids) at positions ctl[0].. through the main model; leaves the final-normed
- * rows in s->xn and their A8 in s->a_h (the head's input). */
-int e_forward(pinfer_ctx *c, const int32_t *tok_dev, int n, int logged) {
+ * rows in s->xn and their A8 in s->a_h (the head's input). keys_last > 0: row n - 1's token is
+ * the argmax of that many partial keys in c->hwork (written to tok_dev[n - 1]). */
+int e_forward(pinfer_ctx *c, int32_t *tok_dev, int n, int logged, int keys_last) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H;
     e_resid r = {s->x, s->x2, NULL};
     /* the embedding rows (the residual stream) and the first layer's input norm, one launch */
     const nmx_a8 none = {NULL, NULL, NULL};
-    CK(nmx_embed_norm(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps, c->layers[0].in_norm,
-                      r.cur, H, NULL, 0, s->a_h, NULL, 0, NULL, NULL, 0, none));
+    if (keys_last > 0)
+        CK(nmx_embed_norm_keys(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps,
+                               c->layers[0].in_norm, r.cur, H, s->a_h, c->hwork, keys_last));
+    else
+        CK(nmx_embed_norm(D, c->embed.w, c->vocab, tok_dev, n, H, c->rms_eps, c->layers[0].in_norm,
+                          r.cur, H, NULL, 0, s->a_h, NULL, 0, NULL, NULL, 0, none));
     for (int l = 0; l < c->n_layers; l++) {
         const e_layer *L = &c->layers[l];
         /* layer 0's input norm ran with the embedding; the others run in the projections */
@@ -200,9 +207,12 @@ int e_head_last(pinfer_ctx *c, int n, int32_t *dst_dev, int want_logits) {
  * hiddens, tok_dev [n] the tokens that follow them, positions ctl[0] + pos_off + i. The
  * selected row (n - 1, or ctl[1] - 1 when head_row_dynamic) gives the draft (argmax over the
  * first nv head rows) to draft_dst and its MTP hidden to m_dst (each may be NULL). advance:
- * ctl[0] += ctl[1] at the end (folded into the draft head's last kernel where it can be). */
-int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int n, int pos_off,
-                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst, int advance) {
+ * ctl[0] += ctl[1] at the end (folded into the draft head's last kernel where it can be).
+ * keys_io (e_keys_ok shapes, one row): E_KEYS_IN, the token from the partial keys in c->hwork
+ * (written to tok_dev[0]); E_KEYS_OUT, the draft left there as keys (draft_dst unused). */
+int e_mtp_forward(pinfer_ctx *c, const float *h_dev, int32_t *tok_dev, int n, int pos_off,
+                  int head_row_dynamic, int nv, int32_t *draft_dst, float *m_dst, int advance,
+                  int keys_io) {
     nmx_ctx *D = c->dev;
     e_scratch *s = &c->s;
     const int H = c->H;
@@ -212,11 +222,14 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
      * never straddles the halves (H % 32 == 0). At most 8 rows, the embedding and both norms
      * run inside the fc matmul's workgroups; else one launch for them, then the matmul */
     e_resid r = {s->x, s->x2, NULL};
+    const int nkeys = nmx_head_row_nkeys(nv);
+    if (keys_io && (n != 1 || !e_keys_ok(c) || head_row_dynamic || advance)) return PINFER_E_ARG;
     if (n <= 8 && H % 256 == 0 && H <= 1024) {
         /* the embedding and both norms inside the fc matmul's workgroups */
         CK(nmx_q4k_matmul_embed_norm(D, c->mtp_fc.w, H, r.cur, H, n, H, c->embed.w, c->vocab,
                                      tok_dev, c->mtp_norm_emb, h_dev, H, c->mtp_norm_hid,
-                                     c->rms_eps, s->a_w));
+                                     c->rms_eps, s->a_w, (keys_io & E_KEYS_IN) ? c->hwork : NULL,
+                                     nkeys));
     } else {
         const size_t hb = (size_t)(H / 32) * n;
         const nmx_a8 a8_emb = s->a_w, a8_hid = {s->a_w.q + hb * 32, s->a_w.d + hb, s->a_w.fs + hb};
@@ -234,6 +247,11 @@ int e_mtp_forward(pinfer_ctx *c, const float *h_dev, const int32_t *tok_dev, int
     if ((rc = mlp_block(c, L, n, &r))) return rc;
     const int32_t *idx = head_row_dynamic ? c->ctl + 1 : c->ctl + 15;
     const int off = head_row_dynamic ? -1 : n - 1;
+    if (keys_io & E_KEYS_OUT) { /* the draft as partial argmax keys for its consumer */
+        CK(nmx_head_row_keys(D, c->head.w, nv, H, r.cur, H, r.add, H, c->mtp_norm_out,
+                             c->rms_eps, idx, off, n, m_dst ? m_dst : s->xn, c->hwork));
+        return PINFER_OK;
+    }
     if (draft_dst && H <= 1024 && H % 256 == 0) {
         /* the selected row's final norm (its MTP hidden to m_dst; a single row always to s->xn)
          * inside the draft head's workgroups */

@@ -61,8 +61,8 @@ static float *m_ping(pinfer_ctx *c, int i) { return c->mbuf + (size_t)(1 + (i & 
 /* The logged main pass over vt[0..ke] and the head with the acceptance of vt[1..ke]; the
  * result (a, bonus, vt) goes to the host mailbox, and ctl[1] = e = a + 1
  * (engine/src/spec.c:323-351). */
-static int seq_verify(pinfer_ctx *c, int ke) {
-    TRY(e_forward(c, c->vt, ke + 1, 1));
+static int seq_verify(pinfer_ctx *c, int ke, int keys_last) {
+    TRY(e_forward(c, c->vt, ke + 1, 1, keys_last));
     e_scratch *sc = &c->s;
     CK(nmx_head_accept_commit(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d,
                               sc->a_h.fs, c->vt + 1, c->hwork, c->hout, c->vt, c->ctl, c->mbox,
@@ -86,22 +86,25 @@ static int commit_lin_cur(pinfer_ctx *c, int redo) {
  * commit of e = ctl[1], the MTP head over the committed rows (its hidden of row e - 1 and the
  * next d1; the pass reads the verify's final-normed rows, s.xn, which at hidden <= 1024 it
  * never writes, and otherwise writes only after its last read), n_past += e (done by the
- * pass's last kernel). */
+ * pass's last kernel). The chain's drafts d2..dk pass as argmax keys: each one's consumer (the
+ * next MTP pass, then the verify's first norm) resolves it and writes it to vt. */
 static int seq_round(pinfer_ctx *c, int ke, int nv) {
+    const int keys = e_keys_ok(c);
     for (int s = 1; s < ke; s++) {
         const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
-        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), 0));
+        const int io = keys ? E_KEYS_OUT | (s > 1 ? E_KEYS_IN : 0) : 0;
+        TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), 0, io));
     }
-    TRY(seq_verify(c, ke));
+    TRY(seq_verify(c, ke, keys && ke > 1 ? nmx_head_row_nkeys(nv) : 0));
     TRY(commit_lin_cur(c, 0));
-    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c), 1));
+    TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c), 1, 0));
     return PINFER_OK;
 }
 
 /* One n-gram round (the host uploaded the drafts into vt[1..ke]): the verify, the commit,
  * n_past += e. The committed rows stay in s.xn for the host to queue for the MTP pass. */
 static int seq_round_ng(pinfer_ctx *c, int ke) {
-    TRY(seq_verify(c, ke));
+    TRY(seq_verify(c, ke, 0));
     TRY(commit_lin_cur(c, 0));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
@@ -204,7 +207,7 @@ static int prefill(pinfer_ctx *c, const int32_t *prompt, int n, int use_mtp, int
         const int nb = n - c0 < E_MAX_BATCH ? n - c0 : E_MAX_BATCH, last = c0 + nb == n;
         CK(nmx_upload(c->dev, c->tok, prompt + c0, (size_t)nb * sizeof(int32_t)));
         TRY(e_set_pos(c, c->n_past));
-        TRY(e_forward(c, c->tok, nb, 0));
+        TRY(e_forward(c, c->tok, nb, 0, 0));
         if (last) TRY(e_head_last(c, nb, c->vt, 0));
         if (use_mtp) {
             CK(nmx_copy_d2d(c->dev, c->hbuf, c->s.xn, (size_t)nb * c->H * sizeof(float)));
@@ -212,7 +215,7 @@ static int prefill(pinfer_ctx *c, const int32_t *prompt, int n, int use_mtp, int
             CK(nmx_upload(c->dev, c->tok, next, (size_t)nb * sizeof(int32_t)));
             if (last) CK(nmx_copy_d2d(c->dev, c->tok + nb - 1, c->vt, sizeof(int32_t)));
             TRY(e_mtp_forward(c, c->hbuf, c->tok, nb, 0, 0, nv, last ? c->vt + 1 : NULL,
-                              last ? m_cur(c) : NULL, 0));
+                              last ? m_cur(c) : NULL, 0, 0));
         }
         c->n_past += nb;
     }
@@ -247,7 +250,7 @@ static int flush_pending(pinfer_ctx *c, e_pending *pd, int nv) {
     if (pd->n == 0) return PINFER_OK;
     CK(nmx_upload(c->dev, c->tok, pd->tok, (size_t)pd->n * sizeof(int32_t)));
     TRY(e_set_pos(c, pd->pos));
-    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c), 0));
+    TRY(e_mtp_forward(c, c->pbuf, c->tok, pd->n, 0, 0, nv, c->vt + 1, m_cur(c), 0, 0));
     c->mtp_rows = pd->pos + pd->n;
     pd->n = 0;
     TRY(e_set_pos(c, c->n_past));
@@ -270,7 +273,7 @@ static int plain_step(pinfer_ctx *c, int use_mtp, e_pending *pd, int nv, int32_t
     const int P = c->n_past;
     if (use_mtp && pd->n == E_MAX_BATCH) TRY(flush_pending(c, pd, nv));
     TRY(e_set_pos(c, P));
-    TRY(e_forward(c, c->vt, 1, 0));
+    TRY(e_forward(c, c->vt, 1, 0, 0));
     c->keep = 0;
     TRY(e_head_last(c, 1, c->vt, 0));
     CK(nmx_download(c->dev, next, c->vt, sizeof(int32_t)));

@@ -121,7 +121,12 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
                             A8]),
     "nmx_silu_mul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, A8]),
     "nmx_q4k_matmul_embed_norm": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp, _vp, _vp,
-                                       _i, _vp, ctypes.c_float, A8]),
+                                       _i, _vp, ctypes.c_float, A8, _vp, _i]),
+    "nmx_head_row_keys": (_i, [_vp, _vp, _i, _i, _vp, _i, _vp, _i, _vp, ctypes.c_float, _vp, _i,
+                               _i, _vp, _vp]),
+    "nmx_head_row_nkeys": (_i, [_i]),
+    "nmx_embed_norm_keys": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _vp, _i, A8,
+                                 _vp, _i]),
     "nmx_q4k_matmul_norm": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, ctypes.POINTER(NormIn),
                                  A8]),
     "nmx_lin_pre": (_i, [_vp, ctypes.POINTER(LinPreArgs)]),
@@ -343,14 +348,34 @@ class Device:
                                            A8(*[_p(t) for t in a1])), "embed_norm")
 
     def q4k_matmul_embed_norm(self, W, rows: int, Y, n: int, H: int, E, vocab: int, tok, w_emb,
-                              h, w_hid, eps: float, a8_tmp=(None, None, None)) -> None:
+                              h, w_hid, eps: float, a8_tmp=(None, None, None), tok_keys=None,
+                              nkeys: int = 0) -> None:
         """nmx_q4k_matmul_embed_norm on contiguous rows: Y [n][rows] = W x A8 of
-        [rmsnorm(embed(tok), w_emb) | rmsnorm(h, w_hid)]."""
+        [rmsnorm(embed(tok), w_emb) | rmsnorm(h, w_hid)]; with tok_keys (one row) the token is
+        the argmax of the nkeys partial keys, written to tok[0]."""
         self.check(self.lib.nmx_q4k_matmul_embed_norm(self.ctx, _p(W), rows, _p(Y), rows, n, H,
                                                       _p(E), vocab, _p(tok), _p(w_emb), _p(h),
                                                       H, _p(w_hid), eps,
-                                                      A8(*[_p(t) for t in a8_tmp])),
+                                                      A8(*[_p(t) for t in a8_tmp]),
+                                                      _p(tok_keys), nkeys),
                    "q4k_matmul_embed_norm")
+
+    def head_row_keys(self, W, rows: int, cols: int, x, nrows: int, w, eps: float, idx, off: int,
+                      keys, *, add=None, y=None) -> None:
+        """nmx_head_row_keys: the one-row head's partial argmax keys (no reduction)."""
+        self.check(self.lib.nmx_head_row_keys(self.ctx, _p(W), rows, cols, _p(x), cols, _p(add),
+                                              cols, _p(w), eps, _p(idx), off, nrows, _p(y),
+                                              _p(keys)), "head_row_keys")
+
+    def head_row_nkeys(self, rows: int) -> int:
+        return self.lib.nmx_head_row_nkeys(rows)
+
+    def embed_norm_keys(self, E, vocab: int, tok, n: int, cols: int, eps: float, w, keys,
+                        nkeys: int, *, xo=None, a8=(None, None, None)) -> None:
+        """nmx_embed_norm_keys: nmx_embed_norm (one set) with row n - 1's token from keys."""
+        self.check(self.lib.nmx_embed_norm_keys(self.ctx, _p(E), vocab, _p(tok), n, cols, eps,
+                                                _p(w), _p(xo), cols, A8(*[_p(t) for t in a8]),
+                                                _p(keys), nkeys), "embed_norm_keys")
 
     def silu_mul(self, gate, up, n: int, cols: int, y=None, a8=(None, None, None)) -> None:
         self.check(self.lib.nmx_silu_mul(self.ctx, _p(gate), _p(up), cols, n, cols, _p(y),

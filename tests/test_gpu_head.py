@@ -304,3 +304,63 @@ def test_head_row_accept_equals_norm_then_head(dev, case):
         assert_bits_equal(y.numpy(), y_ref.numpy(), "y")
     else:
         assert not y.numpy().any(), "y written without being asked for"
+
+
+@pytest.mark.parametrize("rows,n", [(32768, 5), (10004, 1), (2048, 3)])
+def test_head_row_keys_resolved_by_consumers(dev, rows, n):
+    """nmx_head_row_keys (the draft head without its reduction) resolved by its two consumers:
+    nmx_embed_norm_keys (the verify's first norm, last row) and nmx_q4k_matmul_embed_norm with
+    tok_keys (the next MTP pass's fc input). The token each writes equals the one
+    nmx_head_row_accept_to returns, and their outputs equal those of the same calls given that
+    token, bit for bit."""
+    cols, eps, vocab = 1024, 1e-6, rows
+    print(f"[case] head_row_keys rows={rows} n={n}", flush=True)
+    rng = np.random.default_rng(900 + rows + n)
+    W = quantized_head(rng, rows, cols)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    dW, dx, dw = dev.to_device(W), dev.to_device(x), dev.to_device(w)
+    didx = dev.to_device(np.array([1], np.int32))
+    # the token by the head with its own reduction
+    work = dev.zeros(dev.head_work_bytes(rows, 1), np.uint8)
+    out, tok_ref = dev.zeros(3, np.int32), dev.zeros(1, np.int32)
+    dev.head_row_accept_to(dW, rows, cols, dx, 3, dw, eps, didx, 0, work, out, tok_ref)
+    nk = dev.head_row_nkeys(rows)
+    keys = dev.zeros(nk, np.uint64)
+    y = dev.zeros((1, cols), np.float32)
+    dev.head_row_keys(dW, rows, cols, dx, 3, dw, eps, didx, 0, keys, y=y)
+    dev.sync()
+    t = int(tok_ref.numpy()[0])
+    # the verify's first norm: rows 0..n-2 from tok, row n-1 from the keys
+    toks = rng.integers(0, vocab, n).astype(np.int32)
+    toks_ref = toks.copy()
+    toks_ref[n - 1] = t
+    toks[n - 1] = -7  # never read
+    dtok, dtok_ref = dev.to_device(toks), dev.to_device(toks_ref)
+    xo, xo_ref = dev.zeros((n, cols), np.float32), dev.zeros((n, cols), np.float32)
+    a8 = tuple(dev.zeros(s, t_) for s, t_ in (((cols // 32, n, 32), np.int8),
+                                              ((cols // 32, n), np.float32),
+                                              ((cols // 32, n), np.float32)))
+    a8_ref = tuple(dev.zeros(s, t_) for s, t_ in (((cols // 32, n, 32), np.int8),
+                                                  ((cols // 32, n), np.float32),
+                                                  ((cols // 32, n), np.float32)))
+    dev.embed_norm_keys(dW, vocab, dtok, n, cols, eps, dw, keys, nk, xo=xo, a8=a8)
+    dev.embed_norm(dW, vocab, dtok_ref, n, cols, eps, dw, xo0=xo_ref, a0=a8_ref)
+    # the fc input of the next pass: one row, its token from the keys
+    H = cols
+    Wfc = quantized_head(rng, H, 2 * H)
+    h = rng.standard_normal((1, H)).astype(np.float32)
+    dWfc, dh = dev.to_device(Wfc), dev.to_device(h)
+    tk1, tk1_ref = dev.to_device(np.array([-5], np.int32)), dev.to_device(np.array([t], np.int32))
+    Y, Y_ref = dev.zeros((1, H), np.float32), dev.zeros((1, H), np.float32)
+    dev.q4k_matmul_embed_norm(dWfc, H, Y, 1, H, dW, vocab, tk1, dw, dh, dw, eps, tok_keys=keys,
+                              nkeys=nk)
+    dev.q4k_matmul_embed_norm(dWfc, H, Y_ref, 1, H, dW, vocab, tk1_ref, dw, dh, dw, eps)
+    dev.sync()
+    assert int(dtok.numpy()[n - 1]) == t, "embed_norm_keys token"
+    assert_bits_equal(dtok.numpy(), toks_ref, "token row")
+    assert_bits_equal(xo.numpy(), xo_ref.numpy(), "embedding rows")
+    for a, b, what in zip(a8, a8_ref, ("codes", "scales", "fsum")):
+        assert_bits_equal(a.numpy(), b.numpy(), f"A8 {what}")
+    assert int(tk1.numpy()[0]) == t, "fc token"
+    assert_bits_equal(Y.numpy(), Y_ref.numpy(), "fc output")
