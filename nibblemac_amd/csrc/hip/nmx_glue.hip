@@ -1154,6 +1154,14 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
     const int l = blockIdx.y;
     const int E = a.ctl[1] - 1;
     const int tid = blockIdx.x * 256 + threadIdx.x, stride = gridDim.x * 256;
+    if (E == 0 && !a.redo) { /* e = 1: the state after token 0 is the committed one, no replay
+                              * rows, and no later commit of a smaller e can need the kept rows */
+        if (l == 0 && tid == 0) {
+            a.ctl[2] = 0;
+            if (a.vt) a.vt[0] = a.vt[1];
+        }
+        return;
+    }
     float *st = a.state + (size_t)l * a.S * a.C;
     float *bk = a.bak ? a.bak + (size_t)l * a.S * a.C : nullptr;
     const float *src0 = a.redo ? bk : st; /* rows of the state after token 0 */
