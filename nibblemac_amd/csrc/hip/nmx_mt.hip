@@ -615,9 +615,9 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
 
 /* Rows per workgroup for a pass of nv vectors, its threads and blocks per dot unit (*bpu).
  * SwiGLU needs R = 64 (32 gate + 32 up rows = one A8 block). The other launches use chain
- * records and R = 8 (else 4): measured on the verify shapes (1024 .. 3584 columns, 5 vectors)
- * this beat every larger R, since a small workgroup's dot and chain phases are short and
- * several workgroups share a CU. Without a norm prologue, each unit thread takes one block
+ * records and R = 4: measured on the verify shapes (1024 .. 3584 columns, 5 vectors) this beat
+ * every larger R (8 by about 1 tok/s end to end: twice the workgroups, so every CU streams
+ * weights, each with the same short dot and chain phases). Without a norm prologue, each unit thread takes one block
  * when the workgroup's units fit in 1024 threads, else 4 (at most 256 threads): a unit's blocks
  * are one dependent sequence of LDS reads, dots and record stores, so more units shorten the
  * dot phase. */
@@ -648,7 +648,7 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
         }
         return 0;
     }
-    for (int R = swiglu ? 64 : 8; R >= 4; R >>= 1) {
+    for (int R = swiglu ? 64 : 4; R >= 4; R >>= 1) {
         if (swiglu && R != 64) break;
         if (!swiglu && !norm) *bpu = R * 8 * nsb <= MT_REC_THREADS ? 1 : 4;
         if (swiglu) *bpu = R * 4 * nsb <= MT_REC_THREADS ? 2 : 4;
