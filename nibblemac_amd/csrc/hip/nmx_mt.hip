@@ -638,7 +638,11 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
                 const int units = R * (8 / b) * nsb;
                 const int t = 64 * (((units > R * nv ? units : R * nv) + 63) / 64);
                 const int cpt = pair ? 8 : b < 4 ? 2 : MT_NORM_CPT;
-                const int tt = t * cpt < cols ? 64 * ((cols / cpt + 63) / 64) : t;
+                int tt = t * cpt < cols ? 64 * ((cols / cpt + 63) / 64) : t;
+                /* the norm's four chains and tail of each of its (PAIR: 2 nv) rows take one
+                 * thread each */
+                const int tmin = 64 * ((5 * (pair ? 2 : 1) * nv + 63) / 64);
+                tt = tt < tmin ? tmin : tt;
                 if (tt > (b < 4 ? MT_REC_THREADS : MT_NORM_THREADS)) continue;
                 *threads = tt;
                 *bpu = b;
@@ -674,6 +678,8 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
                                          hipFuncAttributeMaxDynamicSharedMemorySize, MT_LDS));
         ready = true;
     }
+    if (NORM && T < 5 * (PAIR ? 2 : 1) * NV) /* one thread per chain and tail of each norm row */
+        return nmx_fail(ctx, "q4k_mt: %d threads for the norm of %d rows", T, (PAIR ? 2 : 1) * NV);
     const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI, PAIR).total;
     const void *in0 = NORM ? (const void *)nm.x : (const void *)q;
     const void *in1 = NORM ? (const void *)nm.add : (const void *)d;

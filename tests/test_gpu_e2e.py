@@ -146,6 +146,28 @@ def test_ngram_drafts_match_reference(models, agree_model, which, k, ngram):
 
 
 @needs_ref
+@pytest.mark.parametrize("k", [2, 4])
+def test_ngram_rounds_state_matches_reference(models, k):
+    """Prompt-lookup rounds late in the generation (the repeated prompt is matched after about
+    90 tokens): their committed rows wait for one MTP pass over up to k + 3 rows after the
+    loop, which runs the MTP fc projection with its embedding and norms inside at 7 rows of a
+    256-wide hidden. The state blob after the generation, MTP cache included, equals the
+    reference engine's (it once held 6 wrong MTP rows: that launch's norm had fewer threads
+    than chains)."""
+    base = np.random.default_rng(9).integers(0, pqfile.SMALL.vocab, 24)
+    prompt = np.concatenate([base, base[:20], base])
+    gpu, ref = pair(models["small"])
+    print(f"[case] n-gram rounds state k={k}", flush=True)
+    tg, sg = gpu.generate(prompt, 96, k=k, ngram=4)
+    tr, sr = ref.generate(prompt, 96, k=k, ngram=4)
+    assert tg == tr
+    assert counters(sg) == counters(sr)
+    assert sg.ngram_rounds > 0, "the workload no longer reaches an n-gram round"
+    assert gpu.state_save() == ref.state_save(), "state after n-gram rounds"
+    gpu.close(), ref.close()
+
+
+@needs_ref
 @pytest.mark.parametrize("which,k,ngram", [("agree", 4, 0), ("agree", 8, 7), ("small", 4, 0),
                                            ("small", 2, 4)])
 def test_adaptive_matches_reference(models, agree_model, which, k, ngram):

@@ -190,7 +190,8 @@ def test_embed_norm(dev, cols, n):
             assert_bits_equal(got.numpy(), ref, f"{what} A8 {part}")
 
 
-@pytest.mark.parametrize("H,n", [(1024, 1), (1024, 5), (1024, 8), (256, 3), (512, 13)])
+@pytest.mark.parametrize("H,n", [(1024, 1), (1024, 5), (1024, 6), (1024, 7), (1024, 8), (256, 3),
+                                 (256, 5), (256, 6), (256, 7), (256, 8), (512, 6), (512, 13)])
 def test_matmul_embed_norm(dev, H, n):
     """nmx_q4k_matmul_embed_norm (the MTP head's fc projection with its embedding and both input
     norms inside the matmul's workgroups; 13 rows take the two-call path) against
