@@ -304,6 +304,26 @@ typedef struct {
     float eps;
 } nmx_norm_in;
 
+/* The launch geometry of the small-row matmul kernel behind nmx_q4k_matmul_norm,
+ * nmx_q4k_swiglu, nmx_q4k_matmul_embed_norm (pair = 1: the MTP fc input, cols = 2 H) and the
+ * plain projections of fewer than 32768 rows, for count matrices of rows[s] rows, cols columns
+ * and n activation rows. Host only (no device, no context): returns 1 and fills g when that
+ * kernel takes the shape, 0 when the shape goes to the other kernels, -1 when the geometry it
+ * picks would leave one of the kernel's phases (weight units, chains, norm columns, norm
+ * chains, PAIR decoders, SwiGLU epilogue, LDS) without the threads it assumes, which the
+ * launch refuses with an error. No counterpart in the reference: its kernels are scalar. */
+typedef struct {
+    int rows_per_wg;       /* R: output rows of one workgroup */
+    int threads;           /* T: threads per workgroup (every pass) */
+    int blocks_per_unit;   /* 32-column blocks per weight unit (1, 2 or 4) */
+    int workgroups;
+    int passes;            /* passes of at most 8 vectors */
+    int nv[8];             /* vectors of each pass */
+    int lds_bytes[8];      /* dynamic LDS of each pass */
+} nmx_mt_geometry;
+int nmx_mt_plan(int count, const int *rows, int cols, int n, int norm, int swiglu, int pair,
+                nmx_mt_geometry *g);
+
 /* nmx_q4k_matmul_multi on the A8 of rmsnorm(in): the norm and the quantization run inside the
  * matmul's workgroups (equal to nmx_rmsnorm + the matmul bit for bit). a8_tmp (n x cols A8
  * buffers) is used only when the shape is outside the fused kernel's limits. */
@@ -373,7 +393,11 @@ int nmx_attn(nmx_ctx *ctx, const nmx_attn_args *p);
  * and at most 8 tokens, else the two calls. */
 int nmx_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p);
 
-/* flag[0] = (top-1 probability of logits[0, n) >= tau): with mx = max (pf_softmax_max) and
+/* The reference's chain gate (engine/src/spec_adapt.c:56, spec.c:89-97) as a device op, for a
+ * caller that drives the reference's own confidence-gated adaptive chain on this device layer;
+ * the engine's own adaptive policy (pinfer_spec_params.adaptive) decides on the host and does
+ * not call it.
+ * flag[0] = (top-1 probability of logits[0, n) >= tau): with mx = max (pf_softmax_max) and
  * s = sum of pf_expf(l_i - mx) in the reference's order (4 interleaved partial sums, tail,
  * pf_softmax_exp engine/src/forward_ops.c:294-353), p = s > 0 ? 1 / s : 0 (spec.c:93-97
  * top1_prob). One workgroup; the decision is exact (an fp64 sum decides unless p is within the
@@ -385,7 +409,9 @@ int nmx_top1_gate(nmx_ctx *ctx, const float *logits, int n, float tau, int32_t *
  * 1..e-1]; pend <- log rows 1..e-1; ctl[2] = e - 1. Arrays are [layers][...] contiguous.
  * state_bak (optional, the size of state) keeps the rows of the state after token 0; a later
  * call with redo = 1 commits a smaller e from them (the host's stop inside a run that the
- * device already committed). */
+ * device already committed). A commit of e = 1 returns before it touches state_bak (the state
+ * after token 0 is then already the committed one), so a redo is valid only after a commit
+ * of e >= 2 and for a smaller e, which is the only case in which the engine issues one. */
 typedef struct {
     int layers, C, conv_k;
     float *state;          /* [layers][conv_k-1][C] */

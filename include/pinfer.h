@@ -76,11 +76,14 @@ int pinfer_eval_select(pinfer_ctx *ctx, const int32_t *tokens, int n, const int3
 typedef struct {
     int k;           /* drafts per verification pass, 0..PINFER_SPEC_MAX_K; 0 = plain */
     int draft_vocab; /* drafts are the argmax over ids [0, draft_vocab); <= 0: full vocabulary */
-    int adaptive;    /* 1: the reference's adaptive policy (engine/src/spec_adapt.c): MTP chains
-                      * end where the newest draft's top-1 probability is below 0.6 (decided on
-                      * the device, nmx_top1_gate), plain steps while speculation is slower than
-                      * a plain step, probed back after 8..64 plain steps. Speed only: the tokens
-                      * equal the fixed-k and the plain greedy output */
+    int adaptive;    /* 1: each MTP round's width is chosen on the host (the role of
+                      * engine/src/spec_adapt.c, by a policy of this engine's own): the width w
+                      * (1 = a plain step, else 1 + drafts, at most k + 1) that maximises the
+                      * expected tokens per second, from decayed per-draft-position acceptance
+                      * counts and the measured seconds of each width's rounds, the stalest
+                      * width re-measured every 32 rounds; prompt-lookup rounds are not part
+                      * of that model. Speed only: the tokens equal the fixed-k and the plain
+                      * greedy output */
     int ngram;       /* prompt-lookup drafts of up to ngram tokens (0..PINFER_SPEC_MAX_K), tried
                       * before the MTP drafts each round (engine/src/spec.c:133-151) */
 } pinfer_spec_params;

@@ -668,6 +668,46 @@ int pick_rows(int cols, int nv, bool norm, bool swiglu, int total_rows, int coun
     return 0;
 }
 
+/* Launch bound of q4k_mt_k<NV, NORM, SWI, BPU, PAIR> (its __launch_bounds__). */
+constexpr int mt_bound(bool norm, bool swi, int bpu) {
+    return bpu < 4 ? MT_REC_THREADS : norm ? MT_NORM_THREADS : swi ? MT_MAX_THREADS : MT_REC4_THREADS;
+}
+
+/* Whether T threads give every phase of q4k_mt_k<nv, norm, swi, bpu, pair> at R rows per
+ * workgroup and cols columns the threads that phase assumes; NULL if so, else the first need
+ * that fails. A phase whose work items outnumber its threads would leave LDS that a later
+ * phase reads unwritten, so the launch refuses such a geometry.
+ *   - the weight units: one thread per (row, BPU-block unit), R (8 / bpu) (cols / 256);
+ *   - the chains: one thread per (row, vector), R nv;
+ *   - the plain norm prologue: T columns per step, CPT steps (2 for 1- and 2-block units,
+ *     else MT_NORM_CPT), so T CPT >= cols;
+ *   - the norm's chains and tails: 4 + 1 threads per normed row (nv rows; PAIR 2 nv);
+ *   - PAIR: one float4 of each h row per thread (cols / 8) and one embedding block of each
+ *     row per thread (nv cols / 64);
+ *   - SwiGLU: R = 64 and one thread per (vector, output column), nv R / 2.
+ * Loops that stride by T (the activation staging, the A8 of the normed rows) need only T to
+ * be a multiple of 64 (lane pairs stay in one wave). */
+const char *mt_geometry_error(int cols, int nv, int R, int T, int bpu, bool norm, bool swi,
+                              bool pair) {
+    const int nsb = cols >> 8;
+    if (cols <= 0 || cols % 256) return "cols not a multiple of 256";
+    if (nv < 1 || nv > MT_MAX_NV) return "vectors per pass";
+    if (bpu != 1 && bpu != 2 && bpu != 4) return "blocks per unit";
+    if (R < 4 || R % 4) return "rows per workgroup";
+    if (T < 64 || T % 64) return "threads not a multiple of 64";
+    if (T > mt_bound(norm, swi, bpu)) return "threads above the launch bound";
+    if (T < R * (8 / bpu) * nsb) return "threads for the weight units";
+    if (T < R * nv) return "threads for the chains";
+    if (pair && (!norm || swi || bpu != 1 || cols % 512)) return "PAIR variant";
+    if (norm && !pair && T * (bpu < 4 ? 2 : MT_NORM_CPT) < cols) return "threads for the norm columns";
+    if (norm && T < 5 * (pair ? 2 : 1) * nv) return "threads for the norm chains";
+    if (pair && T < cols / 8) return "threads for the h float4s";
+    if (pair && T < nv * (cols / 64)) return "threads for the embedding blocks";
+    if (swi && (R != 64 || T < nv * (R / 2))) return "SwiGLU rows or epilogue threads";
+    if (mt_layout(cols, nv, R, norm, swi, pair).total > MT_LDS) return "LDS";
+    return nullptr;
+}
+
 template <int NV, bool NORM, bool SWI, int BPU, bool PAIR = false>
 int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v0, int R, int T,
                const int8_t *q, const float *d, const float *fs, const nmx_norm_in &nm,
@@ -678,8 +718,9 @@ int launch_one(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int 
                                          hipFuncAttributeMaxDynamicSharedMemorySize, MT_LDS));
         ready = true;
     }
-    if (NORM && T < 5 * (PAIR ? 2 : 1) * NV) /* one thread per chain and tail of each norm row */
-        return nmx_fail(ctx, "q4k_mt: %d threads for the norm of %d rows", T, (PAIR ? 2 : 1) * NV);
+    if (const char *why = mt_geometry_error(cols, NV, R, T, BPU, NORM, SWI, PAIR))
+        return nmx_fail(ctx, "q4k_mt: geometry cols=%d nv=%d R=%d T=%d bpu=%d: %s", cols, NV, R,
+                        T, BPU, why);
     const size_t lds = (size_t)mt_layout(cols, NV, R, NORM, SWI, PAIR).total;
     const void *in0 = NORM ? (const void *)nm.x : (const void *)q;
     const void *in1 = NORM ? (const void *)nm.add : (const void *)d;
@@ -716,6 +757,37 @@ int launch_nv(nmx_ctx *ctx, const MtTab &tab, int groups, int cols, int n, int v
     return launch_one<NV, false, false, 4>(ctx, tab, groups, cols, n, v0, R, T, q, d, fs, none, out);
 }
 
+/* The geometry of an n-vector product over count matrices (rows[s] rows each): 0 and the
+ * plan when q4k_mt_k takes the shape, 1 when the shape belongs to the other kernels. The
+ * passes are equal-size groups of at most MT_MAX_NV vectors, larger first (every pass performs
+ * the same per-vector operations, so the split does not change any result); the first pass's
+ * thread count covers every pass. */
+struct MtPlan {
+    int R, T, bpu, nv_max;
+};
+
+int mt_plan(int count, const int *rows, int cols, int n, bool norm, bool swiglu, bool pair,
+            MtPlan *pl) {
+    if (count < 1 || count > NMX_MAX_SEGS || cols <= 0 || cols % 256 || n < 1 || n > MT_MAX_NV)
+        return 1;
+    if (swiglu && (count != 2 || rows[0] != rows[1] || rows[0] % 32)) return 1;
+    if (pair && (!norm || swiglu || cols % 512)) return 1;
+    const int passes = (n + MT_MAX_NV - 1) / MT_MAX_NV;
+    pl->nv_max = (n + passes - 1) / passes;
+    int total_rows = 0;
+    for (int s = 0; s < count; s++) total_rows += rows[s];
+    pl->T = 0;
+    pl->bpu = 4;
+    pl->R = pick_rows(cols, pl->nv_max, norm, swiglu, total_rows, count, &pl->T, &pl->bpu, pair);
+    return pl->R ? 0 : 1;
+}
+
+/* Vectors of each pass: the largest-first equal split of n into passes of <= MT_MAX_NV. */
+int mt_pass_nv(int left) {
+    const int np = (left + MT_MAX_NV - 1) / MT_MAX_NV;
+    return (left + np - 1) / np;
+}
+
 } // namespace
 
 int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int n,
@@ -723,24 +795,17 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
                   bool swiglu, nmx_a8 out, const nmx_mt_pair *pair) {
     /* more rows than one pass: the row-per-lane / K-split kernels read the weights once for
      * all of them (prefill chunks) */
-    if (count < 1 || count > NMX_MAX_SEGS || cols % 256 || n < 1 || n > MT_MAX_NV) return 1;
-    if (swiglu && (count != 2 || segs[0].rows != segs[1].rows || segs[0].rows % 32)) return 1;
-    if (pair && (!norm || swiglu || cols % 512 || (uintptr_t)pair->w_emb & 15 ||
-                 (uintptr_t)pair->h & 15 || pair->h_stride % 4 || (pair->keys && n != 1)))
+    if (count < 1 || count > NMX_MAX_SEGS) return 1;
+    if (pair && ((uintptr_t)pair->w_emb & 15 || (uintptr_t)pair->h & 15 || pair->h_stride % 4 ||
+                 (pair->keys && n != 1)))
         return 1;
-    /* equal-size passes of at most MT_MAX_NV vectors, larger first: every pass performs the
-     * same per-vector operations, so the split does not change any result */
-    const int passes = (n + MT_MAX_NV - 1) / MT_MAX_NV;
-    int T = 0;
-    const int nv_max = (n + passes - 1) / passes;
     /* the fused norm reads its weight as float4 */
     if (norm && ((uintptr_t)norm->w & 15)) return 1;
-    int total_rows = 0;
-    for (int s = 0; s < count; s++) total_rows += segs[s].rows;
-    int bpu = 4;
-    const int R = pick_rows(cols, nv_max, norm != nullptr, swiglu, total_rows, count, &T, &bpu,
-                            pair != nullptr);
-    if (!R) return 1;
+    int rows[NMX_MAX_SEGS];
+    for (int s = 0; s < count; s++) rows[s] = segs[s].rows;
+    MtPlan pl;
+    if (mt_plan(count, rows, cols, n, norm != nullptr, swiglu, pair != nullptr, &pl)) return 1;
+    const int R = pl.R, T = pl.T, bpu = pl.bpu;
     MtTab tab{};
     tab.count = count;
     int groups = 0;
@@ -754,7 +819,7 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
         tab.g0[1] = groups; /* never selected: both halves are addressed from segment 0 */
     }
     for (int v0 = 0; v0 < n;) {
-        const int left = n - v0, np = (left + MT_MAX_NV - 1) / MT_MAX_NV, nv = (left + np - 1) / np;
+        const int nv = mt_pass_nv(n - v0);
         const int Tn = T; /* the first (largest) pass's thread count covers every pass */
         int rc;
         switch (nv) {
@@ -774,6 +839,33 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
 }
 
 extern "C" {
+
+int nmx_mt_plan(int count, const int *rows, int cols, int n, int norm, int swiglu, int pair,
+                nmx_mt_geometry *g) {
+    if (!rows || !g || count < 1 || count > NMX_MAX_SEGS) return 0;
+    for (int s = 0; s < count; s++)
+        if (rows[s] <= 0 || rows[s] % 4) return 0;
+    MtPlan pl;
+    if (mt_plan(count, rows, cols, n, norm != 0, swiglu != 0, pair != 0, &pl)) return 0;
+    *g = nmx_mt_geometry{};
+    g->rows_per_wg = pl.R;
+    g->threads = pl.T;
+    g->blocks_per_unit = pl.bpu;
+    int groups = 0;
+    for (int s = 0; s < count; s++) groups += (rows[s] + pl.R - 1) / pl.R;
+    g->workgroups = swiglu ? rows[0] / (pl.R / 2) : groups;
+    int rc = 1;
+    for (int v0 = 0; v0 < n;) {
+        const int nv = mt_pass_nv(n - v0);
+        g->nv[g->passes] = nv;
+        g->lds_bytes[g->passes] = mt_layout(cols, nv, pl.R, norm != 0, swiglu != 0, pair != 0).total;
+        g->passes++;
+        if (mt_geometry_error(cols, nv, pl.R, pl.T, pl.bpu, norm != 0, swiglu != 0, pair != 0))
+            rc = -1;
+        v0 += nv;
+    }
+    return rc;
+}
 
 int nmx_q4k_matmul_norm(nmx_ctx *ctx, int count, const void *const *W, const int *rows,
                         float *const *Y, const int *y_stride, int cols, int n,

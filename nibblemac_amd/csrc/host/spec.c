@@ -148,7 +148,9 @@ static int launch_round(pinfer_ctx *c, int ke, int nv, int ng) {
 /* A stop inside the accepted run: commit e (< a + 1) instead of the device's a + 1, after the
  * round on the stream: ctl[1] = e, the linear layers' commit redone from the kept conv rows,
  * ctl[0] = P + e, cur = the host's vt[e] (the round's MTP pass has overwritten vt[1]). */
-static int recommit(pinfer_ctx *c, int P, int e, int32_t cur) {
+static int recommit(pinfer_ctx *c, int P, int e, int32_t cur, int e_device) {
+    /* the device's commit of e = 1 keeps no conv rows (nmx_commit_args): a redo needs e >= 2 */
+    if (e < 1 || e >= e_device || e_device < 2) return PINFER_E_ARG;
     CK(nmx_ctl_set(c->dev, c->ctl, 1, e));
     TRY(commit_lin_cur(c, 1));
     CK(nmx_ctl_set(c->dev, c->ctl, 0, P + e));
@@ -401,7 +403,7 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
         memcpy(vt, c->mbox + 2, (size_t)(ke + 2) * sizeof(int32_t));
         int e = 0;
         while (e <= a && !done) done = emit(out, &count, n_max, vt[++e], &stop);
-        if (e != a + 1 && (rc = recommit(c, P, e, vt[e])) != PINFER_OK) break;
+        if (e != a + 1 && (rc = recommit(c, P, e, vt[e], a + 1)) != PINFER_OK) break;
         if (use_ng) {
             if (use_mtp && (rc = defer_rows(c, &pd, vt + 1, e, P)) != PINFER_OK) break;
         } else {
@@ -422,7 +424,9 @@ int e_generate_timed(pinfer_ctx *c, const int32_t *prompt, int n_prompt, int32_t
             }
         }
         const double t = now_sec();
-        if (adaptive) e_adapt_observe(&ad, ke + 1, a, t - t_last);
+        /* prompt-lookup rounds cost and accept differently from MTP rounds of the same width:
+         * they stay out of the MTP width model */
+        if (adaptive && !use_ng) e_adapt_observe(&ad, ke + 1, a, t - t_last);
         t_last = t;
     }
     if (rc == PINFER_OK && use_mtp) rc = flush_pending(c, &pd, nv);

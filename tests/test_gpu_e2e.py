@@ -161,7 +161,8 @@ def test_ngram_rounds_state_matches_reference(models, k):
     tg, sg = gpu.generate(prompt, 96, k=k, ngram=4)
     tr, sr = ref.generate(prompt, 96, k=k, ngram=4)
     assert tg == tr
-    assert counters(sg) == counters(sr)
+    # the drafters differ (this engine's match finder, the reference's hash tables), so the
+    # rounds may too: only the reachability of an n-gram round and the state are checked
     assert sg.ngram_rounds > 0, "the workload no longer reaches an n-gram round"
     assert gpu.state_save() == ref.state_save(), "state after n-gram rounds"
     gpu.close(), ref.close()
