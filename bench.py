@@ -12,10 +12,13 @@ a 512-token random prompt, then generate exactly 128 tokens with EOS ignored at 
 verification pass, drafts from the MTP head over the first 32768 ids. `value` is verified tokens
 per second of the decode: (128 - 1) per step / decode seconds, over K steps.
 
-`roofline` is the LM head as the verify pass runs it (nmx_head_accept: the Q4K x A8 matvec
-248320 x 1024 over k + 1 = 5 rows with the fused argmax, then the acceptance), four rotating
-copies of the 143 MB head so no launch finds it in the 256 MB MALL, timed with HIP events on the
-stream it runs on. `kernels` holds configs 1-4 (nibblemac_amd/kbench.py). `cpu_baseline` is the
+`roofline` is the LM head as the verify round launches it (nmx_head_keys: the Q4K x A8 matvec
+248320 x 1024 over k + 1 = 5 rows with the fused argmax, leaving partial keys whose reduction and
+the acceptance run in the commit's workgroups), four rotating copies of the 143 MB head so no
+launch finds it in the 256 MB MALL, timed with HIP events around back-to-back launches on the
+stream it runs on (so the time is the kernel's, as a kernel trace reports it; the graph-replay
+time is given beside it); the line also carries the same launch with the head resident in the
+MALL (one copy). `kernels` holds configs 1-4 (nibblemac_amd/kbench.py). `cpu_baseline` is the
 reference engine's own sources with the oracle's threaded Q4K operators
 (oracle/_ref/libpinfer_refq4k.so) on the host cores: the config-5 workload itself on the GPU
 box's CPU share (16 threads), its tokens checked against the GPU's, plus a 1-thread run on a
@@ -110,22 +113,27 @@ def head_roofline(copies: int = 4, eager: bool = False, copy_mib: int = 0) -> di
         if eager:
             return head_eager(dev, copies)
         r = kbench.config4_head(dev, copies=copies)
-    line = r["accept0of4"]
+    line = r["in_path_cold"]
     traffic = None
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
     gbs = line["GB_s"]
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "q4k_mvx_k<5,true> + head_finish_k (LM head 248320x1024 Q4K x 5 A8 rows, "
-                      "fused argmax + acceptance, as the verify pass runs it; cold)",
-            "us_per_launch": line["us"], "algorithmic_bytes": r["algorithmic_bytes"],
-            "copies": copies, "timing": "graph replays, HIP events on the kernels' stream",
-            "accept_sweep_us": {k: v["us"] for k, v in r.items() if k.startswith("accept")}}
+            "kernel": r["in_path_kernel"] + ": the LM head 248320x1024 Q4K x 5 A8 rows with the "
+                      "fused argmax as the verify round launches it (the keys' reduction and the "
+                      "acceptance run in the commit's workgroups); cold",
+            "us_per_launch": line["us"], "algorithmic_bytes": r["in_path_algorithmic_bytes"],
+            "copies": copies,
+            "timing": "HIP events around 40 back-to-back launches on the kernel's stream (the "
+                      "kernel's duration); us_graph_replay: the same launches as graph replays",
+            "us_graph_replay": line["us_graph_replay"],
+            "warm_mall_resident": r["in_path_warm"],
+            "api_head_accept_us": {k: v["us"] for k, v in r.items() if k.startswith("accept")}}
 
 
 def head_eager(dev: Device, copies: int, reps: int = 40) -> dict:
-    """Eager launches of the in-path head (for rocprofv3 counter runs)."""
+    """Eager launches of the in-path head, nmx_head_keys (for rocprofv3 counter runs)."""
     s, n = QWEN35_08B, K_DRAFT + 1
     W = pqtool.gauss_q4k(7, 10_000, s.vocab, s.hidden, 0.02)
     heads = [dev.to_device(W) for _ in range(copies)]
@@ -135,11 +143,11 @@ def head_eager(dev: Device, copies: int, reps: int = 40) -> dict:
     fs = dev.empty((s.hidden // 32, n), np.float32)
     dev.quant_a8(X, n, s.hidden, q, d, fs)
     work = dev.alloc(dev.head_work_bytes(s.vocab, n))
-    out, drafts = dev.zeros(66, np.int32), dev.zeros(n - 1, np.int32)
+    dcopy, drafts = dev.zeros(16, np.int32), dev.zeros(n - 1, np.int32)
     e0, e1 = dev.event(), dev.event()
     dev.record(e0)
     for r in range(reps):
-        dev.head_accept(heads[r % copies], s.vocab, s.hidden, n, q, d, fs, None, drafts, work, out)
+        dev.head_keys(heads[r % copies], s.vocab, s.hidden, n, q, d, fs, drafts, work, dcopy)
     dev.record(e1)
     dev.sync()
     return {"us_per_call": round(dev.elapsed_ms(e0, e1) / reps * 1e3, 2), "timing": "eager"}

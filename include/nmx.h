@@ -149,6 +149,18 @@ int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int 
                            const int32_t *drafts, void *work, int32_t *out, int32_t *vt,
                            int32_t *ctl, int32_t *mailbox, int nvt);
 
+/* The head of nmx_head_accept_commit without its reduction launch: the dots and the
+ * per-workgroup partial argmax keys ([n][nmx_head_nkeys(rows, cols, n)] 64-bit keys in work,
+ * nmx_head_work_bytes(rows, n) bytes), and the drafts d1..d(n-1) copied to drafts_copy (n - 1
+ * int32, device). The argmax per row, the acceptance loop and the commit of the accepted run
+ * (engine/src/spec.c:340-351) then run in the consumer's workgroups: nmx_lin_commit_keys. The
+ * verify head of one round is thus one launch, and the reduction costs the commit no launch
+ * of its own. n <= 16. No logits. */
+int nmx_head_nkeys(int rows, int cols, int n);
+int nmx_head_keys(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                  const float *d, const float *fsum, const int32_t *drafts, void *work,
+                  int32_t *drafts_copy);
+
 /* nmx_head_accept without the workspace argument: allocates nothing and takes no workspace.
  * No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
@@ -425,6 +437,24 @@ typedef struct {
     int redo;              /* commit from state_bak instead of state */
 } nmx_commit_args;
 int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p);
+
+/* nmx_lin_commit with e from the verify head's partial keys instead of ctl[1]: every
+ * workgroup resolves the argmax of each of the n rows (n <= 16) from the nkeys keys per row
+ * that nmx_head_keys left and runs the acceptance loop over the drafts copy; the first
+ * workgroup then writes what nmx_head_accept_commit writes (out [2 + n], vt[a + 1] = bonus,
+ * ctl[1] = e = a + 1, the mailbox of nvt <= 64 tokens when not NULL) and cur (vt[0] = bonus),
+ * and the commit of e follows as in nmx_lin_commit. p->vt is required, p->redo must be 0.
+ * Results equal nmx_head_accept_commit + nmx_lin_commit (engine/src/spec.c:340-351,
+ * engine/src/forward_lin.c:185-204). */
+typedef struct {
+    const void *keys;       /* [n][nkeys] partial keys of nmx_head_keys */
+    int nkeys, n;
+    const int32_t *drafts;  /* nmx_head_keys' drafts_copy */
+    int32_t *out;           /* [2 + n] */
+    int32_t *mailbox;       /* optional, host memory */
+    int nvt;
+} nmx_accept_keys;
+int nmx_lin_commit_keys(nmx_ctx *ctx, const nmx_commit_args *p, const nmx_accept_keys *k);
 
 /* After nmx_head_accept: vt[a + 1] = bonus; ctl[1] = a + 1 (the reference's e without a stop,
  * engine/src/spec.c:346-349). */

@@ -1148,17 +1148,94 @@ struct Commit {
     int32_t *vt;                 /* optional: vt[0] = vt[ctl[1]] */
     float *bak;                  /* optional: [layers][S][C] state after token 0 */
     int redo;                    /* commit from bak (which the first commit filled) */
+    /* the acceptance from the head's partial keys (keys NULL: e = ctl[1] from the head's own
+     * reduction): n rows of nkeys keys, drafts d1..d(n-1) from the head launch's copy */
+    const unsigned long long *keys;
+    int nkeys, n;
+    const int32_t *drafts;
+    int32_t *out;                /* [2 + n]: a, bonus, argmax of each row */
+    int32_t *mb;                 /* optional host mailbox of nvt tokens */
+    int nvt;
 };
+
+constexpr int ACC_MAX_N = 16; /* rows of an acceptance resolved from keys */
+
+/* The verify's argmax per row from the head's partial keys, then the acceptance loop
+ * (engine/src/spec.c:340-345): a = 0; g = argmax(row 0); while a < n - 1 and drafts[a] == g:
+ * a++, g = argmax(row a). Every workgroup of the commit resolves it itself (the same keys, the
+ * same result); workgroup (0, 0) also writes what head_finish_k writes with a commit: out, vt[a
+ * + 1] = g, ctl[1] = e = a + 1, the mailbox [a, g, vt[0..nvt) after that update] and its flag
+ * (system-scope release), and cur: vt[0] = g. The drafts come from the head launch's copy, so
+ * that no workgroup reads a vt entry that workgroup (0, 0) writes. Returns a. */
+__device__ int accept_from_keys(const Commit &a, bool lead) {
+    __shared__ unsigned long long red[4][ACC_MAX_N];
+    __shared__ int am[ACC_MAX_N], s_dr[ACC_MAX_N], s_vt[64], s_a;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int dr = tid < a.n - 1 ? a.drafts[tid] : 0;
+    const int vv = lead && a.mb && tid < a.nvt ? a.vt[tid] : 0;
+    unsigned long long k[ACC_MAX_N];
+#pragma unroll
+    for (int v = 0; v < ACC_MAX_N; v++) k[v] = 0ull;
+    for (int b = tid; b < a.nkeys; b += 256) {
+#pragma unroll
+        for (int v = 0; v < ACC_MAX_N; v++)
+            if (v < a.n) {
+                const unsigned long long o = a.keys[(size_t)v * a.nkeys + b];
+                k[v] = o > k[v] ? o : k[v];
+            }
+    }
+    if (tid < a.n - 1) s_dr[tid] = dr;
+    if (lead && a.mb && tid < a.nvt) s_vt[tid] = vv;
+#pragma unroll
+    for (int v = 0; v < ACC_MAX_N; v++) {
+        if (v < a.n) { /* uniform */
+            const unsigned long long m = nmx_max_u64_wave(k[v]);
+            if (lane == 0) red[wv][v] = m;
+        }
+    }
+    __syncthreads();
+    if (tid < a.n) {
+        unsigned long long m = red[0][tid];
+        for (int w = 1; w < 4; w++) m = red[w][tid] > m ? red[w][tid] : m;
+        am[tid] = (int)(0xffffffffu - (unsigned)(m & 0xffffffffull));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0, g = am[0];
+        while (acc < a.n - 1 && s_dr[acc] == g) {
+            acc++;
+            g = am[acc];
+        }
+        s_a = acc;
+        if (lead) {
+            a.out[0] = acc;
+            a.out[1] = g;
+            for (int t = 0; t < a.n; t++) a.out[2 + t] = am[t];
+            a.vt[acc + 1] = g;
+            a.ctl[1] = acc + 1;
+            if (a.mb) {
+                a.mb[0] = acc;
+                a.mb[1] = g;
+                for (int i = 0; i < a.nvt; i++) a.mb[2 + i] = i == acc + 1 ? g : s_vt[i];
+                __hip_atomic_store(a.mb + 2 + a.nvt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            a.vt[0] = g; /* cur <- vt[e] */
+        }
+    }
+    __syncthreads();
+    return s_a;
+}
 
 __global__ __launch_bounds__(256) void commit_k(Commit a) {
     const int l = blockIdx.y;
-    const int E = a.ctl[1] - 1;
+    const bool lead = blockIdx.x == 0 && l == 0;
+    const int E = a.keys ? accept_from_keys(a, lead) : a.ctl[1] - 1;
     const int tid = blockIdx.x * 256 + threadIdx.x, stride = gridDim.x * 256;
     if (E == 0 && !a.redo) { /* e = 1: the state after token 0 is the committed one, no replay
                               * rows, and no later commit of a smaller e can need the kept rows */
         if (l == 0 && tid == 0) {
             a.ctl[2] = 0;
-            if (a.vt) a.vt[0] = a.vt[1];
+            if (a.vt && !a.keys) a.vt[0] = a.vt[1];
         }
         return;
     }
@@ -1189,7 +1266,7 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
     for (int i = tid; i < E * a.row; i += stride) pd[i] = lg[a.row + i];
     if (l == 0 && tid == 0) {
         a.ctl[2] = E;
-        if (a.vt) a.vt[0] = a.vt[E + 1]; /* cur <- vt[e] */
+        if (a.vt && !a.keys) a.vt[0] = a.vt[E + 1]; /* cur <- vt[e] */
     }
 }
 
@@ -1555,18 +1632,39 @@ size_t nmx_kv_bytes(int kv_dtype, int nkv, int max_ctx, int hd) {
     return rows * hd * es + (kv_dtype == KV_I8 ? rows * 4 : 0);
 }
 
-int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p) {
+static int lin_commit(nmx_ctx *ctx, const nmx_commit_args *p, const nmx_accept_keys *k) {
     if (!ctx) return -1;
     if (!p || p->layers < 1 || p->conv_k < 2 || p->conv_k > 8 || p->C < 1 || p->cap < 1 ||
         p->row < 1 || !p->state || !p->xin || !p->log || !p->pend || !p->ctl)
         return nmx_fail(ctx, "nmx_lin_commit: bad arguments");
     if (p->redo && !p->state_bak) return nmx_fail(ctx, "nmx_lin_commit: redo needs state_bak");
     Commit a{p->layers, p->C, p->conv_k - 1, p->state, p->xin, p->log, p->pend, p->cap, p->row,
-             p->ctl, p->vt, p->state_bak, p->redo};
+             p->ctl, p->vt, p->state_bak, p->redo, nullptr, 0, 0, nullptr, nullptr, nullptr, 0};
+    if (k) {
+        if (p->redo || !p->vt || !k->keys || !k->out || k->nkeys < 1 || k->n < 1 ||
+            k->n > ACC_MAX_N || (k->n > 1 && !k->drafts) || (uintptr_t)k->keys % 8 ||
+            k->n > p->cap || (k->mailbox && (k->nvt < k->n + 1 || k->nvt > 64)))
+            return nmx_fail(ctx, "nmx_lin_commit_keys: bad arguments (n=%d nkeys=%d)", k->n,
+                            k->nkeys);
+        a.keys = (const unsigned long long *)k->keys;
+        a.nkeys = k->nkeys;
+        a.n = k->n;
+        a.drafts = k->drafts;
+        a.out = k->out;
+        a.mb = k->mailbox;
+        a.nvt = k->mailbox ? k->nvt : 0;
+    }
     dim3 grid((unsigned)((p->C + 255) / 256), (unsigned)p->layers);
     commit_k<<<grid, 256, 0, ctx->stream>>>(a);
     NMX_LAUNCHED(ctx, "lin_commit");
     return 0;
+}
+
+int nmx_lin_commit(nmx_ctx *ctx, const nmx_commit_args *p) { return lin_commit(ctx, p, nullptr); }
+
+int nmx_lin_commit_keys(nmx_ctx *ctx, const nmx_commit_args *p, const nmx_accept_keys *k) {
+    if (!k) return ctx ? nmx_fail(ctx, "nmx_lin_commit_keys: NULL keys") : -1;
+    return lin_commit(ctx, p, k);
 }
 
 int nmx_accept_commit(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t *ctl) {

@@ -186,6 +186,10 @@ __global__ __launch_bounds__(256) void q4k_mv_k(SegTable tab, int cols, int n, i
     }
 }
 
+__global__ void copy_i32_k(const int32_t *__restrict__ src, int32_t *__restrict__ dst, int n) {
+    for (int t = threadIdx.x; t < n; t += 64) dst[t] = src[t];
+}
+
 /* Bytes i (the lane's row in its tile) of four dwords, gathered into one dword. */
 __device__ __forceinline__ uint32_t gather_byte4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
                                                  uint32_t sel) {
@@ -341,6 +345,158 @@ __global__ __launch_bounds__(64 * WPG) void q4k_mvx_k(SegTable tab, int cols, in
             for (int w = 1; w < WPG; w++) key = wkeys[w][threadIdx.x] > key ? wkeys[w][threadIdx.x] : key;
             amax_key[(size_t)(v0 + threadIdx.x) * gridDim.x + blockIdx.x] = key;
         }
+    }
+}
+
+/* The verify head (one matrix, cols = NSB x 256 known at compile time, 3..MAX_NV vectors): the
+ * dots and chains of q4k_mvx_k, with the weight loads kept in flight across the arithmetic.
+ * Superblock sb + 1's scale line is requested right after sb's scales are decoded, and its
+ * code chunk k right after block k of sb has been unpacked into MFMA operands (the registers
+ * are reused); every block's MFMA pair is issued one block ahead of the previous block's chain
+ * steps. Scheduling barriers keep each block's work together, so each in-order wait on the
+ * load counter names only what that block needs, and every wave has about one superblock of
+ * requests outstanding all the time instead of one superblock at a time. The activation
+ * table's sources are requested before the first weights and stored to LDS after them.
+ * Results equal q4k_mvx_k's bit for bit (same operations per (row, vector) chain, in order).
+ * Leading arguments are what the first requests need (preloaded into SGPRs). dcopy (not NULL):
+ * workgroup 0 copies drafts[0..ndr) there, so that a consumer that also rewrites the drafts'
+ * row (the accept commit writes the bonus to vt[a + 1]) reads them from a copy no workgroup of
+ * its own launch writes. */
+template <int NV, int NSB, int WPG, bool ONEPASS>
+__global__ __launch_bounds__(64 * WPG) void q4k_head_k(const uint8_t *__restrict__ W,
+                                                     const int8_t *__restrict__ q,
+                                                     const float *__restrict__ d,
+                                                     const float *__restrict__ fs,
+                                                     unsigned long long *__restrict__ amax_key,
+                                                     int rows, int n_arg, int v0_arg,
+                                                     float *__restrict__ Y,
+                                                     const int32_t *__restrict__ drafts,
+                                                     int32_t *__restrict__ dcopy, int ndr) {
+    /* ONEPASS (n == NV, v0 == 0): the activations' (d, fsum) offsets are compile-time
+     * constants, so each block's scalar loads are few wide ones instead of 2 NV computed ones */
+    const int n = ONEPASS ? NV : n_arg, v0 = ONEPASS ? 0 : v0_arg;
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    constexpr int NB = NSB * 8, ENT = NB * 2 * NV, TB = ENT * 16;
+    constexpr int TPT = (ENT + 64 * WPG - 1) / (64 * WPG);
+    __shared__ __align__(16) uint8_t xt[2 * TB + 16]; /* table, zero copy, one junk slot */
+    const int total_waves = (rows + 63) / 64;
+    const int wave_raw = blockIdx.x * WPG + (threadIdx.x >> 6);
+    const bool wave_live = wave_raw < total_waves; /* every wave reaches the barriers */
+    const int wave = wave_live ? wave_raw : total_waves - 1;
+    const int lane = threadIdx.x & 63;
+    const int row_raw = wave * 64 + lane;
+    const bool valid = wave_live && row_raw < rows;
+    const int row = row_raw < rows ? row_raw : rows - 1;
+    const uint32_t i = (uint32_t)(row & 3);
+    /* the activation table's sources: entry e = (block, half, vector), 16 bytes each */
+    uint2 ta[TPT], tb[TPT];
+#pragma unroll
+    for (int t = 0; t < TPT; t++) {
+        const int e = threadIdx.x + t * 64 * WPG;
+        const int ee = e < ENT ? e : ENT - 1;
+        const int v = ee % NV, bp = ee / NV, h = bp & 1, blk = bp >> 1;
+        const uint32_t *x = (const uint32_t *)(q + ((size_t)blk * n + v0 + v) * 32);
+        ta[t] = *(const uint2 *)(x + 2 * h);
+        tb[t] = *(const uint2 *)(x + 4 + 2 * h);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * NSB * SB_BYTES);
+    uint4 a0 = tp[0], a1 = tp[1], a2 = tp[2], a3 = tp[3], c[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) c[k] = tp[4 + 4 * k + i];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < TPT; t++) {
+        const int e = threadIdx.x + t * 64 * WPG;
+        const int o0 = e < ENT ? e * 16 : 2 * TB, o1 = e < ENT ? TB + e * 16 : 2 * TB;
+        *(uint4 *)(xt + o0) = make_uint4(ta[t].x, tb[t].x, ta[t].y, tb[t].y);
+        *(uint4 *)(xt + o1) = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const int m = lane & 31, vl = 4 * (m >> 3) + (m & 3);
+    const bool diag = ((m >> 2) & 1) == (lane >> 5) && vl < NV;
+    const uint8_t *xl = xt + (diag ? vl * 16 : TB);
+    const uint32_t sel = 0x0c0c0400u | i | (i << 8), sel2 = i | ((i + 4) << 8) | (i << 16) | ((i + 4) << 24);
+    const v16i zero = {};
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) acc[v] = 0.0f;
+    auto unpack = [](const uint4 w, v4i &b0, v4i &b1) {
+        b0 = v4i{(int)(w.x & 0x0f0f0f0fu), (int)((w.x >> 4) & 0x0f0f0f0fu),
+                 (int)(w.y & 0x0f0f0f0fu), (int)((w.y >> 4) & 0x0f0f0f0fu)};
+        b1 = v4i{(int)(w.z & 0x0f0f0f0fu), (int)((w.z >> 4) & 0x0f0f0f0fu),
+                 (int)(w.w & 0x0f0f0f0fu), (int)((w.w >> 4) & 0x0f0f0f0fu)};
+    };
+    v16i Cc; /* block 0's products, then always one block ahead of the chain */
+    {
+        v4i b0, b1;
+        unpack(c[0], b0, b1);
+        const v4i x0 = *(const v4i *)(xl), x1 = *(const v4i *)(xl + NV * 16);
+        Cc = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b0, zero, 0, 0, 0);
+        Cc = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b1, Cc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int sb = 0; sb < NSB; sb++) {
+        const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
+        const float D = half_bits_to_float(dw >> (16 * (i & 1)));
+        const float M = half_bits_to_float(mw >> (16 * (i & 1)));
+        uint32_t S03, S47, M03, M47;
+        decode6x4(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sel, sel2, S03, S47);
+        decode6x4(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sel, sel2, M03, M47);
+        const uint4 *p = tp + (sb + 1) * (SB_BYTES / 16);
+        __builtin_amdgcn_sched_barrier(0);
+        if (sb + 1 < NSB) { /* the next scale line and chunk 0 (block 0's unpack is done) */
+            a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+            c[0] = p[4 + i];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int blk = sb * 8 + k;
+            v16i Cn = Cc;
+            if (blk + 1 < NB) { /* the next block's products */
+                const int kn = (k + 1) & 7;
+                v4i b0, b1;
+                unpack(c[kn], b0, b1);
+                if (kn != 0 && sb + 1 < NSB) c[kn] = p[4 + 4 * kn + i];
+                int xo = (blk + 1) * 2 * NV * 16;
+                asm volatile("" : "+v"(xo) : "v"(Cc[0])); /* keeps the MFMAs in block order */
+                const v4i x0 = *(const v4i *)(xl + xo);
+                const v4i x1 = *(const v4i *)(xl + xo + NV * 16);
+                Cn = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b0, zero, 0, 0, 0);
+                Cn = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b1, Cn, 0, 0, 0);
+            }
+            const float sc = D * byte_f(k < 4 ? S03 : S47, k & 3); /* exact: 6-bit x 11-bit */
+            const float of = M * byte_f(k < 4 ? M03 : M47, k & 3);
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const size_t ai = (size_t)blk * n + v0 + v;
+                acc[v] = __builtin_fmaf((float)Cc[v], sc * d[ai], acc[v]);
+                acc[v] = __builtin_fmaf(-of, fs[ai], acc[v]);
+            }
+            Cc = Cn;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (valid && Y) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) Y[(size_t)(v0 + v) * rows + row] = acc[v];
+    }
+    if (dcopy && blockIdx.x == 0 && threadIdx.x < ndr) dcopy[threadIdx.x] = drafts[threadIdx.x];
+    __shared__ unsigned long long wkeys[WPG][MAX_NV];
+    const int wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const unsigned long long key = nmx_max_u64_wave(valid ? argmax_key(acc[v], row) : 0ull);
+        if (lane == 0) wkeys[wv][v] = key;
+    }
+    __syncthreads();
+    if (threadIdx.x < NV) {
+        unsigned long long key = wkeys[0][threadIdx.x];
+        for (int w = 1; w < WPG; w++) key = wkeys[w][threadIdx.x] > key ? wkeys[w][threadIdx.x] : key;
+        amax_key[(size_t)(v0 + threadIdx.x) * gridDim.x + blockIdx.x] = key;
     }
 }
 
@@ -827,9 +983,48 @@ int mv_wpg(const SegTable &tab, int n, int cols, bool dots) {
     return 16;
 }
 
+/* The drafts copy of a head launch (q4k_head_k's dcopy): src[0..n) -> dst, by workgroup 0. */
+struct HeadCopy {
+    const int32_t *src;
+    int32_t *dst;
+    int n;
+};
+
+template <int NV, int NSB, int WPG>
+void launch_head(hipStream_t st, unsigned blocks, const Seg &s, int n, int v0, const int8_t *q,
+                 const float *d, const float *fs, unsigned long long *am, const HeadCopy &hc) {
+    if (n == NV && v0 == 0)
+        q4k_head_k<NV, NSB, WPG, true><<<blocks, 64 * WPG, 0, st>>>(
+            (const uint8_t *)s.W, q, d, fs, am, s.rows, n, v0, s.Y, hc.src, hc.dst, hc.n);
+    else
+        q4k_head_k<NV, NSB, WPG, false><<<blocks, 64 * WPG, 0, st>>>(
+            (const uint8_t *)s.W, q, d, fs, am, s.rows, n, v0, s.Y, hc.src, hc.dst, hc.n);
+}
+
+/* q4k_head_k for one matrix with argmax keys at 1, 2, 4 or 8 superblocks per row; false when
+ * the shape is not one of those (q4k_mvx_k then, same results). */
 template <int NV>
-void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
-               const float *d, const float *fs, int32_t *dots, unsigned long long *am, int wpg) {
+bool try_head(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
+              const float *d, const float *fs, unsigned long long *am, int wpg, const HeadCopy &hc) {
+    if (tab.count != 1 || tab.s[0].ystride != tab.s[0].rows) return false;
+    const unsigned blocks = (unsigned)((tab.total_waves + wpg - 1) / wpg);
+    const Seg &s = tab.s[0];
+#define NMX_HEAD(NSB)                                                                             do {                                                                                              if (wpg == 16) launch_head<NV, NSB, 16>(st, blocks, s, n, v0, q, d, fs, am, hc);              else launch_head<NV, NSB, 4>(st, blocks, s, n, v0, q, d, fs, am, hc);                     } while (0)
+    switch (cols) {
+    case 256: NMX_HEAD(1); return true;
+    case 512: NMX_HEAD(2); return true;
+    case 1024: NMX_HEAD(4); return true;
+    case 2048: NMX_HEAD(8); return true;
+    default: return false;
+    }
+#undef NMX_HEAD
+}
+
+/* Returns true when q4k_head_k ran the pass (and with it the drafts copy of hc). */
+template <int NV>
+bool launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
+               const float *d, const float *fs, int32_t *dots, unsigned long long *am, int wpg,
+               const HeadCopy &hc) {
     const unsigned blocks = (unsigned)((tab.total_waves + wpg - 1) / wpg);
     /* 3 or more vectors: the block dots on the matrix cores (bit-identical results; measured at
      * 248320 x 1024, 5 vectors: 30 us against 34-38 us), while its activation table fits in
@@ -837,6 +1032,7 @@ void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, con
     if constexpr (NV >= 3) {
         const size_t xbytes = (size_t)2 * NV * cols;
         if (mvx_used(NV, cols, dots != nullptr)) {
+            if (am && try_head<NV>(st, tab, cols, n, v0, q, d, fs, am, wpg, hc)) return true;
             if (wpg == 16) {
                 if (am) q4k_mvx_k<NV, true, 16><<<blocks, 1024, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
                 else q4k_mvx_k<NV, false, 16><<<blocks, 1024, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
@@ -844,12 +1040,13 @@ void launch_nv(hipStream_t st, const SegTable &tab, int cols, int n, int v0, con
                 if (am) q4k_mvx_k<NV, true, 4><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
                 else q4k_mvx_k<NV, false, 4><<<blocks, 256, xbytes, st>>>(tab, cols, n, v0, q, d, fs, am);
             }
-            return;
+            return false;
         }
     }
     if (am) q4k_mv_k<NV, false, true><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
     else if (dots) q4k_mv_k<NV, true, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
     else q4k_mv_k<NV, false, false><<<blocks, 256, 0, st>>>(tab, cols, n, v0, q, d, fs, dots, am);
+    return false;
 }
 
 /* Rows below which the K-split kernel is used (few waves in the row-per-lane kernel). */
@@ -903,8 +1100,11 @@ int launch_mm(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *
     return 0;
 }
 
+/* copied (may be NULL): set to whether the first pass made hc's drafts copy. */
 int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8_t *q,
-                  const float *d, const float *fs, int32_t *dots, unsigned long long *am = nullptr) {
+                  const float *d, const float *fs, int32_t *dots, unsigned long long *am = nullptr,
+                  HeadCopy hc = HeadCopy{nullptr, nullptr, 0}, bool *copied = nullptr) {
+    if (copied) *copied = false;
     int total_rows = 0;
     for (int s = 0; s < tab.count; s++) total_rows += tab.s[s].rows;
     if (!am && !dots && n > MAX_NV) return launch_mm(ctx, tab, cols, n, q, d, fs);
@@ -922,17 +1122,20 @@ int launch_passes(nmx_ctx *ctx, const SegTable &tab, int cols, int n, const int8
     const int wpg = mv_wpg(tab, n, cols, dots != nullptr);
     for (int v = 0; v < n;) {
         const int nv = pass_nv(n - v);
+        bool head = false;
         switch (nv) {
-        case 8: launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        case 7: launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        case 6: launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        case 5: launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        case 4: launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        case 3: launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        case 2: launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
-        default: launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg); break;
+        case 8: head = launch_nv<8>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        case 7: head = launch_nv<7>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        case 6: head = launch_nv<6>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        case 5: head = launch_nv<5>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        case 4: head = launch_nv<4>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        case 3: head = launch_nv<3>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        case 2: head = launch_nv<2>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
+        default: head = launch_nv<1>(ctx->stream, tab, cols, n, v, q, d, fs, dots, am, wpg, hc); break;
         }
         NMX_LAUNCHED(ctx, "q4k_mv");
+        if (v == 0 && copied) *copied = head && hc.dst;
+        hc.dst = nullptr; /* the drafts are copied by the first pass */
         v += nv;
     }
     return 0;
@@ -1109,6 +1312,47 @@ static int head_accept(nmx_ctx *ctx, const void *W, int rows, int cols, int n, c
     if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, keys)) return -1;
     head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, n, drafts, out, tok_dst, fc);
     NMX_LAUNCHED(ctx, "head_finish");
+    return 0;
+}
+
+int nmx_head_nkeys(int rows, int cols, int n) {
+    if (rows <= 0 || cols <= 0 || n <= 0) return 0;
+    SegTable tab = {};
+    tab.count = 1;
+    tab.s[0] = Seg{nullptr, nullptr, rows, rows, 0, 0};
+    tab.total_waves = (rows + 63) / 64;
+    const int wpg = mv_wpg(tab, n, cols, false);
+    return (tab.total_waves + wpg - 1) / wpg;
+}
+
+int nmx_head_keys(nmx_ctx *ctx, const void *W, int rows, int cols, int n, const int8_t *q,
+                  const float *d, const float *fsum, const int32_t *drafts, void *work,
+                  int32_t *drafts_copy) {
+    if (!ctx) return -1;
+    if (!W || !q || !d || !fsum || !work || (n > 1 && (!drafts || !drafts_copy)))
+        return nmx_fail(ctx, "nmx_head_keys: NULL pointer");
+    if (rows <= 0 || rows % 4 || rows > (1 << 22) || cols <= 0 || cols % 256 || cols > 65536 ||
+        n < 1 || n > 16)
+        return nmx_fail(ctx, "nmx_head_keys: bad shape rows=%d cols=%d n=%d", rows, cols, n);
+    if ((uintptr_t)work % 8) return nmx_fail(ctx, "nmx_head_keys: work not 8-byte aligned");
+    const size_t wb = q4k_bytes(rows, cols), kb = nmx_head_work_bytes(rows, n);
+    if (nmx_overlap(work, kb, W, wb) || nmx_overlap(work, kb, q, (size_t)n * cols) ||
+        (n > 1 && (nmx_overlap(drafts_copy, (size_t)(n - 1) * 4, work, kb) ||
+                   nmx_overlap(drafts_copy, (size_t)(n - 1) * 4, drafts, (size_t)(n - 1) * 4))))
+        return nmx_fail(ctx, "nmx_head_keys: work or drafts_copy aliases another buffer");
+    SegTable tab = {};
+    tab.count = 1;
+    tab.s[0] = Seg{(const uint8_t *)W, nullptr, rows, rows, 0, 0};
+    tab.total_waves = (rows + 63) / 64;
+    bool copied = false;
+    const HeadCopy hc{drafts, n > 1 ? drafts_copy : nullptr, n - 1};
+    if (launch_passes(ctx, tab, cols, n, q, d, fsum, nullptr, (unsigned long long *)work, hc,
+                      &copied))
+        return -1;
+    if (n > 1 && !copied) { /* the first pass ran another kernel (1-2 vectors, other widths) */
+        copy_i32_k<<<1, 64, 0, ctx->stream>>>(drafts, drafts_copy, n - 1);
+        NMX_LAUNCHED(ctx, "copy_i32");
+    }
     return 0;
 }
 

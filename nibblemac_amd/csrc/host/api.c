@@ -133,6 +133,7 @@ static int alloc_state(pinfer_ctx *c) {
     c->tok = dalloc(c, B * 4, &ok);
     c->hout = dalloc(c, (2 + B) * 4, &ok);
     c->hout2 = dalloc(c, 4 * 4, &ok);
+    c->dcopy = dalloc(c, (E_MAX_K + 2) * 4, &ok);
     c->mbox = ok ? (int32_t *)nmx_host_alloc(c->dev, (2 + E_MAX_K + 2 + 1) * sizeof(int32_t)) : NULL;
     if (!c->mbox) ok = 0;
     c->hwork = dalloc(c, nmx_head_work_bytes(c->vocab, E_MAX_K + 1), &ok);

@@ -139,6 +139,7 @@ struct pinfer_ctx {
     int32_t *tok;             /* [E_MAX_BATCH] tokens of an eager forward */
     int32_t *hout;            /* [2 + E_MAX_BATCH] head output */
     int32_t *hout2;           /* [2 + 1] MTP head output */
+    int32_t *dcopy;           /* [E_MAX_K + 2] the verify head's copy of the drafts */
     int32_t *mbox;            /* host memory [2 + E_MAX_K + 2 + 1]: a verify round's (a, bonus, vt), flag */
     void *hwork;              /* head argmax scratch */
     float *logits;            /* [vocab] logits of one row when requested */

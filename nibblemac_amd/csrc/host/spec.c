@@ -58,27 +58,46 @@ static int draft_vocab(const pinfer_ctx *c, const pinfer_spec_params *sp) {
 static float *m_cur(pinfer_ctx *c) { return c->mbuf; }
 static float *m_ping(pinfer_ctx *c, int i) { return c->mbuf + (size_t)(1 + (i & 1)) * c->H; }
 
-/* The logged main pass over vt[0..ke] and the head with the acceptance of vt[1..ke]; the
- * result (a, bonus, vt) goes to the host mailbox, and ctl[1] = e = a + 1
- * (engine/src/spec.c:323-351). */
-static int seq_verify(pinfer_ctx *c, int ke, int keys_last) {
-    TRY(e_forward(c, c->vt, ke + 1, 1, keys_last));
-    e_scratch *sc = &c->s;
-    CK(nmx_head_accept_commit(c->dev, c->head.w, c->vocab, c->H, ke + 1, sc->a_h.q, sc->a_h.d,
-                              sc->a_h.fs, c->vt + 1, c->hwork, c->hout, c->vt, c->ctl, c->mbox,
-                              ke + 2));
-    return PINFER_OK;
-}
-
-/* The rollback commit of every linear layer for e = ctl[1], which also sets cur <- vt[e] (a
- * kernel of its own without linear layers); redo: from the conv rows the last commit kept,
- * leaving vt alone (engine/src/forward_lin.c:185-204). */
-static int commit_lin_cur(pinfer_ctx *c, int redo) {
+static nmx_commit_args commit_args(pinfer_ctx *c, int redo) {
     nmx_commit_args a = {c->n_lin, c->conv_dim, c->conv_k, c->conv_state, c->xin, c->log, c->pend,
                          c->cap, c->lv_heads * (c->lk_dim + c->lv_dim + 1), c->ctl,
                          redo ? NULL : c->vt, c->conv_bak, redo};
+    return a;
+}
+
+/* The logged main pass over vt[0..ke], the head with the acceptance of vt[1..ke] and the
+ * commit of e = a + 1 (engine/src/spec.c:323-351, engine/src/forward_lin.c:185-204): (a, bonus,
+ * vt) to the host mailbox, ctl[1] = e, cur <- vt[e], and the rollback commit of every linear
+ * layer. With linear layers the head leaves partial argmax keys and every workgroup of the
+ * commit resolves the acceptance itself (one launch fewer); without, the head's last kernel
+ * does, and a kernel of its own sets cur. */
+static int seq_verify_commit(pinfer_ctx *c, int ke, int keys_last) {
+    TRY(e_forward(c, c->vt, ke + 1, 1, keys_last));
+    e_scratch *sc = &c->s;
+    const int n = ke + 1;
+    if (c->n_lin && n <= 16) {
+        CK(nmx_head_keys(c->dev, c->head.w, c->vocab, c->H, n, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
+                         c->vt + 1, c->hwork, c->dcopy));
+        const nmx_commit_args a = commit_args(c, 0);
+        const nmx_accept_keys k = {c->hwork, nmx_head_nkeys(c->vocab, c->H, n), n, c->dcopy,
+                                   c->hout, c->mbox, ke + 2};
+        CK(nmx_lin_commit_keys(c->dev, &a, &k));
+        return PINFER_OK;
+    }
+    CK(nmx_head_accept_commit(c->dev, c->head.w, c->vocab, c->H, n, sc->a_h.q, sc->a_h.d,
+                              sc->a_h.fs, c->vt + 1, c->hwork, c->hout, c->vt, c->ctl, c->mbox,
+                              ke + 2));
+    const nmx_commit_args a = commit_args(c, 0);
     if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
-    else if (!redo) CK(nmx_copy_token(c->dev, c->vt, c->ctl));
+    else CK(nmx_copy_token(c->dev, c->vt, c->ctl));
+    return PINFER_OK;
+}
+
+/* The linear layers' commit redone for a smaller e = ctl[1] from the conv rows the round's
+ * commit kept, leaving vt alone (engine/src/forward_lin.c:185-204). */
+static int commit_lin_redo(pinfer_ctx *c) {
+    const nmx_commit_args a = commit_args(c, 1);
+    if (c->n_lin) CK(nmx_lin_commit(c->dev, &a));
     return PINFER_OK;
 }
 
@@ -95,8 +114,7 @@ static int seq_round(pinfer_ctx *c, int ke, int nv) {
         const int io = keys ? E_KEYS_OUT | (s > 1 ? E_KEYS_IN : 0) : 0;
         TRY(e_mtp_forward(c, h, c->vt + s, 1, s - 1, 0, nv, c->vt + s + 1, m_ping(c, s), 0, io));
     }
-    TRY(seq_verify(c, ke, keys && ke > 1 ? nmx_head_row_nkeys(nv) : 0));
-    TRY(commit_lin_cur(c, 0));
+    TRY(seq_verify_commit(c, ke, keys && ke > 1 ? nmx_head_row_nkeys(nv) : 0));
     TRY(e_mtp_forward(c, c->s.xn, c->vt + 1, ke + 1, 0, 1, nv, c->vt + 1, m_cur(c), 1, 0));
     return PINFER_OK;
 }
@@ -104,8 +122,7 @@ static int seq_round(pinfer_ctx *c, int ke, int nv) {
 /* One n-gram round (the host uploaded the drafts into vt[1..ke]): the verify, the commit,
  * n_past += e. The committed rows stay in s.xn for the host to queue for the MTP pass. */
 static int seq_round_ng(pinfer_ctx *c, int ke) {
-    TRY(seq_verify(c, ke, 0));
-    TRY(commit_lin_cur(c, 0));
+    TRY(seq_verify_commit(c, ke, 0));
     CK(nmx_ctl_advance(c->dev, c->ctl));
     return PINFER_OK;
 }
@@ -152,7 +169,7 @@ static int recommit(pinfer_ctx *c, int P, int e, int32_t cur, int e_device) {
     /* the device's commit of e = 1 keeps no conv rows (nmx_commit_args): a redo needs e >= 2 */
     if (e < 1 || e >= e_device || e_device < 2) return PINFER_E_ARG;
     CK(nmx_ctl_set(c->dev, c->ctl, 1, e));
-    TRY(commit_lin_cur(c, 1));
+    TRY(commit_lin_redo(c));
     CK(nmx_ctl_set(c->dev, c->ctl, 0, P + e));
     CK(nmx_upload(c->dev, c->vt, &cur, sizeof cur));
     return PINFER_OK;

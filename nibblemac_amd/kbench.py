@@ -68,6 +68,20 @@ def _copies(dev: Device, host: np.ndarray, total_min: int, at_least: int = 1):
     return [dev.to_device(host) for _ in range(n)]
 
 
+def _time_stream(dev: Device, launches, reps: int) -> float:
+    """ms per round of `launches` issued back to back on the stream (after one warm-up round),
+    between two HIP events on that stream."""
+    launches()
+    dev.sync()
+    e0, e1 = dev.event(), dev.event()
+    dev.record(e0)
+    for _ in range(reps):
+        launches()
+    dev.record(e1)
+    dev.sync()
+    return dev.elapsed_ms(e0, e1) / reps
+
+
 def _a8(dev: Device, rng, n: int, cols: int):
     X = dev.to_device(rng.standard_normal((n, cols)).astype(np.float32))
     q = dev.empty((cols // 32, n, 32), np.int8)
@@ -224,12 +238,17 @@ def config3_deltanet(dev: Device, n: int = 5, layers: int = 18, graphs: int = 20
 
 def config4_head(dev: Device, n: int = 5, copies: int = 4, reps_per_graph: int = 8,
                  graphs: int = 5) -> dict:
-    """Config 4: the LM head as the verify pass runs it (nmx_head_accept: the Q4K matvec
-    248320 x 1024 over k + 1 = 5 A8 rows with the fused argmax, q4k_mvx_k<5,true>, then
-    head_finish_k: the argmax reduction and the acceptance of the 4 drafts), over `copies`
-    rotating copies of the head (4 x 143 MB, so no launch finds it in the 256 MB MALL). The
-    acceptance rate is swept 0 / 50 / 100 % by planting drafts; the outputs are checked
-    against the planted answers."""
+    """Config 4: the LM head 248320 x 1024 over k + 1 = 5 A8 rows with the fused argmax and the
+    acceptance of the 4 drafts.
+
+    in_path_cold / in_path_warm: the head launch of the verify round (nmx_head_keys: the
+    matvec q4k_head_k<5,4,16>, leaving 243 partial argmax keys per row, whose reduction and
+    acceptance run inside the round's commit workgroups), over `copies` rotating copies of the
+    head (4 x 143 MB, so no launch finds it in the 256 MB MALL), and over one copy (resident in
+    the MALL after the first launch). accept<a>of4: the single-call API (nmx_head_accept: the
+    same matvec, then head_finish_k's reduction and acceptance), cold, with the acceptance rate
+    swept 0 / 50 / 100 % by planting drafts; the outputs are checked against the planted
+    answers, and the in-path keys against the same argmax."""
     s = QWEN35_08B
     rows, cols = s.vocab, s.hidden
     rng = np.random.default_rng(4)
@@ -261,6 +280,28 @@ def config4_head(dev: Device, n: int = 5, copies: int = 4, reps_per_graph: int =
         if int(got[0]) != a_plant or int(got[1]) != int(am[a_plant]):
             raise RuntimeError(f"head acceptance: planted a={a_plant}, got {got.tolist()}")
         res[f"accept{a_plant}of{n - 1}"] = _line(algo, us)
+    # the round's head launch: keys only, the drafts copied for the commit's acceptance
+    dcopy = dev.zeros(16, np.int32)
+    nk = dev.head_nkeys(rows, cols, n)
+    algo_k = matvec_algo_bytes(rows, cols, n, out=False) + 2 * 4 * (n - 1)
+    res["in_path_algorithmic_bytes"] = algo_k
+    res["in_path_kernel"] = f"q4k_head_k<{n},{cols // 256},16> (nmx_head_keys, {nk} keys per row)"
+    for name, ncp in (("in_path_cold", copies), ("in_path_warm", 1)):
+        def launches_k():
+            for r in range(reps_per_graph):
+                dev.head_keys(heads[r % ncp], rows, cols, n, q, d, fs, drafts, work, dcopy)
+
+        # back-to-back stream launches: the kernel's own duration (what a kernel trace
+        # reports), and graph replays: with the graph node's launch cost the round pays
+        us = _time_stream(dev, launches_k, graphs) / reps_per_graph * 1e3
+        usg = _time_graph(dev, launches_k, graphs) / reps_per_graph * 1e3
+        keys = dev.download(work, np.uint64, (n, nk))
+        top = keys.max(axis=1)
+        idx = (0xffffffff - (top & 0xffffffff)).astype(np.int64)
+        if not np.array_equal(idx, am):
+            raise RuntimeError(f"head keys: argmax {idx.tolist()} != {am.tolist()}")
+        res[name] = dict(_line(algo_k, us), us_graph_replay=round(usg, 3))
+    dcopy.free()
     for b in heads:
         b.free()
     work.free()

@@ -64,6 +64,21 @@ class LinMixArgs(ctypes.Structure):
                 ("a8", A8)]
 
 
+class CommitArgs(ctypes.Structure):
+    """Mirror of nmx_commit_args (the rollback commit of every linear layer)."""
+
+    _fields_ = [("layers", _i), ("C", _i), ("conv_k", _i), ("state", _vp), ("xin", _vp),
+                ("log", _vp), ("pend", _vp), ("cap", _i), ("row", _i), ("ctl", _vp), ("vt", _vp),
+                ("state_bak", _vp), ("redo", _i)]
+
+
+class AcceptKeys(ctypes.Structure):
+    """Mirror of nmx_accept_keys (the acceptance resolved from the head's partial keys)."""
+
+    _fields_ = [("keys", _vp), ("nkeys", _i), ("n", _i), ("drafts", _vp), ("out", _vp),
+                ("mailbox", _vp), ("nvt", _i)]
+
+
 class AttnArgs(ctypes.Structure):
     """Mirror of nmx_attn_args (gated full attention over the KV caches)."""
 
@@ -110,6 +125,10 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_head_accept_commit": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _i]),
     "nmx_accept_commit": (_i, [_vp, _vp, _vp, _vp]),
+    "nmx_head_nkeys": (_i, [_i, _i, _i]),
+    "nmx_head_keys": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nmx_lin_commit": (_i, [_vp, ctypes.POINTER(CommitArgs)]),
+    "nmx_lin_commit_keys": (_i, [_vp, ctypes.POINTER(CommitArgs), ctypes.POINTER(AcceptKeys)]),
     "nmx_accept_commit_mb": (_i, [_vp, _vp, _vp, _vp, _vp, _i]),
     "nmx_host_alloc": (_vp, [_vp, _sz]),
     "nmx_embed_norm": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp, _vp, _i, _vp, _i, A8,
@@ -477,6 +496,24 @@ class Device:
         self.check(self.lib.nmx_head_accept_commit(self.ctx, _p(W), rows, cols, n, _p(q), _p(d),
                                                    _p(fs), _p(drafts), _p(work), _p(out), _p(vt),
                                                    _p(ctl), mailbox, nvt), "head_accept_commit")
+
+    def head_nkeys(self, rows: int, cols: int, n: int) -> int:
+        """nmx_head_nkeys: partial argmax keys per row of nmx_head_keys."""
+        return int(self.lib.nmx_head_nkeys(rows, cols, n))
+
+    def head_keys(self, W, rows: int, cols: int, n: int, q, d, fs, drafts, work,
+                  drafts_copy) -> None:
+        """nmx_head_keys: the verify head's dots and partial argmax keys, drafts copied."""
+        self.check(self.lib.nmx_head_keys(self.ctx, _p(W), rows, cols, n, _p(q), _p(d), _p(fs),
+                                          _p(drafts), _p(work), _p(drafts_copy)), "head_keys")
+
+    def lin_commit(self, args: CommitArgs, keys: AcceptKeys | None = None) -> None:
+        """nmx_lin_commit, or nmx_lin_commit_keys with the acceptance from keys."""
+        if keys is None:
+            rc = self.lib.nmx_lin_commit(self.ctx, ctypes.byref(args))
+        else:
+            rc = self.lib.nmx_lin_commit_keys(self.ctx, ctypes.byref(args), ctypes.byref(keys))
+        self.check(rc, "lin_commit")
 
     def accept_commit(self, out, vt, ctl, mailbox=None, nvt: int = 0) -> None:
         """nmx_accept_commit, or nmx_accept_commit_mb writing the host mailbox."""

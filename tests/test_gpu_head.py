@@ -241,6 +241,80 @@ def test_head_accept_commit_equals_two_launches(dev, accept, mailbox):
         assert m0 == m1 and m1[-1] == 1 and m1[:2] == [accept, bonus_ref]
 
 
+@pytest.mark.parametrize("rows,k,accept", [(248320, 4, 0), (248320, 4, 2), (248320, 4, 4),
+                                            (32768, 4, 3), (32768, 8, 5), (32768, 1, 1)])
+def test_head_keys_commit_equals_head_accept_commit(dev, rows, k, accept):
+    """The round's verify tail with the reduction inside the commit (nmx_head_keys, then
+    nmx_lin_commit_keys: every commit workgroup resolves the argmax keys and the acceptance)
+    against nmx_head_accept_commit + nmx_lin_commit on the same inputs: out, vt, ctl, the
+    mailbox, the conv state, its backup and the pending rows identical; a and the bonus equal
+    the oracle's. The drafts are vt[1..k], as in the verify round."""
+    import ctypes
+
+    from nibblemac_amd.nmx import AcceptKeys, CommitArgs
+
+    print(f"[case] head_keys commit rows={rows} k={k} accept={accept}", flush=True)
+    rng = np.random.default_rng(90 + rows % 7 + k + accept)
+    cols, n = 1024, k + 1
+    W = quantized_head(rng, rows, cols)
+    X = rng.standard_normal((n, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, n, threads=8)
+    am = np.array([oracle.argmax(ref[t]) for t in range(n)], np.int32)
+    vt0 = np.concatenate([[12345], planted_drafts(am, accept, k)]).astype(np.int32)
+    layers, C, conv_k, cap, row = 3, 640, 4, 9, 2 * (16 + 16 + 1)
+    st0 = rng.standard_normal((layers, conv_k - 1, C)).astype(np.float32)
+    xin0 = rng.standard_normal((layers, cap, C)).astype(np.float32)
+    log0 = rng.standard_normal((layers, cap, row)).astype(np.float32)
+    dW, dq, dd, dfs = dev.to_device(W), dev.to_device(q), dev.to_device(d), dev.to_device(fs)
+    dxin, dlog = dev.to_device(xin0), dev.to_device(log0)
+    nvt = k + 2
+    got = []
+    for fused in (False, True):
+        vt = dev.to_device(np.concatenate([vt0, [-1]]).astype(np.int32))
+        ctl = dev.to_device(np.full(16, 9, np.int32))
+        work = dev.zeros(dev.head_work_bytes(rows, n), np.uint8)
+        dcopy = dev.zeros(16, np.int32)
+        out = dev.zeros(2 + n, np.int32)
+        state, bak = dev.to_device(st0), dev.zeros(st0.shape, np.float32)
+        pend = dev.zeros((layers, cap, row), np.float32)
+        mb = dev.host_alloc((3 + nvt) * 4)
+        try:
+            view = (ctypes.c_int32 * (3 + nvt)).from_address(mb)
+            for i in range(3 + nvt):
+                view[i] = -7
+            view[2 + nvt] = 0
+            args = CommitArgs(layers, C, conv_k, state.ptr, dxin.ptr, dlog.ptr, pend.ptr, cap, row,
+                              ctl.ptr, vt.ptr, bak.ptr, 0)
+            if fused:
+                dev.head_keys(dW, rows, cols, n, dq, dd, dfs, vt.ptr + 4, work, dcopy)
+                keys = AcceptKeys(work.ptr, dev.head_nkeys(rows, cols, n), n, dcopy.ptr, out.ptr,
+                                  mb, nvt)
+                dev.lin_commit(args, keys)
+            else:
+                dev.head_accept_commit(dW, rows, cols, n, dq, dd, dfs, vt.ptr + 4, work, out, vt,
+                                       ctl, mailbox=mb, nvt=nvt)
+                dev.lin_commit(args)
+            dev.sync()
+            got.append((out.numpy(), vt.numpy(), ctl.numpy(), list(view), state.numpy(),
+                        bak.numpy(), pend.numpy()))
+        finally:
+            dev.host_free(mb)
+            for b in (vt, ctl, work, dcopy, out, state, bak, pend):
+                b.free()
+    for b in (dW, dq, dd, dfs, dxin, dlog):
+        b.free()
+    a_ref, bonus_ref, _ = oracle.accept(ref, vt0[1:])
+    assert a_ref == accept
+    two, one = got
+    for name, x, y in zip(("out", "vt", "ctl", "mailbox", "state", "bak", "pend"), two, one):
+        assert np.array_equal(np.asarray(x), np.asarray(y)), name
+    o, v, c, m = one[:4]
+    assert o[0] == accept and o[1] == bonus_ref and list(o[2:]) == list(am)
+    assert v[accept + 1] == bonus_ref and v[0] == bonus_ref and c[1] == accept + 1
+    assert c[2] == accept and m[:2] == [accept, bonus_ref] and m[-1] == 1
+
+
 def test_head_accept_to_writes_token(dev):
     """nmx_head_accept_to stores out[1] (the greedy token) at tok_dst as well."""
     rng = np.random.default_rng(5)
