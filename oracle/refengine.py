@@ -20,6 +20,9 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 REFQ4K = HERE / "_ref" / "libpinfer_refq4k.so"
+# the same engine with the DeltaNet gates on the host's glibc expf / log1pf (the reference's
+# own build), for the pin of the gates' libm
+REFQ4K_GLIBC = HERE / "_ref" / "libpinfer_refq4k_glibc.so"
 
 
 class _Params(ctypes.Structure):
@@ -55,12 +58,13 @@ class RefRun:
     prefill_s: float
     decode_s: float
     state: bytes | None
+    next_logits: np.ndarray | None = None
 
 
-def _lib() -> ctypes.CDLL:
-    if not REFQ4K.exists():
-        raise FileNotFoundError(f"{REFQ4K} not built (make -C oracle ref)")
-    L = ctypes.CDLL(str(REFQ4K))
+def _lib(path: Path = REFQ4K) -> ctypes.CDLL:
+    if not path.exists():
+        raise FileNotFoundError(f"{path} not built (make -C oracle ref)")
+    L = ctypes.CDLL(str(path))
     vp, i = ctypes.c_void_p, ctypes.c_int
     L.pinfer_default_params.restype = _Params
     L.pinfer_load.restype, L.pinfer_load.argtypes = vp, [ctypes.c_char_p, vp, vp]
@@ -69,14 +73,18 @@ def _lib() -> ctypes.CDLL:
     L.pf_spec_decode.restype, L.pf_spec_decode.argtypes = i, [vp] * 8
     L.pinfer_state_size.restype, L.pinfer_state_size.argtypes = ctypes.c_size_t, [vp]
     L.pinfer_state_save.restype, L.pinfer_state_save.argtypes = i, [vp, vp, ctypes.c_size_t]
+    L.pinfer_eval.restype, L.pinfer_eval.argtypes = i, [vp, vp, i, vp]
+    L.pinfer_n_vocab.restype, L.pinfer_n_vocab.argtypes = i, [vp]
     return L
 
 
 def bench_generate(path: str | Path, prompt: np.ndarray, n_gen: int, k: int, draft_vocab: int,
-                   threads: int, max_ctx: int = 1024, want_state: bool = False) -> RefRun:
+                   threads: int, max_ctx: int = 1024, want_state: bool = False,
+                   lib: Path = REFQ4K, next_logits: bool = False) -> RefRun:
     """Prefill `prompt`, then exactly n_gen tokens at draft count k (EOS ignored) on `threads`
-    host threads; with want_state, the state blob (pinfer_state_save) after the decode."""
-    L = _lib()
+    host threads; with want_state, the state blob (pinfer_state_save) after the decode; with
+    next_logits, then the logits of feeding the last generated token (pinfer_eval)."""
+    L = _lib(lib)
     p = L.pinfer_default_params()
     p.max_ctx, p.n_threads = max_ctx, threads
     err = ctypes.c_int(0)
@@ -105,7 +113,13 @@ def bench_generate(path: str | Path, prompt: np.ndarray, n_gen: int, k: int, dra
             if L.pinfer_state_save(ctx, buf, size) != 0:
                 raise RuntimeError("reference pinfer_state_save failed")
             blob = buf.raw
+        logits = None
+        if next_logits:
+            logits = np.zeros(L.pinfer_n_vocab(ctx), np.float32)
+            last = np.array([out[-1]], np.int32)
+            if L.pinfer_eval(ctx, last.ctypes.data, 1, logits.ctypes.data) != 0:
+                raise RuntimeError("reference pinfer_eval failed")
         return RefRun([int(x) for x in out], st.rounds, st.drafted, st.accepted, t1 - t0,
-                      t2 - t1, blob)
+                      t2 - t1, blob, logits)
     finally:
         L.pinfer_free(ctx)
