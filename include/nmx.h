@@ -149,6 +149,15 @@ int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int 
                            const int32_t *drafts, void *work, int32_t *out, int32_t *vt,
                            int32_t *ctl, int32_t *mailbox, int nvt);
 
+/* The head of a plain greedy step (engine/src/spec.c:238-262) on the one A8 row q / d / fsum:
+ * its argmax g to vt[0] (the next step's input token) and to vt[1], ctl[1] = 1, ctl[0] += 1
+ * (n_past advanced by the step) and, when mailbox is not NULL, the host mailbox [0, g, vt[0..nvt)
+ * as nmx_head_accept_commit writes it] and its flag, all in the head's last kernel: a captured
+ * step needs no host read of the token and no position upload. out [3] as nmx_head_accept. */
+int nmx_head_step(nmx_ctx *ctx, const void *W, int rows, int cols, const int8_t *q,
+                  const float *d, const float *fsum, void *work, int32_t *out, int32_t *vt,
+                  int32_t *ctl, int32_t *mailbox, int nvt);
+
 /* The head of nmx_head_accept_commit without its reduction launch: the dots and the
  * per-workgroup partial argmax keys ([n][nmx_head_nkeys(rows, cols, n)] 64-bit keys in work,
  * nmx_head_work_bytes(rows, n) bytes), and the drafts d1..d(n-1) copied to drafts_copy (n - 1
@@ -415,6 +424,12 @@ int nmx_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p);
  * top1_prob). One workgroup; the decision is exact (an fp64 sum decides unless p is within the
  * fp32 sum's error bound of tau, where the ordered fp32 sum itself is formed). */
 int nmx_top1_gate(nmx_ctx *ctx, const float *logits, int n, float tau, int32_t *flag);
+
+/* The DeltaNet gates' exp (which = 0) and log1p (1) as the mixer kernels evaluate them, for
+ * the n binary32 inputs with bit patterns first .. first + n - 1 into y (device): a probe for
+ * parity tests of the device against the host C library the reference calls
+ * (engine/src/forward_lin.c:18-19,59-66). No reference counterpart of its own. */
+int nmx_gate_eval(nmx_ctx *ctx, int which, uint32_t first, long n, float *y);
 
 /* Rollback commit of every linear layer (pf_lin_commit, engine/src/forward_lin.c:185-204)
  * with e = ctl[1]: conv state <- last conv_k - 1 rows of [state after token 0, raw inputs

@@ -1286,6 +1286,16 @@ __global__ void accept_commit_k(const int32_t *out, int32_t *vt, int32_t *ctl, i
     }
 }
 
+/* y[i] = gate (0: nmx_gate_expf, 1: nmx_gate_log1pf) of the binary32 input with bit pattern
+ * first + i */
+__global__ __launch_bounds__(256) void gate_eval_k(int which, uint32_t first, long n,
+                                                   float *__restrict__ y) {
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const float x = __uint_as_float(first + (uint32_t)i);
+        y[i] = which ? nmx_gate_log1pf(x) : nmx_gate_expf(x);
+    }
+}
+
 __global__ void ctl_k(int32_t *ctl, int op, int idx, int value) {
     if (op == 0) ctl[idx] = value;          /* set */
     else ctl[0] = ctl[0] + ctl[1];          /* advance n_past by e */
@@ -1682,6 +1692,15 @@ int nmx_accept_commit_mb(nmx_ctx *ctx, const int32_t *out, int32_t *vt, int32_t 
         return nmx_fail(ctx, "nmx_accept_commit_mb: bad arguments");
     accept_commit_k<<<1, 1, 0, ctx->stream>>>(out, vt, ctl, mailbox, nvt);
     NMX_LAUNCHED(ctx, "accept_commit");
+    return 0;
+}
+
+int nmx_gate_eval(nmx_ctx *ctx, int which, uint32_t first, long n, float *y) {
+    if (!ctx) return -1;
+    if ((which != 0 && which != 1) || n < 1 || !y || (uint64_t)first + (uint64_t)n > (1ull << 32))
+        return nmx_fail(ctx, "nmx_gate_eval: bad arguments");
+    gate_eval_k<<<2048, 256, 0, ctx->stream>>>(which, first, n, y);
+    NMX_LAUNCHED(ctx, "gate_eval");
     return 0;
 }
 

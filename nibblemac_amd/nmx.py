@@ -126,6 +126,7 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
                                     _vp, _vp, _i]),
     "nmx_accept_commit": (_i, [_vp, _vp, _vp, _vp]),
     "nmx_head_nkeys": (_i, [_i, _i, _i]),
+    "nmx_gate_eval": (_i, [_vp, _i, ctypes.c_uint32, ctypes.c_long, _vp]),
     "nmx_head_keys": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_lin_commit": (_i, [_vp, ctypes.POINTER(CommitArgs)]),
     "nmx_lin_commit_keys": (_i, [_vp, ctypes.POINTER(CommitArgs), ctypes.POINTER(AcceptKeys)]),
@@ -496,6 +497,10 @@ class Device:
         self.check(self.lib.nmx_head_accept_commit(self.ctx, _p(W), rows, cols, n, _p(q), _p(d),
                                                    _p(fs), _p(drafts), _p(work), _p(out), _p(vt),
                                                    _p(ctl), mailbox, nvt), "head_accept_commit")
+
+    def gate_eval(self, which: int, first: int, n: int, y) -> None:
+        """nmx_gate_eval: the device's gate exp (0) / log1p (1) of n consecutive bit patterns."""
+        self.check(self.lib.nmx_gate_eval(self.ctx, which, first, n, _p(y)), "gate_eval")
 
     def head_nkeys(self, rows: int, cols: int, n: int) -> int:
         """nmx_head_nkeys: partial argmax keys per row of nmx_head_keys."""

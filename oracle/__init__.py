@@ -56,6 +56,9 @@ _SIGS = {
     "orc_top1_prob": (_f, [_vp, _i]),
     "orc_gate_expf": (_f, [_f]),
     "orc_gate_log1pf": (_f, [_f]),
+    "orc_libm_mismatches": (ctypes.c_longlong, [_i, _i]),
+    "orc_libm_eval": (None, [_i, ctypes.c_uint32, ctypes.c_long, _vp, _i]),
+    "orc_exp2_tab": (ctypes.c_uint64, [_i]),
 }
 
 _lib = None

@@ -97,11 +97,18 @@ float orc_expf_cephes(float x); /* pf_expf, forward_ops.c:41-56 */
  * pf_softmax_exp, forward_ops.c:294-353): p = s > 0 ? 1 / s : 0 */
 float orc_top1_prob(const float *l, int n);
 
-/* exp / log1p for the DeltaNet gates: evaluated in binary64 and rounded once to binary32.
- * The reference calls glibc expf / log1pf (forward_lin.c:18-19,59-66); these stand in for
- * them on both the CPU oracle and the GPU (same source, tests compare with glibc). */
+/* exp / log1p for the DeltaNet gates: the reference calls libm expf / log1pf
+ * (forward_lin.c:18-19,59-66); these restate this platform's (glibc 2.35 on x86-64: Arm's
+ * optimized-routines expf as glibc's FMA build runs it, fdlibm's log1pf) operation for
+ * operation. orc_libm_mismatches counts the inputs on which they differ from the host's
+ * functions over all 2^32 bit patterns (which: 0 expf, 1 log1pf); orc_libm_eval writes the
+ * host's values for the inputs with bit patterns first .. first + n - 1 (threads threads);
+ * orc_exp2_tab is entry i of expf's 2^(i/32) table. */
 float orc_gate_expf(float x);
 float orc_gate_log1pf(float x);
+long long orc_libm_mismatches(int which, int threads);
+void orc_libm_eval(int which, uint32_t first, long n, float *y, int threads);
+uint64_t orc_exp2_tab(int i);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,6 @@
 /* ORACLE — test infrastructure only (see oracle.h). Scalar numeric primitives. */
 #include <math.h>
+#include <pthread.h>
 #include <string.h>
 
 #include "oracle.h"
@@ -115,88 +116,212 @@ float orc_top1_prob(const float *l, int n) {
     return s > 0.0f ? 1.0f / s : 0.0f;
 }
 
-/* ---- gate exp / log1p: binary64 evaluation, one rounding to binary32 -------------------
- * exp: Cody-Waite reduction x = k ln2 + r (ln2 split so k * LN2_HI is exact for |k| < 2^20),
- * |r| <= ln2/2, Taylor polynomial of degree 13 in Horner form (truncation < 2e-17), then the
- * power of two assembled in the exponent field. log1p: 1 + y is exact in binary64 for binary32
- * y >= 1e-4 in magnitude; log(m 2^e) = e ln2 + 2 atanh(s), s = (m-1)/(m+1), m in
- * [sqrt(1/2), sqrt(2)), atanh series to s^25 (Abramowitz & Stegun 4.1.28 form). Small |y| use
- * the log1p series to y^6. The error of the binary64 value is a few units of 2^-53, so the
- * final rounding to binary32 is the correctly rounded result except within ~1e-16 of a
- * rounding midpoint. */
-#define G_LN2_HI 6.93147180369123816490e-01 /* 0x3fe62e42fee00000 */
-#define G_LN2_LO 1.90821492927058770002e-10 /* 0x3dea39ef35793c76 */
-#define G_INV_LN2 1.44269504088896338700e+00
+/* ---- gate exp / log1p: the host C library's, operation for operation ------------------
+ * The reference computes the DeltaNet gates with libm expf / log1pf (forward_lin.c:18-19,
+ * 59-66). On this platform (x86-64, glibc 2.35) those are:
+ *   expf: the table method of Arm's optimized-routines (Szabolcs Nagy), which glibc adopted:
+ *     z = x N / ln2 (N = 32) split as k + r by adding and subtracting 1.5 * 2^52 (round to
+ *     nearest even), 2^(k/N) from a 32-entry table of 2^(i/32) (bit pattern minus i << 47, so
+ *     that adding k << 47 supplies the exponent), 2^(r/N) by a cubic, all in binary64; glibc
+ *     selects its FMA build on this hardware, so z + shift, z - kd and the cubic's three
+ *     multiply-adds are fused (the multiplication x N / ln2 fused into both of its uses);
+ *   log1pf: Sun's fdlibm s_log1pf.c, in binary32 without fused operations: 1 + x split into
+ *     2^k (1 + f) with a correction term c for the rounding of 1 + x, log(1 + f) = f - hfsq +
+ *     s (hfsq + R) with s = f / (2 + f) and R a degree-7 polynomial in s^2, k ln2 in two
+ *     parts.
+ * Both are checked against the host's expf / log1pf over every binary32 input (0 differences;
+ * orc_libm_mismatches). */
+static uint64_t g_exp2_tab[32]; /* bits of 2^(i/32) minus i << 47 */
+static pthread_once_t g_exp2_once = PTHREAD_ONCE_INIT;
 
-static double pow2i(int k) { /* 2^k for -1022 <= k <= 1023 */
-    const uint64_t bits = (uint64_t)(k + 1023) << 52;
-    double d;
-    memcpy(&d, &bits, 8);
-    return d;
-}
-
-float orc_gate_expf(float xf) {
-    if (xf != xf) return xf;
-    if (xf > 89.0f) return INFINITY;
-    if (xf < -104.0f) return 0.0f;
-    const double x = (double)xf;
-    const double k = rint(x * G_INV_LN2);
-    double r = x - k * G_LN2_HI;
-    r = r - k * G_LN2_LO;
-    double p = 1.0 / 6227020800.0;       /* 1/13! */
-    p = p * r + 1.0 / 479001600.0;       /* 1/12! */
-    p = p * r + 1.0 / 39916800.0;        /* 1/11! */
-    p = p * r + 1.0 / 3628800.0;         /* 1/10! */
-    p = p * r + 1.0 / 362880.0;          /* 1/9! */
-    p = p * r + 1.0 / 40320.0;           /* 1/8! */
-    p = p * r + 1.0 / 5040.0;            /* 1/7! */
-    p = p * r + 1.0 / 720.0;             /* 1/6! */
-    p = p * r + 1.0 / 120.0;             /* 1/5! */
-    p = p * r + 1.0 / 24.0;              /* 1/4! */
-    p = p * r + 1.0 / 6.0;               /* 1/3! */
-    p = p * r + 0.5;                     /* 1/2! */
-    p = p * r + 1.0;
-    p = p * r + 1.0;
-    return (float)(p * pow2i((int)k));
-}
-
-float orc_gate_log1pf(float yf) {
-    if (yf != yf) return yf;
-    if (yf <= -1.0f) return yf == -1.0f ? -INFINITY : NAN;
-    if (yf == INFINITY) return yf;
-    const double y = (double)yf;
-    if (fabs(y) < 1e-4) {
-        double p = -1.0 / 6.0;
-        p = p * y + 1.0 / 5.0;
-        p = p * y - 1.0 / 4.0;
-        p = p * y + 1.0 / 3.0;
-        p = p * y - 1.0 / 2.0;
-        p = p * y + 1.0;
-        return (float)(p * y);
+static void exp2_tab_init(void) {
+    for (int i = 0; i < 32; i++) {
+        /* 2^(i/32) rounded to binary64: the 64-bit-mantissa value is within 2^-64 relative
+         * and no entry lies that close to a binary64 rounding midpoint (checked in tests) */
+        const double v = (double)exp2l((long double)i / 32.0L);
+        uint64_t b;
+        memcpy(&b, &v, 8);
+        g_exp2_tab[i] = b - ((uint64_t)i << 47);
     }
-    const double u = 1.0 + y; /* exact */
-    uint64_t bits;
-    memcpy(&bits, &u, 8);
-    int e = (int)((bits >> 52) & 0x7ff) - 1023;
-    bits = (bits & 0x000fffffffffffffull) | 0x3ff0000000000000ull; /* m in [1, 2) */
-    double m;
-    memcpy(&m, &bits, 8);
-    if (m > 1.41421356237309504880) { m = m * 0.5; e += 1; }
-    const double s = (m - 1.0) / (m + 1.0), s2 = s * s;
-    double t = 1.0 / 25.0;
-    t = t * s2 + 1.0 / 23.0;
-    t = t * s2 + 1.0 / 21.0;
-    t = t * s2 + 1.0 / 19.0;
-    t = t * s2 + 1.0 / 17.0;
-    t = t * s2 + 1.0 / 15.0;
-    t = t * s2 + 1.0 / 13.0;
-    t = t * s2 + 1.0 / 11.0;
-    t = t * s2 + 1.0 / 9.0;
-    t = t * s2 + 1.0 / 7.0;
-    t = t * s2 + 1.0 / 5.0;
-    t = t * s2 + 1.0 / 3.0;
-    t = t * s2 + 1.0;
-    const double logm = 2.0 * s * t;
-    const double de = (double)e;
-    return (float)((de * G_LN2_HI + logm) + de * G_LN2_LO);
+}
+
+uint64_t orc_exp2_tab(int i) {
+    pthread_once(&g_exp2_once, exp2_tab_init);
+    return g_exp2_tab[i & 31];
+}
+
+static uint32_t f2u(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+static float u2f(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float orc_gate_expf(float x) {
+    static const double inv_ln2_n = 0x1.71547652b82fep+5, shift = 0x1.8p+52;
+    static const double c0 = 0x1.c6af84b912394p-20, c1 = 0x1.ebfce50fac4f3p-13,
+                        c2 = 0x1.62e42ff0c52d6p-6;
+    pthread_once(&g_exp2_once, exp2_tab_init);
+    const uint32_t top = (f2u(x) >> 20) & 0x7ff;
+    if (top >= (f2u(88.0f) >> 20)) { /* |x| >= 88, inf or nan */
+        if (f2u(x) == f2u(-INFINITY)) return 0.0f;
+        if (top >= (f2u(INFINITY) >> 20)) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;   /* overflow */
+        if (x < -0x1.9fe368p6f) return 0.0f;      /* underflow */
+    }
+    const double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = g_exp2_tab[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double z = fma(c0, r, c1), r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
+}
+
+float orc_gate_log1pf(float x) {
+    static const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
+    static const float lp1 = 6.6666668653e-01f, lp2 = 4.0000000596e-01f,
+                       lp3 = 2.8571429849e-01f, lp4 = 2.2222198546e-01f,
+                       lp5 = 1.8183572590e-01f, lp6 = 1.5313838422e-01f,
+                       lp7 = 1.4798198640e-01f;
+    const int32_t hx = (int32_t)f2u(x), ax = hx & 0x7fffffff;
+    int32_t k = 1, hu = 0;
+    float f = 0.0f, c = 0.0f;
+    if (hx < 0x3ed413d7) {                     /* x < 0.41422 */
+        if (ax >= 0x3f800000) return x == -1.0f ? -INFINITY : NAN; /* x <= -1 */
+        if (ax < 0x31000000) {                 /* |x| < 2^-29 */
+            if (ax < 0x24800000) return x;     /* |x| < 2^-54 */
+            return x - x * x * 0.5f;
+        }
+        if (hx > 0 || hx <= (int32_t)0xbe95f61f) { /* -0.2929 < x < 0.41422 */
+            k = 0;
+            f = x;
+            hu = 1;
+        }
+    } else if (hx >= 0x7f800000) {
+        return x + x;
+    }
+    if (k != 0) {
+        float u;
+        if (hx < 0x5a000000) {
+            u = 1.0f + x;
+            hu = (int32_t)f2u(u);
+            k = (hu >> 23) - 127;
+            c = k > 0 ? 1.0f - (u - x) : x - (u - 1.0f); /* the rounding error of 1 + x */
+            c /= u;
+        } else {
+            u = x;
+            hu = (int32_t)f2u(u);
+            k = (hu >> 23) - 127;
+            c = 0.0f;
+        }
+        hu &= 0x007fffff;
+        if (hu < 0x3504f7) {
+            u = u2f((uint32_t)hu | 0x3f800000u);              /* 1 + f in [1, sqrt 2) */
+        } else {
+            k += 1;
+            u = u2f((uint32_t)hu | 0x3f000000u);              /* (1 + f) / 2 */
+            hu = (0x00800000 - hu) >> 2;
+        }
+        f = u - 1.0f;
+    }
+    const float hfsq = 0.5f * f * f;
+    const float fk = (float)k;
+    if (hu == 0) { /* |f| < 2^-20 */
+        if (f == 0.0f) {
+            if (k == 0) return 0.0f;
+            c += fk * ln2_lo;
+            return fk * ln2_hi + c;
+        }
+        const float R = hfsq * (1.0f - 0.66666666666666666f * f);
+        if (k == 0) return f - R;
+        return fk * ln2_hi - ((R - (fk * ln2_lo + c)) - f);
+    }
+    const float s = f / (2.0f + f), z = s * s;
+    const float R = z * (lp1 + z * (lp2 + z * (lp3 + z * (lp4 + z * (lp5 + z * (lp6 + z * lp7))))));
+    if (k == 0) return f - (hfsq - s * (hfsq + R));
+    return fk * ln2_hi - ((hfsq - (s * (hfsq + R) + (fk * ln2_lo + c))) - f);
+}
+
+/* The number of binary32 inputs (NaNs excluded; a NaN result equals any NaN) on which
+ * orc_gate_expf (which = 0) or orc_gate_log1pf (1) differs from the host C library's expf /
+ * log1pf, over all 2^32 bit patterns, on `threads` threads. */
+typedef struct {
+    uint64_t lo, hi;
+    int which;
+    long long bad;
+} libm_job;
+
+static void *libm_scan(void *p) {
+    libm_job *j = (libm_job *)p;
+    for (uint64_t u = j->lo; u < j->hi; u++) {
+        const float x = u2f((uint32_t)u);
+        if (x != x) continue;
+        const float a = j->which ? log1pf(x) : expf(x);
+        const float b = j->which ? orc_gate_log1pf(x) : orc_gate_expf(x);
+        if (f2u(a) != f2u(b) && !(a != a && b != b)) j->bad++;
+    }
+    return NULL;
+}
+
+long long orc_libm_mismatches(int which, int threads) {
+    pthread_once(&g_exp2_once, exp2_tab_init);
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t t[64];
+    libm_job J[64];
+    const uint64_t span = (1ull << 32) / (uint64_t)threads + 1;
+    for (int i = 0; i < threads; i++) {
+        const uint64_t lo = span * (uint64_t)i, hi = lo + span;
+        J[i] = (libm_job){lo, hi < (1ull << 32) ? hi : (1ull << 32), which, 0};
+        pthread_create(&t[i], NULL, libm_scan, &J[i]);
+    }
+    long long bad = 0;
+    for (int i = 0; i < threads; i++) {
+        pthread_join(t[i], NULL);
+        bad += J[i].bad;
+    }
+    return bad;
+}
+
+/* y[i] = the host C library's expf (which = 0) or log1pf (1) of the binary32 input with bit
+ * pattern first + i, for i < n, on `threads` threads: the reference values of a device sweep. */
+typedef struct {
+    int which;
+    uint32_t first;
+    long lo, hi;
+    float *y;
+} libm_fill;
+
+static void *libm_fill_run(void *p) {
+    const libm_fill *j = (const libm_fill *)p;
+    for (long i = j->lo; i < j->hi; i++) {
+        const float x = u2f(j->first + (uint32_t)i);
+        j->y[i] = j->which ? log1pf(x) : expf(x);
+    }
+    return NULL;
+}
+
+void orc_libm_eval(int which, uint32_t first, long n, float *y, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t t[64];
+    libm_fill J[64];
+    const long span = n / threads + 1;
+    for (int i = 0; i < threads; i++) {
+        const long lo = span * i < n ? span * i : n, hi = lo + span < n ? lo + span : n;
+        J[i] = (libm_fill){which, first, lo, hi, y};
+        pthread_create(&t[i], NULL, libm_fill_run, &J[i]);
+    }
+    for (int i = 0; i < threads; i++) pthread_join(t[i], NULL);
 }

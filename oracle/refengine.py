@@ -20,9 +20,6 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 REFQ4K = HERE / "_ref" / "libpinfer_refq4k.so"
-# the same engine with the DeltaNet gates on the host's glibc expf / log1pf (the reference's
-# own build), for the pin of the gates' libm
-REFQ4K_GLIBC = HERE / "_ref" / "libpinfer_refq4k_glibc.so"
 
 
 class _Params(ctypes.Structure):

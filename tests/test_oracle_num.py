@@ -37,28 +37,49 @@ def correctly_rounded(fn, x):
     return np.float32(fn(np.longdouble(x)))
 
 
+def test_gate_functions_equal_host_libm_everywhere():
+    """The DeltaNet gates' expf / log1pf (the reference calls libm, forward_lin.c:18-19,59-66)
+    restated from this platform's C library equal it on every one of the 2^32 binary32 inputs
+    (all threads of this host; a few seconds)."""
+    import os
+
+    thr = max(1, min(16, len(os.sched_getaffinity(0))))
+    assert L.orc_libm_mismatches(0, thr) == 0, "expf"
+    assert L.orc_libm_mismatches(1, thr) == 0, "log1pf"
+
+
+def test_gate_exp2_table_is_correctly_rounded():
+    """expf's table: entry i + (i << 47) is 2^(i/32) rounded to nearest binary64, computed
+    exactly here from rationals (bisection of the integer 2^(i/32) 2^e bounds)."""
+    from fractions import Fraction
+
+    for i in range(32):
+        bits = L.orc_exp2_tab(i) + (i << 47)
+        d = np.uint64(bits).view(np.float64)
+        m, e = Fraction(float(d)), 52  # d in [1, 2): ulp 2^-52
+        ulp = Fraction(1, 1 << e)
+        # |d - 2^(i/32)| <= ulp / 2  <=>  (d -+ ulp/2)^32 brackets 2^i
+        assert (m - ulp / 2) ** 32 <= 2 ** i <= (m + ulp / 2) ** 32, i
+
+
 @pytest.mark.parametrize("lo,hi", [(-20, 20), (-103, 88), (-1e-3, 1e-3)])
-def test_gate_expf_correctly_rounded_and_near_glibc(lo, hi):
+def test_gate_expf_within_an_ulp_of_exp(lo, hi):
+    """A sanity bound that does not come from the C library: within 1 ulp of the correctly
+    rounded exp (extended precision), and correctly rounded on almost every input."""
     xs = sweep(lo, hi, 20000, seed=1)
     got = np.array([L.orc_gate_expf(float(x)) for x in xs], np.float32)
     exact = np.array([correctly_rounded(np.exp, x) for x in xs], np.float32)
-    assert np.array_equal(got, exact)
-    glibc = np.array([libm.expf(float(x)) for x in xs], np.float32)
-    ulps = np.abs(got.view(np.int32).astype(np.int64) - glibc.view(np.int32).astype(np.int64))
-    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.99
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - exact.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.999
 
 
 @pytest.mark.parametrize("lo,hi", [(0, 5e8), (0, 20), (1e-9, 1e-3), (-0.9, 0.9)])
-def test_gate_log1pf_correctly_rounded_and_near_glibc(lo, hi):
-    """Correctly rounded everywhere; within 1 ulp of this host's glibc log1pf, which is not
-    correctly rounded (a few percent of inputs in [0, 20] differ by one ulp)."""
+def test_gate_log1pf_within_an_ulp_of_log1p(lo, hi):
     xs = sweep(lo, hi, 20000, seed=2)
     got = np.array([L.orc_gate_log1pf(float(x)) for x in xs], np.float32)
     exact = np.array([correctly_rounded(np.log1p, x) for x in xs], np.float32)
-    assert np.array_equal(got, exact)
-    glibc = np.array([libm.log1pf(float(x)) for x in xs], np.float32)
-    ulps = np.abs(got.view(np.int32).astype(np.int64) - glibc.view(np.int32).astype(np.int64))
-    assert ulps.max() <= 1
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - exact.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.9
 
 
 def test_argmax_first_maximum():
