@@ -56,6 +56,32 @@ ONE_PROMPT, ONE_GEN = 16, 5          # the bounded 1-thread sample
 TRAFFIC_FILE = ROOT / "profiles" / "q4k_head_n5_fused_traffic.json"
 
 
+def default_leg(paths: dict, prompt: np.ndarray, steps: int) -> dict:
+    """What a caller of pinfer_default_spec_params() gets (k = 4, adaptive width, prompt-lookup
+    drafts of up to 7 tokens; engine/src/spec.c:385-391) on the config-5 workload, on the
+    random-init model (drafts essentially never accepted) and on the agreeing model; the tokens
+    are checked against plain greedy decoding (k = 0) of the same model, which is timed too."""
+    out = {}
+    for name, path in paths.items():
+        with Model(str(path), max_ctx=1024) as gpu:
+            sp = gpu.default_spec_params()
+            plain, _, _, td0 = gpu.bench_generate(prompt, N_GEN, 0, DRAFT_VOCAB)
+            gpu.bench_generate(prompt, N_GEN, **sp)
+            dec, rounds, ng, acc = 0.0, 0, 0, 0
+            for _ in range(steps):
+                toks, st, _, td = gpu.bench_generate(prompt, N_GEN, **sp)
+                if toks != plain:
+                    raise SystemExit(f"bench.py: default leg ({name}): tokens differ from greedy")
+                dec, rounds, ng, acc = dec + td, rounds + st.rounds, ng + st.ngram_rounds, \
+                    acc + st.accepted
+            out[name] = {"tok_s": round(steps * (N_GEN - 1) / dec, 2),
+                         "plain_k0_tok_s": round((N_GEN - 1) / td0, 2),
+                         "rounds_per_step": rounds / steps, "ngram_rounds_per_step": ng / steps,
+                         "accepted_per_step": acc / steps, "tokens_match_greedy": True}
+    out["spec_params"] = sp
+    return out
+
+
 def accepting_leg(tmp: str, prompt: np.ndarray, steps: int) -> dict:
     """The same workload on the same shape with final norms that make the MTP drafts agree
     (pqfile.agreeing_norm) and an untied head whose rows past the draft vocabulary are
@@ -85,7 +111,7 @@ def accepting_leg(tmp: str, prompt: np.ndarray, steps: int) -> dict:
            "tokens_per_pass": round(steps * (N_GEN - 1) / rounds, 3),
            "ms_per_pass": round(dec / rounds * 1e3, 4),
            "plain_k0_tok_s": round((N_GEN - 1) / td0, 2), "tokens_match_greedy": True}
-    return leg
+    return leg, path
 
 
 def log(msg: str) -> None:
@@ -174,6 +200,8 @@ def cpu_baseline(path: Path, gpu_run: tuple, prompt: np.ndarray) -> dict:
         f"{ONE_GEN} tok {one.decode_s:.2f} s ({(ONE_GEN - 1) / one.decode_s:.4f} tok/s)")
     mv = cpu_matvec_1t()
     log(f"cpu oracle Q4K matvec 3584x1024 n=1, 1 thread: {mv['us']:.0f} us, {mv['GB_s']} GB/s")
+    ks = cpu_kernels(thr)
+    log(f"cpu oracle configs 2-4: {json.dumps(ks)}")
     return {"value": round((N_GEN - 1) / full.decode_s, 4), "unit": "tok/s", "cores": thr,
             "kind": "reference", "tokens_match_gpu": match, "affinity_cpus": aff,
             "prefill_tok_s": round(N_PROMPT / full.prefill_s, 2),
@@ -184,7 +212,78 @@ def cpu_baseline(path: Path, gpu_run: tuple, prompt: np.ndarray) -> dict:
                       f"k={K_DRAFT}, draft vocab {DRAFT_VOCAB}, EOS ignored; decode timed",
             "one_thread": {"value": round((ONE_GEN - 1) / one.decode_s, 4), "unit": "tok/s",
                            "sample": f"prefill {ONE_PROMPT} ids, then {ONE_GEN} tokens at k={K_DRAFT}"},
-            "matvec_config1_1t": mv}
+            "matvec_config1_1t": mv, "configs2to4": ks}
+
+
+def cpu_kernels(thr: int) -> dict:
+    """Configs 2-4 on the oracle (the reference's Q4K / A8, DeltaNet and acceptance arithmetic
+    restated in scalar C, oracle/), on 1 thread and on thr threads (rows split; the output is
+    the same bit for bit), with the inputs of the GPU's kernel lines."""
+    import oracle
+
+    s, n = QWEN35_08B, K_DRAFT + 1
+    H, F = s.hidden, s.ffn
+    rng = np.random.default_rng(2)
+
+    def a8(cols):
+        return oracle.quant_a8(rng.standard_normal((n, cols)).astype(np.float32))
+
+    def timed(f):
+        t0 = time.perf_counter()
+        f()
+        return time.perf_counter() - t0
+
+    out = {}
+    # config 2: one DeltaNet layer's products at 5 rows: qkv/z/b/a, out, gate, up, down
+    mats = [(8224, H), (H, 2048), (F, H), (F, H), (H, F)]
+    Ws = [pqtool.gauss_q4k(20 + i, 0, r, c, 0.02) for i, (r, c) in enumerate(mats)]
+    acts = {c: a8(c) for c in {c for _, c in mats}}
+    wbytes = sum(W.nbytes for W in Ws)
+    c2 = {"weight_bytes": wbytes, "shape": "DeltaNet layer 8224x1024 + 1024x2048 + 2 x 3584x1024 "
+                                           "+ 1024x3584, Q4K x 5 A8 rows"}
+    for t in (1, thr):
+        sec = timed(lambda: [oracle.q4k_matmul(W, r, c, *acts[c], n, threads=t)
+                             for W, (r, c) in zip(Ws, mats)])
+        c2[f"{t}t"] = {"ms": round(sec * 1e3, 2), "GB_s": round(wbytes / sec / 1e9, 3)}
+    out["config2_layer"] = c2
+    # config 3: 16 heads x 128 x 128, 5 tokens: the logged pass (state after token 0, log rows
+    # 1..4), then the replay of the 4 pending rows (a full acceptance)
+    heads, dk, dv = 16, 128, 128
+    qkv = rng.standard_normal((n, 2 * heads * dk + heads * dv)).astype(np.float32)
+    for o in (0, heads * dk):
+        qkv[:, o:o + heads * dk] /= np.linalg.norm(
+            qkv[:, o:o + heads * dk].reshape(n, heads, dk), axis=-1).repeat(dk, axis=1)
+    decay = (0.9 + 0.1 / (1 + np.exp(-rng.standard_normal((n, heads))))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((n, heads))))).astype(np.float32)
+    S0 = (rng.standard_normal((heads, dk, dv)) * 0.02).astype(np.float32)
+    kw = dict(n=n, heads=heads, rep=1, dk=dk, dv=dv)
+
+    def rule_apply():
+        S1, _, lg = oracle.lin_rule(qkv, decay, beta, S0, log=True, **kw)
+        oracle.lin_apply(S1, lg[1:], n - 1, heads, dk, dv)
+
+    rule_apply()
+    reps = 20
+    sec = timed(lambda: [rule_apply() for _ in range(reps)]) / reps
+    out["config3_deltanet_1t"] = {"us_per_layer_pass": round(sec * 1e6, 1),
+                                  "work": "logged pass of 5 tokens + replay of 4 pending rows"}
+    # config 4: the LM head with argmax and acceptance (1 thread: a 16384-row sample)
+    Wh = pqtool.gauss_q4k(7, 10_000, s.vocab, H, 0.02)
+    qh = a8(H)
+    c4 = {"bytes_per_call": int(Wh.nbytes)}
+    for t, rows in ((1, 16384), (thr, s.vocab)):
+        Wr = Wh[:kbench.q4k_bytes(rows, H)]
+
+        def head():
+            Y = oracle.q4k_matmul(Wr, rows, H, *qh, n, threads=t)
+            oracle.accept(Y, np.array([oracle.argmax(Y[i]) for i in range(n - 1)], np.int32))
+
+        sec = timed(head)
+        gbs = Wr.nbytes / sec / 1e9
+        c4[f"{t}t"] = {"GB_s": round(gbs, 3), "ms_per_call": round(Wh.nbytes / gbs / 1e6, 1),
+                       "sample_rows": rows}
+    out["config4_head"] = c4
+    return out
 
 
 def cpu_matvec_1t(reps: int = 20) -> dict:
@@ -257,10 +356,13 @@ def main() -> int:
                     f"{(N_GEN - 1) / td:.1f} tok/s, rounds {st.rounds} accepted {st.accepted}")
             tps = a.steps * (N_GEN - 1) / dec
         cpu = None if a.no_cpu else cpu_baseline(path, (first, first_st), prompt)
-        accept = None
+        accept = default = None
         if not a.no_accept:
-            accept = accepting_leg(tmp, prompt, a.steps)
+            accept, agree_path = accepting_leg(tmp, prompt, a.steps)
             log(f"accepting leg: {json.dumps(accept)}")
+            default = default_leg({"random_init": path, "agreeing": agree_path}, prompt,
+                                  max(1, min(a.steps, 5)))
+            log(f"default spec params leg: {json.dumps(default)}")
     roof = head_roofline()
     log(f"head (in path, cold): {roof['us_per_launch']} us, {roof['achieved']} GB/s")
     kernels = None
@@ -286,7 +388,8 @@ def main() -> int:
                  "tokens_per_pass": round((N_GEN - 1) / rounds, 3) if rounds else None,
                  "ms_per_pass": round(dec / stats[0] * 1e3, 4) if stats[0] else None},
         "prefill_tok_s": round(a.steps * N_PROMPT / pre, 1),
-        "roofline": roof, "cpu_baseline": cpu, "accepting": accept, "kernels": kernels,
+        "roofline": roof, "cpu_baseline": cpu, "accepting": accept,
+        "default_spec_params": default, "kernels": kernels,
     }
     print(json.dumps(rec), flush=True)
     return 0

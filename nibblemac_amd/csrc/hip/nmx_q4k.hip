@@ -1420,6 +1420,16 @@ int nmx_head_row_keys(nmx_ctx *ctx, const void *W, int rows, int cols, const flo
     return 0;
 }
 
+int nmx_head_step(nmx_ctx *ctx, const void *W, int rows, int cols, const int8_t *q,
+                  const float *d, const float *fsum, void *work, int32_t *out, int32_t *vt,
+                  int32_t *ctl, int32_t *mailbox, int nvt) {
+    if (!ctx) return -1;
+    if (!vt || !ctl || (mailbox && (nvt < 2 || nvt > 1024)))
+        return nmx_fail(ctx, "nmx_head_step: bad arguments");
+    return head_accept(ctx, W, rows, cols, 1, q, d, fsum, nullptr, nullptr, work, out, vt,
+                       FinishCommit{vt, ctl, mailbox, mailbox ? nvt : 0, ctl});
+}
+
 int nmx_head_accept_commit(nmx_ctx *ctx, const void *W, int rows, int cols, int n,
                            const int8_t *q, const float *d, const float *fsum,
                            const int32_t *drafts, void *work, int32_t *out, int32_t *vt,

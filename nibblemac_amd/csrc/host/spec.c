@@ -101,6 +101,18 @@ static int commit_lin_redo(pinfer_ctx *c) {
     return PINFER_OK;
 }
 
+/* One plain greedy step (engine/src/spec.c:238-262) at n_past = ctl[0]: cur = vt[0] through
+ * the model, its argmax to vt[0] and the host mailbox, n_past += 1 on the device (every path
+ * that changes n_past leaves ctl[0] equal to it, so a captured step needs no position upload).
+ * The final-normed row stays in s.xn for the MTP pass the host may queue it for. */
+static int seq_plain(pinfer_ctx *c) {
+    TRY(e_forward(c, c->vt, 1, 0, 0));
+    e_scratch *sc = &c->s;
+    CK(nmx_head_step(c->dev, c->head.w, c->vocab, c->H, sc->a_h.q, sc->a_h.d, sc->a_h.fs,
+                     c->hwork, c->hout, c->vt, c->ctl, c->mbox, 2));
+    return PINFER_OK;
+}
+
 /* One MTP round of ke drafts (engine/src/spec.c:303-365): the chain d2..dk, the verify, the
  * commit of e = ctl[1], the MTP head over the committed rows (its hidden of row e - 1 and the
  * next d1; the pass reads the verify's final-normed rows, s.xn, which at hidden <= 1024 it
@@ -108,6 +120,7 @@ static int commit_lin_redo(pinfer_ctx *c) {
  * pass's last kernel). The chain's drafts d2..dk pass as argmax keys: each one's consumer (the
  * next MTP pass, then the verify's first norm) resolves it and writes it to vt. */
 static int seq_round(pinfer_ctx *c, int ke, int nv) {
+    if (ke == 0) return seq_plain(c); /* a round without drafts: a plain step */
     const int keys = e_keys_ok(c);
     for (int s = 1; s < ke; s++) {
         const float *h = s == 1 ? m_cur(c) : m_ping(c, s - 1);
@@ -287,19 +300,24 @@ static int defer_rows(pinfer_ctx *c, e_pending *pd, const int32_t *tok, int m, i
 }
 
 /* One plain step (engine/src/spec.c:238-262): cur through the model at n_past, argmax; with
- * the MTP head the final-normed row is queued for a later MTP pass. */
+ * the MTP head the final-normed row is queued for a later MTP pass. With graphs the step is
+ * one launch (the round graph of 0 drafts) whose head writes the token to the mailbox. */
 static int plain_step(pinfer_ctx *c, int use_mtp, e_pending *pd, int nv, int32_t *next) {
     const int P = c->n_past;
     if (use_mtp && pd->n == E_MAX_BATCH) TRY(flush_pending(c, pd, nv));
-    TRY(e_set_pos(c, P));
-    TRY(e_forward(c, c->vt, 1, 0, 0));
+    if (c->use_graphs) {
+        TRY(launch_round(c, 0, nv, 0));
+        if (wait_mailbox(c, 0)) return PINFER_E_ARG;
+        *next = c->mbox[1];
+    } else {
+        TRY(e_set_pos(c, P));
+        TRY(seq_plain(c));
+        CK(nmx_download(c->dev, next, c->vt, sizeof(int32_t)));
+    }
     c->keep = 0;
-    TRY(e_head_last(c, 1, c->vt, 0));
-    CK(nmx_download(c->dev, next, c->vt, sizeof(int32_t)));
     if (use_mtp) TRY(defer_rows(c, pd, next, 1, P));
     e_ngram_push(&c->ng, next, 1);
     c->n_past = P + 1;
-    TRY(e_set_pos(c, c->n_past));
     return PINFER_OK;
 }
 

@@ -86,6 +86,12 @@ class Model:
             raise PinferError(status.value or n, "pinfer_generate_greedy")
         return [int(x) for x in out[:n]], st
 
+    def default_spec_params(self) -> dict:
+        """pinfer_default_spec_params() as a dict (k, draft_vocab, adaptive, ngram)."""
+        sp = self.lib.pinfer_default_spec_params()
+        return {"k": sp.k, "draft_vocab": sp.draft_vocab, "adaptive": sp.adaptive,
+                "ngram": sp.ngram}
+
     def state_save(self) -> bytes:
         """The context state as a blob (pinfer_state_save)."""
         n = self.lib.pinfer_state_size(self.ctx)
@@ -114,7 +120,8 @@ class Model:
     def checkpoint_n_past(self) -> int:
         return self.lib.pinfer_checkpoint_n_past(self.ctx)
 
-    def bench_generate(self, prompt, n_gen: int, k: int = 4, draft_vocab: int = 32768):
+    def bench_generate(self, prompt, n_gen: int, k: int = 4, draft_vocab: int = 32768,
+                       adaptive: int = 0, ngram: int = 0):
         """The reference CLI's benchmark timing (engine/tools/pinfer_run.c:384-430): reset,
         prefill, then exactly n_gen tokens with EOS ignored. Returns (tokens, stats, prefill
         seconds, decode seconds); decode tok/s is (n_gen - 1) / decode seconds."""
@@ -122,7 +129,7 @@ class Model:
             raise PinferError(-4, f"{self.lib.path} has no pinfer_bench_generate")
         t = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(n_gen, np.int32)
-        sp, st = SpecParams(k, draft_vocab, 0, 0), SpecStats()
+        sp, st = SpecParams(k, draft_vocab, adaptive, ngram), SpecStats()
         tp, td = ctypes.c_double(0.0), ctypes.c_double(0.0)
         n = self.lib.pinfer_bench_generate(
             self.ctx, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), t.size,
