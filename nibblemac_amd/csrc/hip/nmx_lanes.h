@@ -79,18 +79,19 @@ __device__ __forceinline__ unsigned long long nmx_max_u64_wave(unsigned long lon
 
 /* The row of the greatest of nk argmax keys (order-preserving value bits over the complemented
  * row index, so the greatest key is the first maximum): what head_finish_k resolves for one
- * vector. Every lane of the calling wave gets it; the first 256 keys are requested together. */
+ * vector. Every lane of the calling wave gets it; the first 512 keys (the draft head over 32768
+ * rows leaves 512) are requested together. */
 __device__ __forceinline__ int nmx_keys_token(const unsigned long long *keys, int nk) {
     const int lane = threadIdx.x & 63;
-    unsigned long long k[4], m = 0ull;
+    unsigned long long k[8], m = 0ull;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < 8; u++) {
         const int i = lane + 64 * u;
         k[u] = keys[i < nk ? i : nk - 1];
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) m = k[u] > m ? k[u] : m;
-    for (int i = lane + 256; i < nk; i += 64) m = keys[i] > m ? keys[i] : m;
+    for (int u = 0; u < 8; u++) m = k[u] > m ? k[u] : m;
+    for (int i = lane + 512; i < nk; i += 64) m = keys[i] > m ? keys[i] : m;
     m = nmx_max_u64_wave(m);
     return (int)(0xffffffffu - (uint32_t)(m & 0xffffffffull));
 }

@@ -512,10 +512,15 @@ struct FinishCommit {
 /* The one-row head with its input's RMSNorm inside (nmx_head_row_accept_to): row *idx + off of
  * x (+ add), clamped to [0, nrows), normed with w (rms4_load / rms4_finish: the arithmetic of
  * nmx_rmsnorm_row) into y (written by workgroup 0) and into a one-vector A8 in LDS; then the
- * dots of q4k_mv_k<1, false, true> with the activations read from LDS. The row's loads are
- * requested before the first superblock's weights, so the norm runs while the weights are in
- * flight. cols <= 1024; W has rows rows. The leading 16 SGPRs of arguments are what the first
- * requests need (preloaded with the wave). */
+ * dots of the row against 64 rows of W per workgroup, split over the cols / 256 superblocks: wave
+ * s requests superblock s of its 64 rows at entry (right behind the norm's row), computes that
+ * superblock's exact int32 block dots with v_dot4 (activations from LDS) and its (float)dot,
+ * (D s) d, -(M m), fsum records in registers, and the fp32 chain then runs wave 0 -> 1 -> ... in
+ * column order, the running accumulator handed over through LDS, so each (row) chain performs
+ * the reference's operations in its order (engine/src/kern_quant.c:148-245) while every
+ * superblock's loads are in flight at once. One partial argmax key per workgroup. cols <= 1024
+ * (64 cols / 4 threads: the norm's float4 per thread); W has rows rows. The leading arguments
+ * are what the first requests need (preloaded with the wave). */
 constexpr int MVR_MAX_COLS = 1024;
 
 __global__ __launch_bounds__(256) void q4k_mvr_k(const int32_t *__restrict__ idx,
@@ -529,77 +534,72 @@ __global__ __launch_bounds__(256) void q4k_mvr_k(const int32_t *__restrict__ idx
     __shared__ __align__(16) int8_t s_q[MVR_MAX_COLS];
     __shared__ float s_d[MVR_MAX_COLS / 32], s_fs[MVR_MAX_COLS / 32];
     __shared__ __align__(16) float s_sq[4 * cm_stride(MVR_MAX_COLS) + 4];
-    __shared__ float s_red[8];
+    __shared__ float s_red[8], hand[64];
     /* the norm's row first */
     const int ri = *idx + off;
     const size_t r = (size_t)(ri < 0 ? 0 : ri >= nrows ? nrows - 1 : ri);
     float4 xv[1], av[1], wv[1];
     rms4_load<1>(x + r * x_stride, add ? add + r * add_stride : nullptr, w, cols, xv, av, wv);
 
-    const int total_waves = (rows + 63) / 64;
-    const int wave_raw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const bool wave_live = wave_raw < total_waves;
-    const int wave = wave_live ? wave_raw : total_waves - 1;
+    const int sb = threadIdx.x >> 6, nsb = cols >> 8; /* this wave's superblock */
     const int lane = threadIdx.x & 63;
-    const int row_raw = wave * 64 + lane;
-    const bool valid = wave_live && row_raw < rows;
-    const int row = row_raw < rows ? row_raw : rows - 1;
+    const int row_raw = blockIdx.x * 64 + lane;
+    const bool valid = row_raw < rows;
+    const int row = valid ? row_raw : rows - 1;
     const int i = row & 3, sh8 = 8 * i;
-    const int nsb = cols >> 8;
-    const uint4 *tp = (const uint4 *)(W + (size_t)(row >> 2) * nsb * SB_BYTES);
-    uint4 a0 = tp[0], a1 = tp[1], a2 = tp[2], a3 = tp[3], c[8];
+    const uint4 *p = (const uint4 *)(W + ((size_t)(row >> 2) * nsb + sb) * SB_BYTES);
+    const uint4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+    uint4 c[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) c[k] = tp[4 + 4 * k + i];
+    for (int k = 0; k < 8; k++) c[k] = p[4 + 4 * k + i];
 
     rms4_finish<1>(xv, av, wv, add != nullptr, nullptr, cols, eps, blockIdx.x == 0 ? y : nullptr,
                    s_q, s_d, s_fs, 1, 0, s_sq, s_red);
     __syncthreads(); /* the A8 row is in LDS */
 
-    float acc = 0.0f;
-    for (int sb = 0; sb < nsb; sb++) {
-        const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
-        const float D = half_bits_to_float(dw >> (16 * (i & 1)));
-        const float M = half_bits_to_float(mw >> (16 * (i & 1)));
-        int s6[8], m6[8];
-        decode6(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, s6);
-        decode6(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, m6);
+    const uint32_t dw = (i & 2) ? a0.y : a0.x, mw = (i & 2) ? a0.w : a0.z;
+    const float D = half_bits_to_float(dw >> (16 * (i & 1)));
+    const float M = half_bits_to_float(mw >> (16 * (i & 1)));
+    int s6[8], m6[8];
+    decode6(a1.x, a1.y, a1.z, a1.w, a2.x, a2.y, sh8, s6);
+    decode6(a2.z, a2.w, a3.x, a3.y, a3.z, a3.w, sh8, m6);
+    float tf[8], tm[8], to[8], tfs[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float sc = D * (float)s6[k]; /* exact: 6-bit x 11-bit mantissa */
-            const float of = M * (float)m6[k];
-            const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
-            const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
-            const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
-            const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
-            const int blk = sb * 8 + k;
-            const int4 x0 = *(const int4 *)(s_q + blk * 32), x1 = *(const int4 *)(s_q + blk * 32 + 16);
-            int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
-            dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
-            dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
-            dot = __builtin_amdgcn_sdot4(lo3, x0.w, dot, false);
-            dot = __builtin_amdgcn_sdot4(hi0, x1.x, dot, false);
-            dot = __builtin_amdgcn_sdot4(hi1, x1.y, dot, false);
-            dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
-            dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
-            acc = __builtin_fmaf((float)dot, sc * s_d[blk], acc);
-            acc = __builtin_fmaf(-of, s_fs[blk], acc);
-        }
-        if (sb + 1 < nsb) {
-            const uint4 *p = tp + (sb + 1) * (SB_BYTES / 16);
-            a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
-#pragma unroll
-            for (int k = 0; k < 8; k++) c[k] = p[4 + 4 * k + i];
-        }
+    for (int k = 0; k < 8; k++) {
+        const int blk = sb * 8 + k;
+        const int4 x0 = *(const int4 *)(s_q + blk * 32), x1 = *(const int4 *)(s_q + blk * 32 + 16);
+        int dot = __builtin_amdgcn_sdot4((int)(c[k].x & 0x0f0f0f0fu), x0.x, 0, false);
+        dot = __builtin_amdgcn_sdot4((int)(c[k].y & 0x0f0f0f0fu), x0.y, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)(c[k].z & 0x0f0f0f0fu), x0.z, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)(c[k].w & 0x0f0f0f0fu), x0.w, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((c[k].x >> 4) & 0x0f0f0f0fu), x1.x, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((c[k].y >> 4) & 0x0f0f0f0fu), x1.y, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((c[k].z >> 4) & 0x0f0f0f0fu), x1.z, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((c[k].w >> 4) & 0x0f0f0f0fu), x1.w, dot, false);
+        tf[k] = (float)dot;
+        tm[k] = (D * (float)s6[k]) * s_d[blk]; /* exact: 6-bit x 11-bit mantissa, then d */
+        to[k] = -(M * (float)m6[k]);
+        tfs[k] = s_fs[blk];
     }
-    /* the argmax keys, as q4k_mv_k */
-    __shared__ unsigned long long wkeys[4];
-    const unsigned long long key = nmx_max_u64_wave(valid ? argmax_key(acc, row) : 0ull);
-    if (lane == 0) wkeys[threadIdx.x >> 6] = key;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long k0 = wkeys[0];
-        for (int w = 1; w < 4; w++) k0 = wkeys[w] > k0 ? wkeys[w] : k0;
-        amax_key[blockIdx.x] = k0;
+    /* the chain: acc = fma((float)dot, (D*s)*d, acc); acc = fma(-(M*m), fsum, acc), block by
+     * block, superblock 0 first */
+    float acc = 0.0f;
+    for (int turn = 0; turn < nsb; turn++) {
+        if (turn == sb) {
+            if (sb > 0) acc = hand[lane];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc = __builtin_fmaf(tf[k], tm[k], acc);
+                acc = __builtin_fmaf(to[k], tfs[k], acc);
+            }
+            if (sb + 1 < nsb) hand[lane] = acc;
+        }
+        __syncthreads();
+    }
+    /* the argmax key of the workgroup's 64 rows, from the last superblock's wave */
+    if (sb == nsb - 1) {
+        const unsigned long long key = nmx_max_u64_wave(valid ? argmax_key(acc, row) : 0ull);
+        if (lane == 0) amax_key[blockIdx.x] = key;
     }
 }
 
@@ -1388,10 +1388,11 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
             return -1;
         return advance ? nmx_ctl_advance(ctx, advance) : 0;
     }
-    const int blocks = ((rows + 63) / 64 + 3) / 4;
+    const int blocks = nmx_head_row_nkeys(rows);
     unsigned long long *keys = (unsigned long long *)work;
-    q4k_mvr_k<<<blocks, 256, 0, ctx->stream>>>(idx, x, add, w, (const uint8_t *)W, off, nrows,
-                                                x_stride, add_stride, cols, rows, eps, y, keys);
+    q4k_mvr_k<<<blocks, cols / 4, 0, ctx->stream>>>(idx, x, add, w, (const uint8_t *)W, off,
+                                                     nrows, x_stride, add_stride, cols, rows, eps,
+                                                     y, keys);
     NMX_LAUNCHED(ctx, "q4k_mvr");
     head_finish_k<<<1, 1024, 0, ctx->stream>>>(keys, blocks, 1, nullptr, out, tok_dst,
                                                 FinishCommit{nullptr, nullptr, nullptr, 0, advance});
@@ -1399,7 +1400,7 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
     return 0;
 }
 
-int nmx_head_row_nkeys(int rows) { return rows > 0 ? ((rows + 63) / 64 + 3) / 4 : 0; }
+int nmx_head_row_nkeys(int rows) { return rows > 0 ? (rows + 63) / 64 : 0; }
 
 int nmx_head_row_keys(nmx_ctx *ctx, const void *W, int rows, int cols, const float *x,
                       int x_stride, const float *add, int add_stride, const float *w, float eps,
@@ -1413,7 +1414,7 @@ int nmx_head_row_keys(nmx_ctx *ctx, const void *W, int rows, int cols, const flo
         !al(w) || x_stride % 4 || (add && (!al(add) || add_stride % 4)) || (y && !al(y)) ||
         (uintptr_t)keys % 8)
         return nmx_fail(ctx, "nmx_head_row_keys: shape outside the fused kernel (cols %d)", cols);
-    q4k_mvr_k<<<nmx_head_row_nkeys(rows), 256, 0, ctx->stream>>>(
+    q4k_mvr_k<<<nmx_head_row_nkeys(rows), cols / 4, 0, ctx->stream>>>(
         idx, x, add, w, (const uint8_t *)W, off, nrows, x_stride, add_stride, cols, rows, eps, y,
         (unsigned long long *)keys);
     NMX_LAUNCHED(ctx, "q4k_mvr");
