@@ -1373,8 +1373,8 @@ int nmx_head_row_accept_to(nmx_ctx *ctx, const void *W, int rows, int cols, cons
         (add && add_stride < cols))
         return nmx_fail(ctx, "nmx_head_row_accept_to: bad arguments");
     auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
-    const bool fused = cols % 256 == 0 && cols <= MVR_MAX_COLS && rows > 0 && rows % 4 == 0 &&
-                       rows <= (1 << 22) && al(x) && al(w) && x_stride % 4 == 0 &&
+    const bool fused = cols > 0 && cols % 256 == 0 && cols <= MVR_MAX_COLS && rows > 0 &&
+                       rows % 4 == 0 && rows <= (1 << 22) && al(x) && al(w) && x_stride % 4 == 0 &&
                        (!add || (al(add) && add_stride % 4 == 0)) && (!y || al(y)) &&
                        (uintptr_t)work % 8 == 0;
     if (!fused) { /* the norm, then the head on its A8 */
@@ -1410,8 +1410,9 @@ int nmx_head_row_keys(nmx_ctx *ctx, const void *W, int rows, int cols, const flo
     if (!W || !x || !w || !idx || !keys || nrows < 1 || x_stride < cols ||
         (add && add_stride < cols))
         return nmx_fail(ctx, "nmx_head_row_keys: bad arguments");
-    if (cols % 256 || cols > MVR_MAX_COLS || rows <= 0 || rows % 4 || rows > (1 << 22) || !al(x) ||
-        !al(w) || x_stride % 4 || (add && (!al(add) || add_stride % 4)) || (y && !al(y)) ||
+    if (cols <= 0 || cols % 256 || cols > MVR_MAX_COLS || rows <= 0 || rows % 4 ||
+        rows > (1 << 22) || !al(x) || !al(w) || x_stride % 4 ||
+        (add && (!al(add) || add_stride % 4)) || (y && !al(y)) ||
         (uintptr_t)keys % 8)
         return nmx_fail(ctx, "nmx_head_row_keys: shape outside the fused kernel (cols %d)", cols);
     q4k_mvr_k<<<nmx_head_row_nkeys(rows), cols / 4, 0, ctx->stream>>>(
