@@ -14,8 +14,9 @@
  *      activations are staged into LDS (copied, or computed by the RMSNorm prologue);
  *   1. every unit decodes its sub-scales and computes its 4 blocks x NV exact int32 dots with
  *      v_dot4_i32_i8, storing one record ((float)dot, (D*s)*d_v, -(M*m), fsum_v) per (block,
- *      vector, row) to LDS laid out [block][vector][row] (the 64-row SwiGLU launch stores
- *      ((float)dot, (D*s)*d_v) pairs and -(M*m) separately, to fit in 160 KB);
+ *      vector, row) to LDS laid out [vector][row][block] (a chain's records contiguous, so its
+ *      reads take immediate offsets; the 64-row SwiGLU launch stores ((float)dot, (D*s)*d_v)
+ *      pairs [block][vector][row] and -(M*m) separately, to fit in 160 KB);
  *   2. one lane per (row, vector) runs the fp32 chain over the blocks in column order, two
  *      FMAs per block from one 16-byte LDS read (three reads for SwiGLU), then stores the row
  *      (or, for SwiGLU, the workgroup combines its gate and up halves, silu(g) * u, and
@@ -118,9 +119,10 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     L.ad = (aq_off(nb, nv) + 15) & ~15;
     L.afs = L.ad + nb * nv * 4;
     L.work = (L.afs + nb * nv * 4 + 15) & ~15;
-    /* chain records: (dot, (D*s)*d, -(M*m), fsum) float4 [nb][nv][R]; the SwiGLU launch (64
-     * rows) keeps ((float)dot, (D*s)*d) float2 [nb][nv][R] and -(M*m) [nb][R] to fit */
-    int work = swiglu ? nb * nv * R * 8 + nb * R * 4 : nb * nv * R * 16;
+    /* chain records: (dot, (D*s)*d, -(M*m), fsum) float4 [nv][R][nb | 1] (each chain's blocks
+     * contiguous, an odd stride between chains); the SwiGLU launch (64 rows) keeps ((float)dot,
+     * (D*s)*d) float2 [nb][nv][R] and -(M*m) [nb][R] to fit */
+    int work = swiglu ? nb * nv * R * 8 + nb * R * 4 : nv * R * (nb | 1) * 16;
     /* the norm prologue: chain-major squares, then the summed rows [nv][cols] (PAIR: 2 nv rows
      * of cols / 2) */
     const int nr = pair ? 2 * nv : nv, rc = pair ? cols / 2 : cols;
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     int8_t *aq = (int8_t *)(smem + L.aq);
     float *ad = (float *)(smem + L.ad), *afs = (float *)(smem + L.afs);
     constexpr bool REC = !SWI; /* one float4 record per (block, vector, row) */
-    float4 *rec = (float4 *)(smem + L.work);  /* [nb][NV][R] (dot, (D*s)*d, -(M*m), fsum) */
+    float4 *rec = (float4 *)(smem + L.work);  /* [NV][R][nb | 1] (dot, (D*s)*d, -(M*m), fsum) */
     float2 *lp = (float2 *)(smem + L.work);  /* [nb][NV][R] ((float)dot, (D*s)*d) */
     float *lof = (float *)(lp + nb * NV * R); /* [nb][R] -(M*m) */
 
@@ -525,7 +527,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                 dot = __builtin_amdgcn_sdot4(hi2, x1.z, dot, false);
                 dot = __builtin_amdgcn_sdot4(hi3, x1.w, dot, false);
                 if constexpr (REC)
-                    rec[(blk * NV + v) * R + u_r] =
+                    rec[(v * R + u_r) * (nb | 1) + blk] =
                         make_float4((float)dot, sc * sdv[k * NV + v], -of, sfv[k * NV + v]);
                 else
                     lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * sdv[k * NV + v]);
@@ -546,12 +548,13 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     if (chain) {
         /* per block: acc = fma((float)dot, (D*s)*d_v, acc); acc = fma(-(M*m), fsum_v, acc) */
         if constexpr (REC) {
-            const float4 *rp = rec + cv * R + cr;
+            /* the chain's records are contiguous: one base, immediate offsets */
+            const float4 *rp = rec + (cv * R + cr) * (nb | 1);
             int b = 0;
             for (; b + 8 <= nb; b += 8) {
                 float4 r[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) r[u] = rp[(b + u) * NV * R];
+                for (int u = 0; u < 8; u++) r[u] = rp[b + u];
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
                     acc = __builtin_fmaf(r[u].x, r[u].y, acc);
@@ -559,7 +562,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                 }
             }
             for (; b < nb; b++) {
-                const float4 r = rp[b * NV * R];
+                const float4 r = rp[b];
                 acc = __builtin_fmaf(r.x, r.y, acc);
                 acc = __builtin_fmaf(r.z, r.w, acc);
             }
