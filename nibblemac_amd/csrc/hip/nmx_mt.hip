@@ -16,7 +16,7 @@
  *      v_dot4_i32_i8, storing one record ((float)dot, (D*s)*d_v, -(M*m), fsum_v) per (block,
  *      vector, row) to LDS laid out [vector][row][block] (a chain's records contiguous, so its
  *      reads take immediate offsets; the 64-row SwiGLU launch stores ((float)dot, (D*s)*d_v)
- *      pairs [block][vector][row] and -(M*m) separately, to fit in 160 KB);
+ *      pairs and -(M*m) separately, laid out the same way, to fit in 160 KB);
  *   2. one lane per (row, vector) runs the fp32 chain over the blocks in column order, two
  *      FMAs per block from one 16-byte LDS read (three reads for SwiGLU), then stores the row
  *      (or, for SwiGLU, the workgroup combines its gate and up halves, silu(g) * u, and
@@ -121,8 +121,8 @@ __host__ __device__ inline MtLayout mt_layout(int cols, int nv, int R, bool norm
     L.work = (L.afs + nb * nv * 4 + 15) & ~15;
     /* chain records: (dot, (D*s)*d, -(M*m), fsum) float4 [nv][R][nb | 1] (each chain's blocks
      * contiguous, an odd stride between chains); the SwiGLU launch (64 rows) keeps ((float)dot,
-     * (D*s)*d) float2 [nb][nv][R] and -(M*m) [nb][R] to fit */
-    int work = swiglu ? nb * nv * R * 8 + nb * R * 4 : nv * R * (nb | 1) * 16;
+     * (D*s)*d) float2 [nv][R][nb | 1] and -(M*m) [R][nb | 1] to fit */
+    int work = swiglu ? (nv * R * 8 + R * 4) * (nb | 1) : nv * R * (nb | 1) * 16;
     /* the norm prologue: chain-major squares, then the summed rows [nv][cols] (PAIR: 2 nv rows
      * of cols / 2) */
     const int nr = pair ? 2 * nv : nv, rc = pair ? cols / 2 : cols;
@@ -166,8 +166,8 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     float *ad = (float *)(smem + L.ad), *afs = (float *)(smem + L.afs);
     constexpr bool REC = !SWI; /* one float4 record per (block, vector, row) */
     float4 *rec = (float4 *)(smem + L.work);  /* [NV][R][nb | 1] (dot, (D*s)*d, -(M*m), fsum) */
-    float2 *lp = (float2 *)(smem + L.work);  /* [nb][NV][R] ((float)dot, (D*s)*d) */
-    float *lof = (float *)(lp + nb * NV * R); /* [nb][R] -(M*m) */
+    float2 *lp = (float2 *)(smem + L.work);  /* [NV][R][nb | 1] ((float)dot, (D*s)*d) */
+    float *lof = (float *)(lp + NV * R * (nb | 1)); /* [R][nb | 1] -(M*m) */
 
     /* ---- segment and rows of this workgroup (segment 0 from the preloaded arguments: its
      * workgroups are the first ceil(rows0 / R); SwiGLU launches are one segment pair) ---- */
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
             }
             const float sc = D * (float)s6[kh + k]; /* exact: 6-bit x 11-bit mantissa */
             const float of = M * (float)m6[kh + k];
-            if constexpr (!REC) lof[blk * R + u_r] = -of;
+            if constexpr (!REC) lof[u_r * (nb | 1) + blk] = -of;
             const int lo0 = (int)(c[k].x & 0x0f0f0f0fu), hi0 = (int)((c[k].x >> 4) & 0x0f0f0f0fu);
             const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
             const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
@@ -530,7 +530,8 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                     rec[(v * R + u_r) * (nb | 1) + blk] =
                         make_float4((float)dot, sc * sdv[k * NV + v], -of, sfv[k * NV + v]);
                 else
-                    lp[(blk * NV + v) * R + u_r] = make_float2((float)dot, sc * sdv[k * NV + v]);
+                    lp[(v * R + u_r) * (nb | 1) + blk] =
+                        make_float2((float)dot, sc * sdv[k * NV + v]);
             }
             if (k < BPU - 1) {
 #pragma unroll
@@ -567,17 +568,18 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                 acc = __builtin_fmaf(r.z, r.w, acc);
             }
         } else {
-        const float2 *pp = lp + cv * R + cr;
-        const float *op = lof + cr;
+        const float2 *pp = lp + (cv * R + cr) * (nb | 1);
+        const float *op = lof + cr * (nb | 1);
+        const float *fp = afs + cv; /* uniform in a wave (R = 64) */
         int b = 0;
         for (; b + 8 <= nb; b += 8) {
             float2 pv[8];
             float of[8], ff[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                pv[u] = pp[(b + u) * NV * R];
-                of[u] = op[(b + u) * R];
-                ff[u] = afs[(b + u) * NV + cv];
+                pv[u] = pp[b + u];
+                of[u] = op[b + u];
+                ff[u] = fp[(b + u) * NV];
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
@@ -586,10 +588,10 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
             }
         }
         for (; b < nb; b++) {
-            const float2 pv = pp[b * NV * R];
-            const float ff = afs[b * NV + cv];
+            const float2 pv = pp[b];
+            const float ff = fp[b * NV];
             acc = __builtin_fmaf(pv.x, pv.y, acc);
-            acc = __builtin_fmaf(op[b * R], ff, acc);
+            acc = __builtin_fmaf(op[b], ff, acc);
         }
         }
     }
