@@ -376,27 +376,42 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
         }
         }
         __syncthreads();
-        if (tid < 4 * NR) { /* chain l of row v, the next 32 terms' reads issued ahead */
+        if (tid < 4 * NR) { /* chain l of row v: two register sets of 32 terms take turns, the
+                             * next set requested before the current one is added (scheduling
+                             * barriers keep that order; a request past the end re-reads) */
             const float *ch = sq + (tid >> 2) * rsz + (tid & 3) * s4;
             float a = 0.0f;
             int m = 0;
+            auto fetch = [&](float4 (&b)[8], int m0) {
+#pragma unroll
+                for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + m0 + 4 * u);
+            };
+            auto add = [&](const float4 (&b)[8]) {
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    a = a + b[u].x;
+                    a = a + b[u].y;
+                    a = a + b[u].z;
+                    a = a + b[u].w;
+                }
+            };
             if (m4 >= 32) {
-                float4 b[8], nb4[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + 4 * u);
-                for (; m + 32 <= m4; m += 32) {
-                    const int mn = m + 64 <= m4 ? m + 32 : m; /* past the end: a reread */
-#pragma unroll
-                    for (int u = 0; u < 8; u++) nb4[u] = *(const float4 *)(ch + mn + 4 * u);
-#pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        a = a + b[u].x;
-                        a = a + b[u].y;
-                        a = a + b[u].z;
-                        a = a + b[u].w;
-                    }
-#pragma unroll
-                    for (int u = 0; u < 8; u++) b[u] = nb4[u];
+                float4 ba[8], bb[8];
+                fetch(ba, 0);
+                for (; m + 64 <= m4; m += 64) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    fetch(bb, m + 32);
+                    __builtin_amdgcn_sched_barrier(0);
+                    add(ba);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fetch(ba, m + 96 <= m4 ? m + 64 : m);
+                    __builtin_amdgcn_sched_barrier(0);
+                    add(bb);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (m + 32 <= m4) { /* ba holds terms m .. m + 31 */
+                    add(ba);
+                    m += 32;
                 }
             }
             for (; m < m4; m++) a = a + ch[m];
