@@ -395,7 +395,15 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                     a = a + b[u].w;
                 }
             };
-            if (m4 >= 32) {
+            /* (the second set would spill at 6 or more rows in 1024-thread launches) */
+            constexpr bool TWO = NV <= 5 || BPU == 4;
+            if (!TWO) {
+                for (; m + 32 <= m4; m += 32) {
+                    float4 b[8];
+                    fetch(b, m);
+                    add(b);
+                }
+            } else if (m4 >= 32) {
                 float4 ba[8], bb[8];
                 fetch(ba, 0);
                 for (; m + 64 <= m4; m += 64) {

@@ -12,23 +12,45 @@
 #include "nmx_lanes.h"
 
 /* The same sum over values stored chain-major: chain l's m-th value at cm[l * s4 + m]
- * (s4 a multiple of 4, so a chain is read as float4), the cols % 4 tail at cm[4 * s4 + k]. */
+ * (s4 a multiple of 4, so a chain is read as float4), the cols % 4 tail at cm[4 * s4 + k].
+ * Two register sets of 32 values take turns: the next set is requested before the current
+ * one is added (scheduling barriers keep that order; a request past the end re-reads). */
 __device__ inline float ordered_sum4_cm(const float *cm, int cols, int s4, float *red) {
     const int tid = threadIdx.x, m4 = cols >> 2;
     if (tid < 4) {
         const float *ch = cm + tid * s4;
         float c = 0.0f;
         int m = 0;
-        for (; m + 32 <= m4; m += 32) {
-            float4 b[8];
+        auto fetch = [&](float4 (&b)[8], int m0) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + m + 4 * u);
+            for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(ch + m0 + 4 * u);
+        };
+        auto add = [&](const float4 (&b)[8]) {
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 c = c + b[u].x;
                 c = c + b[u].y;
                 c = c + b[u].z;
                 c = c + b[u].w;
+            }
+        };
+        if (m4 >= 32) {
+            float4 ba[8], bb[8];
+            fetch(ba, 0);
+            for (; m + 64 <= m4; m += 64) {
+                __builtin_amdgcn_sched_barrier(0);
+                fetch(bb, m + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                add(ba);
+                __builtin_amdgcn_sched_barrier(0);
+                fetch(ba, m + 96 <= m4 ? m + 64 : m);
+                __builtin_amdgcn_sched_barrier(0);
+                add(bb);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (m + 32 <= m4) { /* ba holds values m .. m + 31 */
+                add(ba);
+                m += 32;
             }
         }
         for (; m < m4; m++) c = c + ch[m];
