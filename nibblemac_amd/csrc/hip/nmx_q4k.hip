@@ -1002,7 +1002,9 @@ void launch_head(hipStream_t st, unsigned blocks, const Seg &s, int n, int v0, c
 }
 
 /* q4k_head_k for one matrix with argmax keys at 1, 2, 4 or 8 superblocks per row; false when
- * the shape is not one of those (q4k_mvx_k then, same results). */
+ * the shape is not one of those (q4k_mvx_k then, same results). 8 vectors at 8 superblocks in
+ * 16-wave workgroups would need more than the 128 registers a wave may hold there (the
+ * compiler spills), so that shape takes q4k_mvx_k too. */
 template <int NV>
 bool try_head(hipStream_t st, const SegTable &tab, int cols, int n, int v0, const int8_t *q,
               const float *d, const float *fs, unsigned long long *am, int wpg, const HeadCopy &hc) {
@@ -1014,7 +1016,15 @@ bool try_head(hipStream_t st, const SegTable &tab, int cols, int n, int v0, cons
     case 256: NMX_HEAD(1); return true;
     case 512: NMX_HEAD(2); return true;
     case 1024: NMX_HEAD(4); return true;
-    case 2048: NMX_HEAD(8); return true;
+    case 2048:
+        if constexpr (NV < 8) {
+            NMX_HEAD(8);
+            return true;
+        } else {
+            if (wpg == 16) return false; /* q4k_mvx_k */
+            launch_head<NV, 8, 4>(st, blocks, s, n, v0, q, d, fs, am, hc);
+            return true;
+        }
     default: return false;
     }
 #undef NMX_HEAD

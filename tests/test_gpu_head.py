@@ -122,6 +122,27 @@ def test_head_widths_and_no_logits(dev, n):
     assert np.array_equal(out[2:], am)
 
 
+@pytest.mark.parametrize("n", [3, 5, 8])
+def test_head_2048_cols_widths(dev, n):
+    """A 2048-column head (8 superblocks per row): the one-launch head at 3-7 rows, and at 8 rows
+    the row-per-lane matrix-core kernel it falls back to in 16-wave workgroups; logits
+    bit-exact, argmax and acceptance equal."""
+    print(f"[case] head 2048 cols n={n}", flush=True)
+    rng = np.random.default_rng(70 + n)
+    rows, cols = 16384, 2048
+    W = quantized_head(rng, rows, cols)
+    X = rng.standard_normal((n, cols)).astype(np.float32)
+    q, d, fs = oracle.quant_a8(X)
+    ref = oracle.q4k_matmul(W, rows, cols, q, d, fs, n, threads=8)
+    am = np.array([oracle.argmax(ref[t]) for t in range(n)], np.int32)
+    drafts = planted_drafts(am, n // 2, n - 1)
+    a_ref, bonus_ref, _ = oracle.accept(ref, drafts)
+    out, logits = run_head(dev, W, rows, cols, X, drafts)
+    assert_bits_equal(logits, ref, f"logits 2048 cols n={n}")
+    assert out[0] == a_ref and out[1] == bonus_ref
+    assert np.array_equal(out[2:], am)
+
+
 def test_head_accept_graph_replays_reuse_work(dev):
     """The fused argmax keeps its device-wide state in the caller's work buffer and leaves it
     reset: consecutive calls and several replays of one captured graph (with eager uploads of new
