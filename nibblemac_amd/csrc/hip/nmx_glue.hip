@@ -606,6 +606,69 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
     }
 }
 
+/* acc += x[0] + ... + x[n-1] in order, x[i] = p[i * stride] in LDS, with the reads of 3
+ * batches of 8 in flight ahead of the adds (at most 16 LDS reads outstanding). Each batch is
+ * four register pairs: two reads of one pair merge into one ds_read2 that lands in the pair
+ * itself, so the loop-carried batches need no register copies (with scalar batches the
+ * merged reads landed in fresh registers and were copied at the loop's end, which waited for
+ * every read in flight). The scheduling barriers keep each batch's reads where they are
+ * issued: left alone, the scheduler sinks them to just before their adds. */
+__device__ __forceinline__ void pv_load8(float2 (&X)[4], const float *p, int stride, int r) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) X[u] = make_float2(p[(r + 2 * u) * stride], p[(r + 2 * u + 1) * stride]);
+}
+
+__device__ __forceinline__ float pv_add8(float acc, const float2 (&X)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        acc = acc + X[u].x;
+        acc = acc + X[u].y;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float pv_chain(float acc, const float *p, int stride, int n) {
+    int r = 0;
+    if (n >= 32) {
+        float2 A[4], B[4], C[4], D[4];
+        pv_load8(A, p, stride, 0);
+        pv_load8(B, p, stride, 8);
+        pv_load8(C, p, stride, 16);
+        for (; r + 32 <= n; r += 32) {
+            /* A, B, C = rows r .. r+23 loaded; reads past n are clamped (not used) */
+            const int d0 = r + 24, a0 = r + 40 <= n ? r + 32 : r, b0 = r + 48 <= n ? r + 40 : r,
+                      c0 = r + 56 <= n ? r + 48 : r;
+            pv_load8(D, p, stride, d0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_add8(acc, A);
+            pv_load8(A, p, stride, a0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_add8(acc, B);
+            pv_load8(B, p, stride, b0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_add8(acc, C);
+            pv_load8(C, p, stride, c0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_add8(acc, D);
+        }
+        /* A, B, C hold r .. r+23 when those are in range */
+        if (r + 8 <= n) {
+            acc = pv_add8(acc, A);
+            r += 8;
+            if (r + 8 <= n) {
+                acc = pv_add8(acc, B);
+                r += 8;
+                if (r + 8 <= n) {
+                    acc = pv_add8(acc, C);
+                    r += 8;
+                }
+            }
+        }
+    }
+    for (; r < n; r++) acc = acc + p[r * stride];
+    return acc;
+}
+
 /* attn_prep_k and attn_score_k in one launch (nmx_attn_fused), for hd = 256 (a thread per
  * element of a row) and at most 4 query heads per KV group. Each workgroup (chunk of CP
  * positions, token t, group g) normalises and rotates the group's query heads of token t
@@ -613,8 +676,13 @@ __global__ __launch_bounds__(256) void attn_score_k(Attn a, float *__restrict__ 
  * operations of attn_prep_k; the keys are rounded to the cache format and back, so each score
  * equals the one read from the cache. The workgroup whose chunk holds token t's own position
  * stores that K row and the V row (each (token, group) once; later passes and the P.V launch
- * read them). The rotated queries are not written back: only the scores use them. */
+ * read them). The rotated queries are not written back: only the scores use them.
+ * Every global read of a workgroup (the queries, the chunk's cache rows, the new keys, the
+ * value row, both norm weights and the RoPE coefficients) is issued at entry, so they share
+ * one memory latency; the threads that hold an element write its square to LDS, and each row's
+ * four chains of the norm only add (pv_chain: reads batched ahead of the adds). */
 constexpr int QK_HD = 256;
+constexpr int QK_NMAX = 8; /* tokens per pass: new key rows of a chunk */
 
 /* max |x| of a row of QK_HD values, one per thread, exact in any order */
 __device__ __forceinline__ float qk_row_amax(float x, float *amx, int slot) {
@@ -632,97 +700,112 @@ __global__ __launch_bounds__(256) void attn_qk_k(const float *__restrict__ q_in,
                                                  const float *__restrict__ v_in, void *kc,
                                                  int nh, int nkv, int pos_off, int max_ctx,
                                                  Attn a, float *__restrict__ sc) {
-    constexpr int HD = QK_HD, LP = 64 / CP, CPL = 16 / LP, RS = HD + 4, F4 = HD / 4;
+    constexpr int HD = QK_HD, LP = 64 / CP, CPL = 16 / LP, RS = HD + 4, F4 = HD / 4,
+                  OLD4 = CP * F4 / 256; /* float4 reads of cache rows per thread */
+    static_assert(CP * F4 % 256 == 0 && HD / 4 <= 256, "attn_qk_k tiling");
     extern __shared__ float4 smem4[];
-    __shared__ float part[(4 + CP) * 4]; /* partial sums of squares, 4 per row */
-    __shared__ float rn[4 + CP];         /* 1 / rms of each row */
-    __shared__ float amx[(CP + 1) * 4];  /* int8 cache: per (row, wave) max |x| */
+    __shared__ float part[(4 + QK_NMAX) * 4]; /* partial sums of squares, 4 per row */
+    __shared__ float rn[4 + QK_NMAX];         /* 1 / rms of each row */
+    __shared__ float amx[(CP + 1) * 4];       /* int8 cache: per (row, wave) max |x| */
     const int i = threadIdx.x, lane = i & 63, w = i >> 6;
     const int rep = nh / nkv, h2 = a.rot / 2;
     const int t = blockIdx.y, g = blockIdx.z, p0 = blockIdx.x * CP;
     float *ks = (float *)smem4; /* [CP][RS] key rows of the chunk, as the cache gives them */
     float *qs = ks + CP * RS;   /* [4][HD] rotated queries */
-    float *qw = qs + 4 * HD;    /* [4][HD] queries being normalised */
-    float *kw = qw + 4 * HD;    /* [CP][HD] new keys being normalised */
-    /* the queries first (their address does not wait for the position) */
+    float *qw = qs + 4 * HD;    /* [4][HD] squares, then normalised queries */
+    float *kw = qw + 4 * HD;    /* [QK_NMAX][HD] squares, then normalised new keys */
+    /* the queries and norm weights first (their addresses do not wait for the position) */
     float qv[4];
 #pragma unroll
     for (int hh = 0; hh < 4; hh++)
         qv[hh] = hh < rep ? q_in[((size_t)t * nh + g * rep + hh) * 2 * HD + i] : 0.0f;
+    const float qn = a.q_norm[i], kn = a.k_norm[i];
     const int pos0 = *posp + pos_off; /* position of token 0 */
     const int np = pos0 + t + 1;
     if (p0 >= np) return;
     const int rows = np - p0 < CP ? np - p0 : CP;
     const int nold = pos0 - p0 <= 0 ? 0 : pos0 - p0 < rows ? pos0 - p0 : rows;
-    const int nnew = rows - nold;
+    const int nnew = rows - nold; /* <= t + 1 <= QK_NMAX (the launch's limit) */
     const bool own = np - p0 <= CP; /* token t's own position is row rows - 1 of the chunk */
     const size_t R0 = (size_t)g * max_ctx + p0;
     const float *ksc = kv_scales<KVT>(kc, a);
-    /* new keys and, for the own row, the values: raw inputs */
-    for (int r = nold; r < rows; r++)
-        kw[r * HD + i] = k_in[(size_t)(p0 + r - pos0) * nkv * HD + g * HD + i];
+    /* new keys (row nold + u of the chunk is token p0 + nold + u - pos0) and, for the own
+     * row, the values: raw inputs */
+    float knw[QK_NMAX];
+#pragma unroll
+    for (int u = 0; u < QK_NMAX; u++)
+        knw[u] = u < nnew ? k_in[(size_t)(p0 + nold + u - pos0) * nkv * HD + g * HD + i] : 0.0f;
     const float vv = own ? v_in[(size_t)t * nkv * HD + g * HD + i] : 0.0f;
-    /* the old rows from the cache */
-    for (int f0 = 0; f0 < nold * F4; f0 += 4 * 256) {
-        float4 b[4];
+    /* the old rows from the cache (element f: float4 f % F4 of row f / F4) */
+    float4 b[OLD4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int f = f0 + u * 256 + i;
-            b[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (f < nold * F4) b[u] = kv_load4<KVT>(kc, R0 + f / F4, HD, 4 * (f % F4), ksc);
-        }
+    for (int u = 0; u < OLD4; u++) {
+        const int f = u * 256 + i;
+        b[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (f < nold * F4) b[u] = kv_load4<KVT>(kc, R0 + f / F4, HD, 4 * (f % F4), ksc);
+    }
+    /* RoPE coefficients of element i at the query's and each new key's position: element
+     * i < h2 pairs with i + h2, element h2 <= i < 2 h2 with i - h2; both use index i mod h2 */
+    const bool rot = i < 2 * h2;
+    const int ri = i < h2 ? i : i - h2;
+    float qc = 0.0f, qsn = 0.0f, kcs[QK_NMAX], ksn[QK_NMAX];
+    if (rot) {
+        qc = a.rcos[(size_t)(pos0 + t) * h2 + ri];
+        qsn = a.rsin[(size_t)(pos0 + t) * h2 + ri];
+    }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int f = f0 + u * 256 + i;
-            if (f < nold * F4) {
-                const int r = f / F4, c4 = f - r * F4;
-                *(float4 *)(ks + r * RS + 4 * c4) = b[u];
-            }
+    for (int u = 0; u < QK_NMAX; u++) {
+        kcs[u] = 0.0f, ksn[u] = 0.0f;
+        if (rot && u < nnew) {
+            kcs[u] = a.rcos[(size_t)(p0 + nold + u) * h2 + ri];
+            ksn[u] = a.rsin[(size_t)(p0 + nold + u) * h2 + ri];
         }
     }
 #pragma unroll
-    for (int hh = 0; hh < 4; hh++) qw[hh * HD + i] = qv[hh];
+    for (int u = 0; u < OLD4; u++) {
+        const int f = u * 256 + i;
+        if (f < nold * F4) {
+            const int r = f / F4, c4 = f - r * F4;
+            *(float4 *)(ks + r * RS + 4 * c4) = b[u];
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) qw[hh * HD + i] = qv[hh] * qv[hh];
+#pragma unroll
+    for (int u = 0; u < QK_NMAX; u++)
+        if (u < nnew) kw[u * HD + i] = knw[u] * knw[u];
     __syncthreads();
     /* RMSNorm of every row (attn_prep_k: 4 partial sums of squares over i = l (mod 4) in i
      * order, combined (c0 + c1) + (c2 + c3), empty tail), rows 0-3 the queries, then the new
-     * keys */
-    for (int x = i; x < (4 + nnew) * 4; x += 256) {
-        const int j = x >> 2, l = x & 3;
-        const float *row = j < 4 ? qw + j * HD : kw + (nold + j - 4) * HD;
-        float c = 0.0f;
-#pragma unroll 8
-        for (int m = 0; m < HD / 4; m++) {
-            const float v = row[4 * m + l];
-            c = c + v * v;
-        }
-        part[x] = c;
+     * keys; at most 48 chains, all in wave 0 */
+    if (i < (4 + nnew) * 4) {
+        const int j = i >> 2, l = i & 3;
+        part[i] = pv_chain(0.0f, (j < 4 ? qw + j * HD : kw + (j - 4) * HD) + l, 4, HD / 4);
     }
     __syncthreads();
-    for (int j = i; j < 4 + nnew; j += 256) {
-        const float *r4 = part + 4 * j;
+    if (i < 4 + nnew) {
+        const float *r4 = part + 4 * i;
         const float ss = ((r4[0] + r4[1]) + (r4[2] + r4[3])) + 0.0f;
-        rn[j] = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        rn[i] = 1.0f / sqrtf(ss / (float)HD + a.eps);
     }
     __syncthreads();
 #pragma unroll
-    for (int hh = 0; hh < 4; hh++) qw[hh * HD + i] = (qw[hh * HD + i] * rn[hh]) * a.q_norm[i];
-    for (int r = nold; r < rows; r++)
-        kw[r * HD + i] = (kw[r * HD + i] * rn[4 + r - nold]) * a.k_norm[i];
+    for (int hh = 0; hh < 4; hh++) qw[hh * HD + i] = (qv[hh] * rn[hh]) * qn;
+#pragma unroll
+    for (int u = 0; u < QK_NMAX; u++)
+        if (u < nnew) kw[u * HD + i] = (knw[u] * rn[4 + u]) * kn;
     __syncthreads();
-    /* RoPE over the first rot elements at each row's position */
-    auto rope = [&](const float *row, int p) {
-        if (i < h2) {
-            const float c = a.rcos[(size_t)p * h2 + i], s = a.rsin[(size_t)p * h2 + i];
-            return row[i] * c - row[i + h2] * s;
-        } else if (i < 2 * h2) {
-            const float c = a.rcos[(size_t)p * h2 + i - h2], s = a.rsin[(size_t)p * h2 + i - h2];
-            return row[i] * c + row[i - h2] * s;
-        }
+    /* RoPE over the first rot elements */
+    auto rope = [&](const float *row, float c, float s) {
+        if (i < h2) return row[i] * c - row[i + h2] * s;
+        if (i < 2 * h2) return row[i] * c + row[i - h2] * s;
         return row[i];
     };
 #pragma unroll
-    for (int hh = 0; hh < 4; hh++) qs[hh * HD + i] = rope(qw + hh * HD, pos0 + t);
-    for (int r = nold; r < rows; r++) ks[r * RS + i] = rope(kw + r * HD, p0 + r);
+    for (int hh = 0; hh < 4; hh++) qs[hh * HD + i] = rope(qw + hh * HD, qc, qsn);
+#pragma unroll
+    for (int u = 0; u < QK_NMAX; u++)
+        if (u < nnew) ks[(nold + u) * RS + i] = rope(kw + u * HD, kcs[u], ksn[u]);
     if constexpr (KVT == KV_I8) {
         /* row maxima of the new keys (and of the own row's values) for their int8 codes */
         __syncthreads(); /* the rotated keys are in ks */
@@ -822,69 +905,6 @@ constexpr int PV_PT2 = 384;         /* positions of each later tile (loaded by w
 constexpr int PV_PER = PV_PT * (PV_DS / 4) / 256;    /* float4 loads per thread, first tile */
 constexpr int PV_PER2 = PV_PT2 * (PV_DS / 4) / 192;  /* per thread of waves 1-3, later tiles */
 
-/* acc += x[0] + ... + x[n-1] in order, x[i] = p[i * stride] in LDS, with the reads of 3
- * batches of 8 in flight ahead of the adds (at most 16 LDS reads outstanding). Each batch is
- * four register pairs: two reads of one pair merge into one ds_read2 that lands in the pair
- * itself, so the loop-carried batches need no register copies (with scalar batches the
- * merged reads landed in fresh registers and were copied at the loop's end, which waited for
- * every read in flight). The scheduling barriers keep each batch's reads where they are
- * issued: left alone, the scheduler sinks them to just before their adds. */
-__device__ __forceinline__ void pv_load8(float2 (&X)[4], const float *p, int stride, int r) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) X[u] = make_float2(p[(r + 2 * u) * stride], p[(r + 2 * u + 1) * stride]);
-}
-
-__device__ __forceinline__ float pv_add8(float acc, const float2 (&X)[4]) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        acc = acc + X[u].x;
-        acc = acc + X[u].y;
-    }
-    return acc;
-}
-
-__device__ __forceinline__ float pv_chain(float acc, const float *p, int stride, int n) {
-    int r = 0;
-    if (n >= 32) {
-        float2 A[4], B[4], C[4], D[4];
-        pv_load8(A, p, stride, 0);
-        pv_load8(B, p, stride, 8);
-        pv_load8(C, p, stride, 16);
-        for (; r + 32 <= n; r += 32) {
-            /* A, B, C = rows r .. r+23 loaded; reads past n are clamped (not used) */
-            const int d0 = r + 24, a0 = r + 40 <= n ? r + 32 : r, b0 = r + 48 <= n ? r + 40 : r,
-                      c0 = r + 56 <= n ? r + 48 : r;
-            pv_load8(D, p, stride, d0);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = pv_add8(acc, A);
-            pv_load8(A, p, stride, a0);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = pv_add8(acc, B);
-            pv_load8(B, p, stride, b0);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = pv_add8(acc, C);
-            pv_load8(C, p, stride, c0);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = pv_add8(acc, D);
-        }
-        /* A, B, C hold r .. r+23 when those are in range */
-        if (r + 8 <= n) {
-            acc = pv_add8(acc, A);
-            r += 8;
-            if (r + 8 <= n) {
-                acc = pv_add8(acc, B);
-                r += 8;
-                if (r + 8 <= n) {
-                    acc = pv_add8(acc, C);
-                    r += 8;
-                }
-            }
-        }
-    }
-    for (; r < n; r++) acc = acc + p[r * stride];
-    return acc;
-}
-
 template <int KVT>
 __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
                                                  const int32_t *__restrict__ posp,
@@ -903,6 +923,8 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
     const float *srow = sc + ((size_t)t * nh + h) * max_ctx;
     const size_t R0 = (size_t)g * max_ctx;
     const float *vsc = kv_scales<KVT>(vc, a);
+    /* the output gate of lane tid < PV_DS (read here so its latency overlaps the tile's) */
+    const float gate = tid < PV_DS ? a.q[((size_t)t * nh + h) * 2 * hd + hd + d0 + tid] : 0.0f;
     /* the scores row, then the first tile's values (element f = u 256 + tid: float4 f % F4 of
      * row f / F4) */
     float bs[4];
@@ -995,10 +1017,8 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
         base = next, rows = rows2;
     }
     if (tid < PV_DS) {
-        const int d = d0 + tid;
-        const float *qrow = a.q + ((size_t)t * nh + h) * 2 * hd;
-        o = o * nmx_sigmoid(qrow[hd + d]);
-        const int col = h * hd + d;
+        o = o * nmx_sigmoid(gate);
+        const int col = h * hd + d0 + tid;
         a.o[(size_t)t * nh * hd + col] = o;
         if (a.aq) a8_block(o, col >> 5, t, a.n, a.aq, a.ad, a.afs);
     }
@@ -1571,13 +1591,13 @@ int launch_pv(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
  * norms, measured slower than the separate launch), the three launches */
 template <int KVT>
 int launch_attn_fused(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
-    if (p->hd != QK_HD || p->nh / p->nkv > 4 || p->n > 8) {
+    if (p->hd != QK_HD || p->nh / p->nkv > 4 || p->n > QK_NMAX) {
         launch_attn_prep<KVT>(ctx, p, a);
         NMX_LAUNCHED(ctx, "attn_prep");
         return launch_attn<KVT>(ctx, p, a);
     }
     constexpr int CP = 32;
-    const size_t lds = ((size_t)CP * (QK_HD + 4) + 8 * (size_t)QK_HD + (size_t)CP * QK_HD) * 4;
+    const size_t lds = ((size_t)CP * (QK_HD + 4) + (8 + (size_t)QK_NMAX) * QK_HD) * 4;
     static bool ready = false; /* idempotent */
     if (!ready) {
         NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_qk_k<CP, KVT>,
