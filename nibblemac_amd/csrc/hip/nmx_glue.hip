@@ -1191,19 +1191,22 @@ __device__ int accept_from_keys(const Commit &a, bool lead) {
     __shared__ unsigned long long red[4][ACC_MAX_N];
     __shared__ int am[ACC_MAX_N], s_dr[ACC_MAX_N], s_vt[64], s_a;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int dr = tid < a.n - 1 ? a.drafts[tid] : 0;
-    const int vv = lead && a.mb && tid < a.nvt ? a.vt[tid] : 0;
     unsigned long long k[ACC_MAX_N];
 #pragma unroll
     for (int v = 0; v < ACC_MAX_N; v++) k[v] = 0ull;
     for (int b = tid; b < a.nkeys; b += 256) {
+        unsigned long long o[ACC_MAX_N]; /* every row's load issued before the first compare */
 #pragma unroll
         for (int v = 0; v < ACC_MAX_N; v++)
-            if (v < a.n) {
-                const unsigned long long o = a.keys[(size_t)v * a.nkeys + b];
-                k[v] = o > k[v] ? o : k[v];
-            }
+            if (v < a.n) o[v] = a.keys[(size_t)v * a.nkeys + b];
+#pragma unroll
+        for (int v = 0; v < ACC_MAX_N; v++)
+            if (v < a.n) k[v] = o[v] > k[v] ? o[v] : k[v];
     }
+    /* the drafts and vt after the keys: loads complete in order, so their LDS stores cannot
+     * hold back the key requests */
+    const int dr = tid < a.n - 1 ? a.drafts[tid] : 0;
+    const int vv = lead && a.mb && tid < a.nvt ? a.vt[tid] : 0;
     if (tid < a.n - 1) s_dr[tid] = dr;
     if (lead && a.mb && tid < a.nvt) s_vt[tid] = vv;
 #pragma unroll
@@ -1246,11 +1249,36 @@ __device__ int accept_from_keys(const Commit &a, bool lead) {
     return s_a;
 }
 
+/* The commit of e = E + 1 tokens per linear layer (one conv channel per thread: the grid
+ * covers C): the conv state rows become rows E .. E + S - 1 of [state after token 0; xin rows
+ * 1 ..], and log rows 1 .. E become the pending rows. Every row a commit can take is requested
+ * before E is known (E <= n - 1 with keys, read from ctl otherwise), so the acceptance's round
+ * trip and these loads overlap, and the commit itself only selects and stores. */
 __global__ __launch_bounds__(256) void commit_k(Commit a) {
+    constexpr int XR = ACC_MAX_N - 1, LR = 4; /* xin rows, log values per thread, in registers */
     const int l = blockIdx.y;
     const bool lead = blockIdx.x == 0 && l == 0;
-    const int E = a.keys ? accept_from_keys(a, lead) : a.ctl[1] - 1;
-    const int tid = blockIdx.x * 256 + threadIdx.x, stride = gridDim.x * 256;
+    const int tid = blockIdx.x * 256 + threadIdx.x, stride = gridDim.x * 256, c = tid;
+    float *st = a.state + (size_t)l * a.S * a.C;
+    float *bk = a.bak ? a.bak + (size_t)l * a.S * a.C : nullptr;
+    const float *src0 = a.redo ? bk : st; /* rows of the state after token 0 */
+    const float *xi = a.xin + (size_t)l * a.cap * a.C;
+    const float *lg = a.log + (size_t)l * a.cap * a.row;
+    float *pd = a.pend + (size_t)l * a.cap * a.row;
+    const int E0 = a.keys ? 0 : a.ctl[1] - 1;
+    const int emax = a.keys ? a.n - 1 : E0; /* the largest E */
+    const bool ch = c < a.C;
+    float old[8], xr[XR], lv[LR];
+#pragma unroll
+    for (int j = 0; j < 8; j++) old[j] = ch && j < a.S ? src0[(size_t)j * a.C + c] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < XR; u++) xr[u] = ch && u < emax ? xi[(size_t)(u + 1) * a.C + c] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < LR; u++) {
+        const int i = tid + u * stride;
+        lv[u] = i < emax * a.row ? lg[a.row + i] : 0.0f;
+    }
+    const int E = a.keys ? accept_from_keys(a, lead) : E0;
     if (E == 0 && !a.redo) { /* e = 1: the state after token 0 is the committed one, no replay
                               * rows, and no later commit of a smaller e can need the kept rows */
         if (l == 0 && tid == 0) {
@@ -1259,18 +1287,22 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
         }
         return;
     }
-    float *st = a.state + (size_t)l * a.S * a.C;
-    float *bk = a.bak ? a.bak + (size_t)l * a.S * a.C : nullptr;
-    const float *src0 = a.redo ? bk : st; /* rows of the state after token 0 */
-    const float *xi = a.xin + (size_t)l * a.cap * a.C;
-    for (int c = tid; c < a.C; c += stride) {
-        float old[8], nv[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) old[j] = j < a.S ? src0[(size_t)j * a.C + c] : 0.0f;
+    if (ch) {
+        float nv[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int src = j + E;
-            nv[j] = j >= a.S ? 0.0f : src < a.S ? old[src] : xi[(size_t)(src - a.S + 1) * a.C + c];
+            const int src = j + E; /* row src of [state after token 0 (S rows); xin rows 1 ..] */
+            float x = 0.0f;
+            if (src < a.S) {
+#pragma unroll
+                for (int r = 0; r < 8; r++) x = r == src ? old[r] : x;
+            } else if (src - a.S < XR) {
+#pragma unroll
+                for (int u = 0; u < XR; u++) x = u == src - a.S ? xr[u] : x;
+            } else {
+                x = xi[(size_t)(src - a.S + 1) * a.C + c];
+            }
+            nv[j] = j < a.S ? x : 0.0f;
         }
         if (bk && !a.redo) {
 #pragma unroll
@@ -1281,9 +1313,12 @@ __global__ __launch_bounds__(256) void commit_k(Commit a) {
         for (int j = 0; j < 8; j++)
             if (j < a.S) st[(size_t)j * a.C + c] = nv[j];
     }
-    const float *lg = a.log + (size_t)l * a.cap * a.row;
-    float *pd = a.pend + (size_t)l * a.cap * a.row;
-    for (int i = tid; i < E * a.row; i += stride) pd[i] = lg[a.row + i];
+#pragma unroll
+    for (int u = 0; u < LR; u++) {
+        const int i = tid + u * stride;
+        if (i < E * a.row) pd[i] = lv[u]; /* E <= emax */
+    }
+    for (int i = tid + LR * stride; i < E * a.row; i += stride) pd[i] = lg[a.row + i];
     if (l == 0 && tid == 0) {
         a.ctl[2] = E;
         if (a.vt && !a.keys) a.vt[0] = a.vt[E + 1]; /* cur <- vt[e] */

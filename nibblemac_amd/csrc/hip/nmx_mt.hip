@@ -183,9 +183,11 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     /* ---- phase 0a: first round of activation / norm-input loads, issued before the weight
      * loads so that waiting for them does not wait for the weights ---- */
     const int nq = nb * NV * 2, ns = nb * NV; /* 16-byte code halves; (block, vector) pairs */
-    /* staged per thread and round: NQB code halves, NDB (d, fsum) pairs (wide workgroups of
-     * one-block units need fewer) */
-    constexpr int NQB = BPU == 1 ? 2 : 8, NDB = BPU == 1 ? 1 : 4;
+    /* staged per thread and round: NQB code halves, NDB (d, fsum) pairs. One-block units have
+     * T >= 8 R nsb threads, so a round needs at most nq / T <= 2 NV / R halves and NV / R pairs
+     * per thread: one round for every pass of up to 8 vectors at R >= 4 rows (a second
+     * round's loads would be issued only after the first round's have landed) */
+    constexpr int NQB = BPU == 1 ? 4 : 8, NDB = BPU == 1 ? 2 : 4;
     int4 buf[NQB];
     float bd[NDB], bf[NDB];
     if constexpr (!NORM) {
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
         for (int u = 0; u < NDB; u++) {
             const int e = u * T + tid;
             const int b = e / NV, v = e - b * NV;
-            const size_t gi = e < ns ? (size_t)b * n + v0 + v : 0;
+            const int gi = e < ns ? b * n + v0 + v : 0; /* nb n < 2^31 */
             bd[u] = d[gi];
             bf[u] = fs[gi];
         }
@@ -302,7 +304,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
                 for (int u = 0; u < NDB; u++) {
                     const int e = (r0 * NDB + u) * T + tid;
                     const int b = e / NV, v = e - b * NV;
-                    const size_t gi = e < ns ? (size_t)b * n + v0 + v : 0;
+                    const int gi = e < ns ? b * n + v0 + v : 0; /* nb n < 2^31 */
                     bd[u] = d[gi];
                     bf[u] = fs[gi];
                 }

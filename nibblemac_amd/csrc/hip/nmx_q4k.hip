@@ -618,20 +618,19 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
     __shared__ unsigned long long red[16][8];
     __shared__ int am[64], sdr[64], svt[1024];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int dr = drafts && tid < n - 1 ? drafts[tid] : 0;
-    const int vv = fc.mb && tid < fc.nvt ? fc.vt[tid] : 0;
     bool staged = false;
     for (int t0 = 0; t0 < n; t0 += 8) {
         unsigned long long k[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) k[j] = 0ull;
         for (int b = tid; b < nblk; b += 1024) {
+            unsigned long long o[8]; /* every row's load issued before the first compare */
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                if (t0 + j < n) {
-                    const unsigned long long o = keys[(size_t)(t0 + j) * nblk + b];
-                    k[j] = o > k[j] ? o : k[j];
-                }
+                if (t0 + j < n) o[j] = keys[(size_t)(t0 + j) * nblk + b];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (t0 + j < n) k[j] = o[j] > k[j] ? o[j] : k[j];
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -639,7 +638,10 @@ __global__ __launch_bounds__(1024) void head_finish_k(const unsigned long long *
             k[j] = nmx_max_u64_wave(k[j]);
             if (lane == 0) red[wv][j] = k[j];
         }
-        if (!staged) { /* the keys' loads waited for these (issued first) */
+        if (!staged) { /* the drafts and vt after the first keys: loads complete in order, so
+                        * their LDS stores cannot hold back the key requests */
+            const int dr = drafts && tid < n - 1 ? drafts[tid] : 0;
+            const int vv = fc.mb && tid < fc.nvt ? fc.vt[tid] : 0;
             if (tid < n - 1) sdr[tid] = dr;
             if (tid < fc.nvt) svt[tid] = vv;
             staged = true;
