@@ -193,10 +193,11 @@ __global__ __launch_bounds__(256) void rmsnorm4_pair_k(RmsSet s0, RmsSet s1, int
     const RmsSet &s = blockIdx.y ? s1 : s0;
     const int row = blockIdx.x;
     if (s.keys && row == n - 1) { /* uniform: the token from the keys, by every wave */
+        float4 v[P4], a[P4], wv[P4];
+        rms4_load_w<P4>(s.w, cols, wv); /* before the keys the row waits for */
         const int tk = nmx_keys_token(s.keys, s.nkeys);
         if (threadIdx.x == 0) s.tok_w[row] = tk;
-        float4 v[P4], a[P4], wv[P4];
-        rms4_load<P4>(nullptr, nullptr, s.w, cols, v, a, wv, s.E, tk);
+        rms4_load<P4, true>(nullptr, nullptr, s.w, cols, v, a, wv, s.E, tk);
         rms4_finish<P4>(v, a, wv, false, s.xo ? s.xo + (size_t)row * s.xo_stride : nullptr, cols,
                         eps, s.y ? s.y + (size_t)row * s.y_stride : nullptr, s.q, s.d, s.fs, n,
                         row, sq, red);

@@ -68,6 +68,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[8 * 64];
     __shared__ float spdec[MIX_TB]; /* decays of the pending batch (red serves the L2 norms) */
+    __shared__ uint64_t sx2[32];    /* the gate exp's 2^(i/32) table */
     constexpr int DK = DK4 * 4, PAD = DK4 + 4, ROW = 4 * PAD;
     const int n = n_, dv = dv_, heads = a.heads;
     const int h = blockIdx.x, tid = threadIdx.x, T = 4 * dv, c = tid & 3; /* the launch's size */
@@ -126,6 +127,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     } else if (gy >= n && gy < 2 * n) {
         ga = b_in[(size_t)(gy - n) * g_stride + h];
     }
+    const uint64_t x2v = tid < 32 ? nmx_exp2_32[tid] : 0ull;
     /* z of the first tokens and the norm weight, as float4 (x4 = tid over [n0][dv / 4]) */
     const bool z_on = 4 * tid < n0 * dv, w_on = 4 * tid < dv;
     float4 zq = make_float4(0.f, 0.f, 0.f, 0.f), wq = zq;
@@ -160,6 +162,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     if (tid < pb0) spdec[tid] = pdec;
     if (z_on) *(float4 *)(sz + 4 * tid) = zq;
     if (w_on) *(float4 *)(sw + 4 * tid) = wq;
+    if (tid < 32) sx2[tid] = x2v;
     __syncthreads();
 
     /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv), one per thread ---- */
@@ -213,13 +216,13 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
                 const float av = first ? ga : a_in[(size_t)x * g_stride + h];
                 const float Ai = first ? gA : a.A ? a.A[h] : a.A_log[h];
                 const float dt = first ? gdt : a.dt_bias[h];
-                const float A = a.A ? Ai : -nmx_gate_expf(Ai);
+                const float A = a.A ? Ai : -nmx_gate_expf_t(Ai, sx2);
                 float sp_ = av + dt;
-                sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf(sp_));
-                sdec[x] = nmx_gate_expf(A * sp_);
+                sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf_t(sp_, sx2));
+                sdec[x] = nmx_gate_expf_t(A * sp_, sx2);
             } else {
                 const float b = first ? ga : b_in[(size_t)(x - n) * g_stride + h];
-                sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf(-b));
+                sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf_t(-b, sx2));
             }
         }
     }

@@ -52,7 +52,9 @@ static __device__ __constant__ const uint64_t nmx_exp2_32[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float nmx_gate_expf(float x) {
+/* tab: the 32 entries above, from this constant copy or from a copy in LDS (a kernel that
+ * stages them at entry turns each lookup's memory round trip into an LDS read) */
+__device__ __forceinline__ float nmx_gate_expf_t(float x, const uint64_t *tab) {
     const uint32_t top = (__float_as_uint(x) >> 20) & 0x7ffu;
     if (top >= (0x42b00000u >> 20)) { /* |x| >= 88, inf or nan */
         if (__float_as_uint(x) == 0xff800000u) return 0.0f;
@@ -65,13 +67,15 @@ __device__ __forceinline__ float nmx_gate_expf(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= 0x1.8p+52;
     const double r = __builtin_fma(0x1.71547652b82fep+5, xd, -kd);
-    const uint64_t t = nmx_exp2_32[ki % 32] + (ki << 47);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
     const double s = __longlong_as_double((long long)t);
     const double z = __builtin_fma(0x1.c6af84b912394p-20, r, 0x1.ebfce50fac4f3p-13), r2 = r * r;
     double y = __builtin_fma(0x1.62e42ff0c52d6p-6, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
 }
+
+__device__ __forceinline__ float nmx_gate_expf(float x) { return nmx_gate_expf_t(x, nmx_exp2_32); }
 
 __device__ __forceinline__ float nmx_gate_log1pf(float x) {
     const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
@@ -138,9 +142,12 @@ __device__ __forceinline__ float nmx_half(const uint8_t *p) {
     return (float)f;
 }
 
-/* value j of a packed 6-bit array (engine/src/kern_act.c:47-50) */
+/* value j of a packed 6-bit array (engine/src/kern_act.c:47-50): low nibble of byte j for
+ * j < 16, high nibble of byte j - 16 otherwise, and bits 2 (j / 8) of byte 16 + j % 8. Both
+ * reads are unconditional, so they are requested together (a select between two loads waited
+ * for each one in turn). */
 __device__ __forceinline__ int nmx_get6(const uint8_t *p, int j) {
-    const int lo = j < 16 ? (p[j] & 15) : (p[j - 16] >> 4);
+    const int lo = (p[j & 15] >> (4 * (j >> 4))) & 15;
     return lo | (((p[16 + (j & 7)] >> (2 * (j >> 3))) & 3) << 4);
 }
 

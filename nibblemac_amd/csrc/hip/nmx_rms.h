@@ -112,18 +112,30 @@ __device__ __forceinline__ float4 embed4(const uint8_t *E, int row, int cols, in
 
 /* rms4_row in two steps: rms4_load requests the row (x, add, w; P4 float4 per thread, indexes
  * clamped in-bounds) so that a caller can issue other loads before the first use, and
- * rms4_finish adds, squares, reduces and writes y and the A8 blocks. */
+ * rms4_finish adds, squares, reduces and writes y and the A8 blocks. rms4_load_w requests the
+ * norm weights alone, for callers whose row address waits for a load (a token); rms4_load<P4,
+ * true> then leaves wv as it is. */
 template <int P4>
+__device__ __forceinline__ void rms4_load_w(const float *w, int cols, float4 (&wv)[P4]) {
+    const int tid = threadIdx.x, c4 = cols >> 2;
+#pragma unroll
+    for (int u = 0; u < P4; u++) {
+        const int j = tid + 256 * u, jc = j < c4 ? j : c4 - 1;
+        wv[u] = ((const float4 *)w)[jc];
+    }
+}
+
+template <int P4, bool HAVE_W = false>
 __device__ __forceinline__ void rms4_load(const float *xr, const float *ar, const float *w,
                                           int cols, float4 (&v)[P4], float4 (&a)[P4],
                                           float4 (&wv)[P4], const uint8_t *E = nullptr,
                                           int er = 0) {
     const int tid = threadIdx.x, c4 = cols >> 2;
+    if constexpr (!HAVE_W) rms4_load_w<P4>(w, cols, wv);
 #pragma unroll
     for (int u = 0; u < P4; u++) {
         const int j = tid + 256 * u, jc = j < c4 ? j : c4 - 1;
         v[u] = E ? embed4(E, er, cols, jc) : ((const float4 *)xr)[jc];
-        wv[u] = ((const float4 *)w)[jc];
         a[u] = ar ? ((const float4 *)ar)[jc] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 }
@@ -177,8 +189,9 @@ __device__ __forceinline__ void rms4_row(const float *x, int x_stride, const flo
                                          int row, float *sq, float *red,
                                          const uint8_t *E = nullptr, const int32_t *tok = nullptr) {
     float4 v[P4], a[P4], wv[P4];
-    rms4_load<P4>(x + (size_t)row * x_stride, add ? add + (size_t)row * add_stride : nullptr, w,
-                  cols, v, a, wv, E, E ? tok[row] : 0);
+    rms4_load_w<P4>(w, cols, wv); /* before the token the embedding row waits for */
+    rms4_load<P4, true>(x + (size_t)row * x_stride, add ? add + (size_t)row * add_stride : nullptr,
+                        w, cols, v, a, wv, E, E ? tok[row] : 0);
     rms4_finish<P4>(v, a, wv, add != nullptr, xo ? xo + (size_t)row * xo_stride : nullptr, cols,
                     eps, y ? y + (size_t)row * y_stride : nullptr, q, d, fs, n, row, sq, red);
 }
