@@ -670,6 +670,55 @@ __device__ __forceinline__ float pv_chain(float acc, const float *p, int stride,
     return acc;
 }
 
+/* acc += x[0] + ... + x[n-1] in order, x contiguous in LDS and 16-byte aligned: the terms
+ * arrive four per ds_read_b128 with immediate offsets, two sets of 32 taking turns (the next
+ * set requested before the current one is added), so the chain's wave issues about 0.3 other
+ * instructions per dependent add (pv_chain, strided, about 1.3). */
+__device__ __forceinline__ float pv_chain4(float acc, const float *x, int n) {
+    auto fetch = [&](float4 (&b)[8], int r0) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) b[u] = *(const float4 *)(x + r0 + 4 * u);
+    };
+    auto add = [&](const float4 (&b)[8]) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            acc = acc + b[u].x;
+            acc = acc + b[u].y;
+            acc = acc + b[u].z;
+            acc = acc + b[u].w;
+        }
+    };
+    int r = 0;
+    if (n >= 32) {
+        float4 ba[8], bb[8];
+        fetch(ba, 0);
+        for (; r + 64 <= n; r += 64) {
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(bb, r + 32);
+            __builtin_amdgcn_sched_barrier(0);
+            add(ba);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(ba, r + 96 <= n ? r + 64 : r); /* clamped: not used past n */
+            __builtin_amdgcn_sched_barrier(0);
+            add(bb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (r + 32 <= n) { /* ba holds terms r .. r + 31 */
+            add(ba);
+            r += 32;
+        }
+    }
+    for (; r + 4 <= n; r += 4) {
+        const float4 v = *(const float4 *)(x + r);
+        acc = acc + v.x;
+        acc = acc + v.y;
+        acc = acc + v.z;
+        acc = acc + v.w;
+    }
+    for (; r < n; r++) acc = acc + x[r];
+    return acc;
+}
+
 /* attn_prep_k and attn_score_k in one launch (nmx_attn_fused), for hd = 256 (a thread per
  * element of a row) and at most 4 query heads per KV group. Each workgroup (chunk of CP
  * positions, token t, group g) normalises and rotates the group's query heads of token t
@@ -893,18 +942,30 @@ __global__ __launch_bounds__(256) void attn_qk_k(const float *__restrict__ q_in,
  * (dims, KV group) i mod S and (query head of the group, token) i / S, S = hd / PV_DS x nkv:
  * consecutive workgroups go to different XCDs (round-robin), so the workgroups reading one
  * slice share one XCD's L2. The scores row and the first PV_PT value rows are requested at
- * entry; each tile lands in LDS as w_p v_p[d] (the products the chain adds). Wave 0's lanes
- * run the chains (one per dimension), reading batches of 8 positions ahead of the adds; while
- * wave 0 runs a tile's chains, waves 1-3 load the next PV_PT2 rows. A dependent fp32 add costs
- * 11-17 cycles in wave 0, so the chains bound the kernel; 32 dims per workgroup give twice
- * the workgroups of 64, and a first tile of PV_PT positions keeps a workgroup's LDS under half
- * of the CU's for contexts up to 1024 positions, so two workgroups share a CU and a 5-token
- * verify pass (320 workgroups) runs in one round. */
+ * entry; the scores and then the exponentials sit in LDS chain-major (each partial sum's
+ * terms contiguous), and each tile lands in LDS as w_p v_p[d] (the products the chain adds),
+ * one row per dimension. Wave 0's lanes run the chains (one per dimension), four terms per
+ * 16-byte read, the next 32 requested ahead of the adds; while wave 0 runs a tile's chains,
+ * waves 1-3 load the next PV_PT2 rows. The dependent fp32 adds bound the kernel; 32 dims per
+ * workgroup give twice the workgroups of 64, and a first tile of PV_PT positions keeps a
+ * workgroup's LDS under half of the CU's for contexts up to 1024 positions, so two workgroups
+ * share a CU and a 5-token verify pass (320 workgroups) runs in one round. */
 constexpr int PV_DS = 32;           /* output dims per workgroup: one A8 block */
 constexpr int PV_PT = 576;          /* positions of the first tile */
 constexpr int PV_PT2 = 384;         /* positions of each later tile (loaded by waves 1-3) */
 constexpr int PV_PER = PV_PT * (PV_DS / 4) / 256;    /* float4 loads per thread, first tile */
 constexpr int PV_PER2 = PV_PT2 * (PV_DS / 4) / 192;  /* per thread of waves 1-3, later tiles */
+/* attn_pv_k keeps a tile's products w_p v_p[d] one row per output dim (PV_DS rows of PV_RS,
+ * positions contiguous): 16-byte aligned rows 4 words apart modulo 64 banks, so the chain
+ * lanes' 16-byte reads are conflict-free */
+constexpr int PV_RS = PV_PT + 4;
+
+/* Chain-major index of position p of an np-position row, m4 = np / 4, s4 the row stride:
+ * the terms of partial sum l = p % 4 of the ordered softmax sum contiguous, the tail after the
+ * four rows. */
+__device__ __forceinline__ int pv_cm(int p, int m4, int s4) {
+    return p < 4 * m4 ? (p & 3) * s4 + (p >> 2) : 4 * s4 + (p - 4 * m4);
+}
 
 template <int KVT>
 __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
@@ -919,8 +980,9 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
     const int d0 = (sl % (hd / PV_DS)) * PV_DS, g = sl / (hd / PV_DS);
     const int h = g * rep + k % rep, t = k / rep;
     const int np = *posp + pos_off + t + 1;
-    float *att = (float *)smem4;                    /* [max_ctx] */
-    float *vt = att + ((max_ctx + 3) & ~3);       /* [PV_PT][PV_DS] */
+    const int m4 = np >> 2, s4 = cm_stride(max_ctx);
+    float *ecm = (float *)smem4; /* [4 s4 + 4] scores, then exponentials, chain-major */
+    float *vt = ecm + 4 * s4 + 4; /* [PV_DS][PV_RS] products of a tile, one row per dim */
     const float *srow = sc + ((size_t)t * nh + h) * max_ctx;
     const size_t R0 = (size_t)g * max_ctx;
     const float *vsc = kv_scales<KVT>(vc, a);
@@ -945,46 +1007,48 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int p = u * 256 + tid;
-        if (p < np) att[p] = bs[u];
+        if (p < np) ecm[pv_cm(p, m4, s4)] = bs[u];
     }
     for (int p0 = 4 * 256; p0 < np; p0 += 256) { /* contexts beyond 1024 positions */
         const int p = p0 + tid;
-        if (p < np) att[p] = srow[p];
+        if (p < np) ecm[pv_cm(p, m4, s4)] = srow[p];
     }
     __syncthreads();
     float mx = -INFINITY;
-    for (int p = tid; p < np; p += 256) mx = fmaxf(mx, att[p]);
+    for (int p = tid; p < np; p += 256) mx = fmaxf(mx, ecm[pv_cm(p, m4, s4)]);
     mx = nmx_max_f32_wave(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
-    for (int p = tid; p < np; p += 256) att[p] = nmx_expf_cephes(att[p] - mx);
+    for (int p = tid; p < np; p += 256) {
+        const int i = pv_cm(p, m4, s4);
+        ecm[i] = nmx_expf_cephes(ecm[i] - mx);
+    }
     __syncthreads();
     /* 4 partial sums over e[4m + l] (m ascending) + the tail, in the reference's order */
-    {
-        const int m4 = np >> 2;
-        if (tid < 4) red[tid] = pv_chain(0.0f, att + tid, 4, m4);
-        else if (tid == 4) {
-            float tl = 0.0f;
-            for (int i = 4 * m4; i < np; i++) tl = tl + att[i];
-            red[4] = tl;
-        }
+    if (tid < 4) {
+        red[tid] = pv_chain4(0.0f, ecm + tid * s4, m4);
+    } else if (tid == 4) {
+        float tl = 0.0f;
+        for (int i = 0; i < np - 4 * m4; i++) tl = tl + ecm[4 * s4 + i];
+        red[4] = tl;
     }
     __syncthreads();
     const float inv = 1.0f / (((red[0] + red[1]) + (red[2] + red[3])) + red[4]);
-    for (int p = tid; p < np; p += 256) att[p] = att[p] * inv;
-
+    /* w_p = e_p * (1 / sum); the tile's rows of dims 4 c4 .. 4 c4 + 3 get w_p v_p[d] */
+    auto put = [&](int r, int c4, float w, float4 v) {
+        float *q = vt + 4 * c4 * PV_RS + r;
+        q[0] = w * v.x;
+        q[PV_RS] = w * v.y;
+        q[2 * PV_RS] = w * v.z;
+        q[3 * PV_RS] = w * v.w;
+    };
     float o = 0.0f;
-    __syncthreads(); /* att scaled */
 #pragma unroll
     for (int u = 0; u < PV_PER; u++) {
         const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
-        if (r < rows0) {
-            const float w = att[r];
-            *(float4 *)(vt + r * PV_DS + 4 * c4) =
-                make_float4(w * vb[u].x, w * vb[u].y, w * vb[u].z, w * vb[u].w);
-        }
+        if (r < rows0) put(r, c4, ecm[pv_cm(r, m4, s4)] * inv, vb[u]);
     }
     __syncthreads();
     for (int base = 0, rows = rows0; base < np;) {
@@ -999,7 +1063,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
                 if (r < rows2) nb[u] = kv_load4<KVT>(vc, R0 + next + r, hd, d0 + 4 * c4, vsc);
             }
         }
-        if (tid < PV_DS) o = pv_chain(o, vt + tid, PV_DS, rows);
+        if (tid < PV_DS) o = pv_chain4(o, vt + tid * PV_RS, rows);
         __syncthreads(); /* the chains of this tile are done */
         if (next >= np) break;
         if (tid >= 64) {
@@ -1007,11 +1071,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
 #pragma unroll
             for (int u = 0; u < PV_PER2; u++) {
                 const int f = u * 192 + f0, r = f / F4, c4 = f - r * F4;
-                if (r < rows2) {
-                    const float w = att[next + r];
-                    *(float4 *)(vt + r * PV_DS + 4 * c4) =
-                        make_float4(w * nb[u].x, w * nb[u].y, w * nb[u].z, w * nb[u].w);
-                }
+                if (r < rows2) put(r, c4, ecm[pv_cm(next + r, m4, s4)] * inv, nb[u]);
             }
         }
         __syncthreads();
@@ -1603,12 +1663,13 @@ int launch_attn(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
 template <int KVT>
 int launch_pv(nmx_ctx *ctx, const nmx_attn_args *p, const Attn &a) {
     const unsigned pgrid = (unsigned)((p->hd / PV_DS) * p->nh * p->n);
-    const size_t plds = ((size_t)((p->max_ctx + 3) & ~3) + (size_t)PV_PT * PV_DS) * 4;
+    const size_t plds = ((size_t)4 * cm_stride(p->max_ctx) + 4 + (size_t)PV_DS * PV_RS) * 4;
     static bool pv_ready = false; /* idempotent */
     if (!pv_ready) {
         NMX_HIP(ctx, hipFuncSetAttribute((const void *)attn_pv_k<KVT>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)((PV_ATT_MAX + (size_t)PV_PT * PV_DS) * 4)));
+                                         (int)((4 * (size_t)cm_stride(PV_ATT_MAX) + 4 +
+                                                (size_t)PV_DS * PV_RS) * 4)));
         pv_ready = true;
     }
     if (p->max_ctx > PV_ATT_MAX) {
