@@ -266,12 +266,13 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     const uint8_t *wbase = wseg == 0 ? W0 : tab.s[wseg].W;
     const uint4 *p = (const uint4 *)(wbase + ((size_t)(lrow >> 2) * nsb + u_sb) * 576);
     const int ti = lrow & 3;
-    uint4 a0 = {}, a1 = {}, a2 = {}, a3 = {}, c[BPU] = {};
-    if (has_unit) {
-        a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+    /* unconditional (a thread without a unit reads unit 0's bytes, in bounds, and ignores
+     * them): loads in a branch make every later wait also wait for them, so the norm
+     * prologue would hold its squares until the weights had landed */
+    const uint4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+    uint4 c[BPU];
 #pragma unroll
-        for (int k = 0; k < BPU; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
-    }
+    for (int k = 0; k < BPU; k++) c[k] = p[4 + 4 * (u_k0 + k) + ti];
 
     float ev32[PAIR ? 32 : 1];
     if constexpr (PAIR) {
