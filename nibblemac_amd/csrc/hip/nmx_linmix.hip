@@ -353,10 +353,10 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
         srn[2 * n + t] = 1.0f / sqrtf(ss / (float)dv + a.eps);
     }
     __syncthreads();
-    for (int x = tid; x < n * dv; x += T) { /* a 32-lane half-wave holds one A8 block */
+    auto out = [&](int x, float z) { /* a 32-lane half-wave holds one A8 block */
         const int t = x / dv, jj = x - t * dv;
         const float ov = so[t * dv + jj];
-        const float gz = nmx_silu(t < n0 ? sz[x] : z_in[(size_t)t * z_stride + h * dv + jj]);
+        const float gz = nmx_silu(z);
         float yv = (ov * srn[2 * n + t]) * sw[jj];
         yv = yv * gz;
         const int col = h * dv + jj;
@@ -365,6 +365,14 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
             const size_t u = (size_t)(col >> 5) * n + t;
             nmx_a8_store(yv, a.aq + u * 32, a.ad + u, a.afs + u);
         }
+    };
+    /* z of the first n0 tokens from LDS, of later ones from memory, in two loops: one load
+     * through a pointer that may be either is a generic load, and a wait for it waits for every
+     * memory operation in flight, the state and log stores included */
+    for (int x = tid; x < n0 * dv; x += T) out(x, sz[x]);
+    for (int x = n0 * dv + tid; x < n * dv; x += T) {
+        const int t = x / dv, jj = x - t * dv;
+        out(x, z_in[(size_t)t * z_stride + h * dv + jj]);
     }
 }
 

@@ -155,7 +155,12 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     __shared__ float red[(PAIR ? 10 : 5) * MT_MAX_NV];
     const int tid = threadIdx.x;
     const int8_t *q = (const int8_t *)in0;
-    const float *d = (const float *)in1, *fs = (const float *)(uintptr_t)aux;
+    const float *d = (const float *)in1;
+    /* fs (an integer argument) as a pointer to global memory: its loads are then global loads,
+     * which a wait can count (a wait for a generic load's result waits for every load in
+     * flight, the weights too) */
+    const __attribute__((address_space(1))) float *fs =
+        (const __attribute__((address_space(1))) float *)(uintptr_t)aux;
     const float *nx = (const float *)in0, *nadd = PAIR ? nullptr : (const float *)in1;
     const int xs = (int)(uint32_t)aux, as = (int)(uint32_t)(aux >> 32);
     const int nb = cols >> 5, nsb = cols >> 8;
