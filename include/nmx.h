@@ -94,8 +94,9 @@ int nmx_q4k_matmul_multi(nmx_ctx *ctx, int count, const void *const *W, const in
 /* ---- Gated DeltaNet recurrence with the speculative rollback log -------------------------
  * Replaces pf_lin_rule / pf_lin_apply (engine/src/ops.h:54-93, matvec_ref.c:140-188,
  * kern_lin.c:155-185) and nm_metal_lin_rule / _apply (engine/metal/metal.h:66-71).
- * S: [heads][dv][dk] fp32 in HBM (column-major per head; the layout is private to this
- * contract, zero = reset). qkv [n][qkv_stride] = q | k (heads/rep heads of dk) | v (heads x dv);
+ * S: heads x dv x dk fp32 in HBM, element (head h, value column j, key i) at
+ * nmx_state_index(h, j, i, dk, dv) below (the layout is private to this contract; zero =
+ * reset). qkv [n][qkv_stride] = q | k (heads/rep heads of dk) | v (heads x dv);
  * decay, beta [n][heads]; o [n][o_stride]. log [n][heads][dk + dv + 1] = k | delta | decay.
  * log == NULL: plain pass, S advances by all n tokens.
  * log != NULL, log0 == 0 (the reference's logged pass): S advances by token 0 only; rows
@@ -105,6 +106,13 @@ int nmx_q4k_matmul_multi(nmx_ctx *ctx, int count, const void *const *W, const in
  * keep > 0: S first advances by the keep rows of pend ([keep][heads][dk + dv + 1]), with the
  *   replay arithmetic (row = row * decay; row = row + k_i * delta_j).
  * dk in {32, 64, 128, 256}; dv <= 1024; n <= 64; keep <= 64. */
+/* The state's layout: per head, the value columns in groups of 16 (one wave of the
+ * recurrence kernels: a quad of lanes per column, lane c holding keys [c dk/4, (c+1) dk/4)),
+ * and within a group of W columns (W = 16, or fewer for the last group) the float4 slot k of
+ * every lane (keys c dk/4 + 4k .. + 3 of column j at lane 4 (j mod 16) + c) contiguous: a
+ * wave's state loads and stores are 16 B per lane over one contiguous 64 x 16 B run. */
+size_t nmx_state_index(int h, int j, int i, int dk, int dv);
+
 typedef struct {
     int n, heads, rep, dk, dv;
     int qkv_stride, o_stride;

@@ -81,6 +81,22 @@ int nmx_mt_matmul(nmx_ctx *ctx, int count, const nmx_mt_seg *segs, int cols, int
 int nmx_head_scratch_init(nmx_ctx *ctx);
 
 /* [a, a + na) and [b, b + nb) overlap (byte ranges). */
+/* The DeltaNet state layout (nmx_state_index): per head, the value columns in groups of 16 (a
+ * wave of the recurrence kernels: lane 4 (j mod 16) + c holds keys [c dk/4, (c+1) dk/4) of
+ * column j), and within a group of W columns the float4 slot k of every lane contiguous. A
+ * lane's keys 4k .. 4k + 3 of its quarter are at state_lane(..) + k state_slot(..). */
+__host__ __device__ inline size_t state_lane(int h, int j, int c, int dk, int dv) {
+    return ((size_t)h * dv + (j & ~15)) * dk + (size_t)(4 * (j & 15) + c) * 4;
+}
+__host__ __device__ inline int state_slot(int j, int dv) {
+    const int w = dv - (j & ~15);
+    return 16 * (w < 16 ? w : 16);
+}
+__host__ __device__ inline size_t state_index(int h, int j, int i, int dk, int dv) {
+    const int dk4 = dk / 4;
+    return state_lane(h, j, i / dk4, dk, dv) + (size_t)((i % dk4) / 4) * state_slot(j, dv) + i % 4;
+}
+
 static inline bool nmx_overlap(const void *a, size_t na, const void *b, size_t nb) {
     const char *pa = (const char *)a, *pb = (const char *)b;
     return na && nb && pa < pb + nb && pb < pa + na;

@@ -16,8 +16,11 @@
  * reference).
  * q and k of the token are staged in LDS (broadcast reads, padded against bank conflicts).
  *
- * State layout in HBM (private to this contract, engine/src/ops.h:74-75): [heads][dv][dk],
- * i.e. column-major per head, so a lane's dk/4 keys are contiguous (128-bit loads).
+ * State layout in HBM (private to this contract, engine/src/ops.h:74-75; nmx_state_index):
+ * per head, the value columns in groups of 16 (one wave's quads), and within a group the
+ * float4 slot k of every lane contiguous, so each 128-bit load or store of a wave covers one
+ * contiguous 1 KB run (a lane's dk/4 keys contiguous instead put 64 lanes on 64 lines per
+ * instruction, and issuing them took about 2 us per workgroup in the mixer).
  * Log rows keep the reference layout [n][heads][dk + dv + 1] = k | delta | decay. */
 #include "nmx_internal.h"
 #include "nmx_a8.h"
@@ -43,11 +46,12 @@ __global__ __launch_bounds__(256) void lin_rule_k(nmx_lin_args a) {
     const size_t logw = (size_t)DK + dv + 1;
     const bool logged = a.log != nullptr;
 
-    float *Sp = a.S + ((size_t)h * dv + jj) * DK + c * DK4;
+    float *Sp = a.S + state_lane(h, jj, c, DK, dv);
+    const int SS = state_slot(jj, dv);
     float s[DK4];
 #pragma unroll
     for (int r = 0; r < DK4; r += 4) {
-        const float4 x = *(const float4 *)(Sp + r);
+        const float4 x = *(const float4 *)(Sp + (r >> 2) * SS);
         s[r] = x.x, s[r + 1] = x.y, s[r + 2] = x.z, s[r + 3] = x.w;
     }
 
@@ -101,7 +105,7 @@ __global__ __launch_bounds__(256) void lin_rule_k(nmx_lin_args a) {
     const bool store_now = (a.n == 0) || (a.log0 && keep > 0);
     if (store_now && live) {
 #pragma unroll
-        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + (r >> 2) * SS) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
     }
 
     for (int t0 = 0; t0 < a.n; t0 += TB) {
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(256) void lin_rule_k(nmx_lin_args a) {
             if (commit && live) {
 #pragma unroll
                 for (int r = 0; r < DK4; r += 4)
-                    *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+                    *(float4 *)(Sp + (r >> 2) * SS) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
             }
         }
     }
@@ -248,6 +252,8 @@ int nmx_lin_rule(nmx_ctx *ctx, const nmx_lin_args *a) {
     if (a->n < 1) return nmx_fail(ctx, "nmx_lin_rule: n=%d (>= 1 needed)", a->n);
     return dispatch(ctx, *a);
 }
+
+size_t nmx_state_index(int h, int j, int i, int dk, int dv) { return state_index(h, j, i, dk, dv); }
 
 int nmx_lin_apply(nmx_ctx *ctx, float *S, const float *log, int keep, int heads, int dk, int dv) {
     if (!ctx) return -1;

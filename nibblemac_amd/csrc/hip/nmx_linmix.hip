@@ -137,11 +137,12 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     }
     if (w_on) wq = *(const float4 *)(a.w + 4 * tid);
     /* recurrence state of the quad's keys */
-    float *Sp = a.S + ((size_t)h * dv + j) * DK + c * DK4;
+    float *Sp = a.S + state_lane(h, j, c, DK, dv);
+    const int SS = state_slot(j, dv); /* a wave's loads: one contiguous 1 KB run each */
     float s[DK4];
 #pragma unroll
     for (int r = 0; r < DK4; r += 4) {
-        const float4 x = *(const float4 *)(Sp + r);
+        const float4 x = *(const float4 *)(Sp + (r >> 2) * SS);
         s[r] = x.x, s[r + 1] = x.y, s[r + 2] = x.z, s[r + 3] = x.w;
     }
 
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     const bool store_now = a.log0 && keep > 0;
     if (store_now) {
 #pragma unroll
-        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+        for (int r = 0; r < DK4; r += 4) *(float4 *)(Sp + (r >> 2) * SS) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
     }
 
     /* ---- recurrence over the tokens (nmx_lin_rule arithmetic) ---- */
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
         if (commit) {
 #pragma unroll
             for (int r = 0; r < DK4; r += 4)
-                *(float4 *)(Sp + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+                *(float4 *)(Sp + (r >> 2) * SS) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
         }
     }
     __syncthreads();

@@ -5,9 +5,9 @@
  * model fingerprint; then per linear layer the conv state [(conv_k-1)][conv_dim] and the
  * recurrent state; per full-attention layer the K rows [n_kv][n_past] then the V rows; then
  * the MTP head's K and V rows), so a state moves between this engine and the reference's.
- * The recurrent state lives on the device as [heads][dv][dk] (a value column's keys
- * contiguous, the layout of the recurrence kernels) and is written to the blob in the
- * reference's [heads][dk][dv] order.
+ * The recurrent state lives on the device in the recurrence kernels' layout
+ * (nmx_state_index: a value column's keys in quarters, tiled so that each wave's loads are
+ * contiguous) and is written to the blob in the reference's [heads][dk][dv] order.
  *
  * The checkpoint keeps a device copy of the conv and recurrent states only, like the
  * reference: KV rows below the checkpoint's n_past are never rewritten while it is valid. */
@@ -112,12 +112,12 @@ static int copy_lin(pinfer_ctx *c, int li, char *cur, int to_blob, float *tmp, c
         for (int h = 0; h < c->lv_heads; h++)
             for (int j = 0; j < dv; j++)
                 for (int i = 0; i < dk; i++)
-                    blob_s[((size_t)h * dk + i) * dv + j] = tmp[((size_t)h * dv + j) * dk + i];
+                    blob_s[((size_t)h * dk + i) * dv + j] = tmp[nmx_state_index(h, j, i, dk, dv)];
     } else {
         for (int h = 0; h < c->lv_heads; h++)
             for (int j = 0; j < dv; j++)
                 for (int i = 0; i < dk; i++)
-                    tmp[((size_t)h * dv + j) * dk + i] = blob_s[((size_t)h * dk + i) * dv + j];
+                    tmp[nmx_state_index(h, j, i, dk, dv)] = blob_s[((size_t)h * dk + i) * dv + j];
         if (nmx_upload(c->dev, conv, cur, cb) || nmx_upload(c->dev, rec, tmp, sb)) return PINFER_E_ARG;
     }
     *next = cur + cb + sb;

@@ -17,7 +17,7 @@
  * engine/src/pinfer.c:196; the state blob copies it, state.c:89-90). Every call therefore
  * stages its inputs to the device and its outputs back, synchronously; that PCIe traffic
  * bounds this integration, while libpinfer.so keeps the whole verify round on the device.
- * The recurrent state has the device kernels' layout [heads][dv][dk] (ops.h:74-75 leaves the
+ * The recurrent state has the device kernels' layout (nmx_state_index; ops.h:74-75 leaves the
  * layout to the implementation), so state blobs of this build hold that layout.
  * Results are bit-identical to the reference's operators (same fp32 roundings, in the same
  * order); the contract has no error return, so a device failure prints the nmx error and

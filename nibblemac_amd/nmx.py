@@ -116,6 +116,7 @@ _SIGS: dict[str, tuple[object, list[object]]] = {
     "nmx_q4k_matmul_multi": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "nmx_lin_rule": (_i, [_vp, ctypes.POINTER(LinArgs)]),
     "nmx_lin_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "nmx_state_index": (_sz, [_i, _i, _i, _i, _i]),
     "nmx_head_work_bytes": (_sz, [_i, _i]),
     "nmx_head_accept": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nmx_head_accept_to": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

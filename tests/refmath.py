@@ -92,3 +92,32 @@ def unpack_q4k(W: np.ndarray, rows: int, cols: int):
     D = D.transpose(0, 2, 1).reshape(rows, nsb)
     M = M.transpose(0, 2, 1).reshape(rows, nsb)
     return u.astype(np.int64), s, m, D, M
+
+
+def state_offsets(heads: int, dk: int, dv: int) -> np.ndarray:
+    """Offsets [h][j][i] of the DeltaNet state element (head h, value column j, key i) in the
+    device layout, restated from its description in include/nmx.h: per head the columns in
+    groups of 16, and within a group of W columns the float4 slot k (keys 4k .. 4k + 3 of a
+    quarter c of dk/4 keys) of every lane 4 (j mod 16) + c contiguous."""
+    dk4 = dk // 4
+    h = np.arange(heads)[:, None, None]
+    j = np.arange(dv)[None, :, None]
+    i = np.arange(dk)[None, None, :]
+    g = j // 16
+    w = np.minimum(16, dv - 16 * g)
+    lane = 4 * (j % 16) + i // dk4
+    k = (i % dk4) // 4
+    return (h * dv + 16 * g) * dk + (k * 4 * w + lane) * 4 + i % 4
+
+
+def state_to_dev(S, heads: int, dk: int, dv: int) -> np.ndarray:
+    """oracle layout [h][dk][dv] -> the device layout (flat)."""
+    out = np.empty(heads * dk * dv, np.float32)
+    out[state_offsets(heads, dk, dv)] = np.asarray(S, np.float32).reshape(heads, dk, dv).transpose(0, 2, 1)
+    return out
+
+
+def state_from_dev(S, heads: int, dk: int, dv: int) -> np.ndarray:
+    """the device layout (flat) -> oracle layout [h][dk][dv]."""
+    flat = np.asarray(S, np.float32).ravel()
+    return np.ascontiguousarray(flat[state_offsets(heads, dk, dv)].transpose(0, 2, 1))

@@ -13,17 +13,18 @@ import pytest
 
 import oracle
 from nibblemac_amd.nmx import NmxError
+from tests.refmath import state_from_dev, state_to_dev
 
 pytestmark = pytest.mark.gpu
 
 
 def to_dev_layout(S, heads, dk, dv):
-    """oracle [h][dk][dv] -> device [h][dv][dk]."""
-    return np.ascontiguousarray(S.reshape(heads, dk, dv).transpose(0, 2, 1))
+    """oracle [h][dk][dv] -> the device layout (include/nmx.h, nmx_state_index)."""
+    return state_to_dev(S, heads, dk, dv)
 
 
 def from_dev_layout(S, heads, dk, dv):
-    return np.ascontiguousarray(S.reshape(heads, dv, dk).transpose(0, 2, 1))
+    return state_from_dev(S, heads, dk, dv)
 
 
 def bits_equal(a, b, what):

@@ -16,6 +16,7 @@ import pytest
 
 import oracle
 from nibblemac_amd.nmx import A8, LinArgs, LinMixArgs, LinPreArgs
+from tests.refmath import state_from_dev
 from tests.test_gpu_q4k import assert_bits_equal
 
 pytestmark = pytest.mark.gpu
@@ -118,8 +119,8 @@ def test_lin_mix_equals_three_kernels(dev, case):
 
 
 def from_dev(S, heads, dk, dv):
-    """device [h][dv][dk] -> oracle [h][dk][dv]"""
-    return np.ascontiguousarray(np.asarray(S).reshape(heads, dv, dk).transpose(0, 2, 1))
+    """the device layout (include/nmx.h, nmx_state_index) -> oracle [h][dk][dv]"""
+    return state_from_dev(S, heads, dk, dv)
 
 
 @pytest.mark.parametrize("e", [1, 2, 3, 4, 5])

@@ -22,6 +22,7 @@ import pytest
 import oracle
 from nibblemac_amd import pqfile
 from oracle import HERE as ORACLE_DIR
+from tests.refmath import state_from_dev, state_to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -69,12 +70,12 @@ def plug():
 
 
 def dev_layout(S, heads, dk, dv):
-    """[h][dk][dv] (oracle) -> [h][dv][dk] (the plug's private layout)."""
-    return np.ascontiguousarray(S.reshape(heads, dk, dv).transpose(0, 2, 1))
+    """[h][dk][dv] (oracle) -> the plug's private layout (the device kernels', nmx_state_index)."""
+    return state_to_dev(S, heads, dk, dv)
 
 
 def from_dev(S, heads, dk, dv):
-    return np.ascontiguousarray(S.reshape(heads, dv, dk).transpose(0, 2, 1))
+    return state_from_dev(S, heads, dk, dv)
 
 
 def lin_inputs(rng, n, heads, rep, dk, dv):
