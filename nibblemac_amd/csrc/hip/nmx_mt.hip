@@ -153,7 +153,9 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     static_assert(!PAIR || (NORM && !SWI), "PAIR is a norm prologue of a plain matmul");
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[(PAIR ? 10 : 5) * MT_MAX_NV];
+    __shared__ __align__(16) int zl[8]; /* 32 zero bytes: the matrix-core dots' off-diagonal rows */
     const int tid = threadIdx.x;
+    if (tid < 8) zl[tid] = 0;
     const int8_t *q = (const int8_t *)in0;
     const float *d = (const float *)in1;
     /* fs (an integer argument) as a pointer to global memory: its loads are then global loads,
@@ -498,6 +500,42 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
     __syncthreads();
 
     /* ---- phase 1: exact int32 dots of the unit ---- */
+    /* The SwiGLU launch (R = 64: a wave's lanes are the 64 rows of one block pair) computes its
+     * dots on the matrix cores, as q4k_head_k does: per block two v_mfma_i32_32x32x32_i8 with
+     * B = the lane's own row's 32 nibbles and A = the block's activation codes of vector v(m)
+     * in the rows m of K group (m / 4) % 2 (zero elsewhere), so every lane receives its own
+     * row's exact int32 dots for all NV vectors (4 matrix instructions per block pair instead
+     * of 16 NV v_dot4). Every lane of the wave runs them (lanes without a unit read unit 0's
+     * bytes and discard the result). */
+    constexpr bool MF = SWI && NV >= 3 && BPU == 2;
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    v16i mfd[MF ? BPU : 1];
+    if constexpr (MF) {
+        const int lane = tid & 63, m = lane & 31, vl = 4 * (m >> 3) + (m & 3);
+        const bool diag = ((m >> 2) & 1) == (lane >> 5) && vl < NV;
+        const int blk0 = u_sb * 8 + u_k0;
+        const v16i zero = {};
+#pragma unroll
+        for (int k = 0; k < BPU; k++) {
+            /* A: entries [8h .. 8h + 3 | 16 + 8h .. | 8h + 4 .. | 16 + 8h + 4 ..] of half h,
+             * matching the nibble order of B below */
+            const int8_t *xb = diag ? aq + aq_off(blk0 + k, NV) + vl * 32 : (const int8_t *)zl;
+            const uint2 ta0 = *(const uint2 *)xb, tb0 = *(const uint2 *)(xb + 16);
+            const uint2 ta1 = *(const uint2 *)(xb + 8), tb1 = *(const uint2 *)(xb + 24);
+            const v4i x0 = {(int)ta0.x, (int)tb0.x, (int)ta0.y, (int)tb0.y};
+            const v4i x1 = {(int)ta1.x, (int)tb1.x, (int)ta1.y, (int)tb1.y};
+            /* B: the low nibbles of code bytes 4u .. 4u + 3 are columns 4u .., the high ones
+             * columns 16 + 4u .. */
+            const uint4 w = c[k];
+            const v4i b0 = {(int)(w.x & 0x0f0f0f0fu), (int)((w.x >> 4) & 0x0f0f0f0fu),
+                            (int)(w.y & 0x0f0f0f0fu), (int)((w.y >> 4) & 0x0f0f0f0fu)};
+            const v4i b1 = {(int)(w.z & 0x0f0f0f0fu), (int)((w.z >> 4) & 0x0f0f0f0fu),
+                            (int)(w.w & 0x0f0f0f0fu), (int)((w.w >> 4) & 0x0f0f0f0fu)};
+            mfd[k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, b0, zero, 0, 0, 0);
+            mfd[k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, b1, mfd[k], 0, 0, 0);
+        }
+    }
     if (has_unit) {
         const int sh8 = 8 * ti;
         const uint32_t dw = (ti & 2) ? a0.y : a0.x, mw = (ti & 2) ? a0.w : a0.z;
@@ -523,16 +561,18 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
 #pragma unroll
             for (int i = 0; i < BPU * NV; i++) sdv[i] = ad[blk0 * NV + i], sfv[i] = afs[blk0 * NV + i];
         }
-        int4 xa[NV][2], xn[NV][2];
+        int4 xa[MF ? 1 : NV][2], xn[MF ? 1 : NV][2];
+        if constexpr (!MF) {
 #pragma unroll
-        for (int v = 0; v < NV; v++) {
-            const int8_t *xb = aq + aq_off(blk0, NV) + v * 32;
-            xa[v][0] = *(const int4 *)xb, xa[v][1] = *(const int4 *)(xb + 16);
+            for (int v = 0; v < NV; v++) {
+                const int8_t *xb = aq + aq_off(blk0, NV) + v * 32;
+                xa[v][0] = *(const int4 *)xb, xa[v][1] = *(const int4 *)(xb + 16);
+            }
         }
 #pragma unroll
         for (int k = 0; k < BPU; k++) {
             const int blk = blk0 + k;
-            if (k < BPU - 1) {
+            if (!MF && k < BPU - 1) {
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
                     const int8_t *xb = aq + aq_off(blk + 1, NV) + v * 32;
@@ -546,9 +586,15 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
             const int lo1 = (int)(c[k].y & 0x0f0f0f0fu), hi1 = (int)((c[k].y >> 4) & 0x0f0f0f0fu);
             const int lo2 = (int)(c[k].z & 0x0f0f0f0fu), hi2 = (int)((c[k].z >> 4) & 0x0f0f0f0fu);
             const int lo3 = (int)(c[k].w & 0x0f0f0f0fu), hi3 = (int)((c[k].w >> 4) & 0x0f0f0f0fu);
+            if constexpr (MF) {
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    lp[(v * R + u_r) * (nb | 1) + blk] = make_float2((float)mfd[k][v], sc * sdv[k * NV + v]);
+                continue;
+            }
 #pragma unroll
             for (int v = 0; v < NV; v++) {
-                const int4 x0 = xa[v][0], x1 = xa[v][1];
+                const int4 x0 = xa[MF ? 0 : v][0], x1 = xa[MF ? 0 : v][1];
                 int dot = __builtin_amdgcn_sdot4(lo0, x0.x, 0, false);
                 dot = __builtin_amdgcn_sdot4(lo1, x0.y, dot, false);
                 dot = __builtin_amdgcn_sdot4(lo2, x0.z, dot, false);
@@ -566,7 +612,7 @@ __global__ __launch_bounds__(BPU < 4 ? 1024 : NORM ? MT_NORM_THREADS : SWI ? MT_
             }
             if (k < BPU - 1) {
 #pragma unroll
-                for (int v = 0; v < NV; v++) xa[v][0] = xn[v][0], xa[v][1] = xn[v][1];
+                for (int v = 0; v < (MF ? 1 : NV); v++) xa[v][0] = xn[v][0], xa[v][1] = xn[v][1];
             }
         }
     }
