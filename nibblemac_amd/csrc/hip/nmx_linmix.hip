@@ -69,6 +69,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     __shared__ float red[8 * 64];
     __shared__ float spdec[MIX_TB]; /* decays of the pending batch (red serves the L2 norms) */
     __shared__ uint64_t sx2[32];    /* the gate exp's 2^(i/32) table */
+    __shared__ float sgh[2];        /* the head's A (or A_log) and dt_bias */
     constexpr int DK = DK4 * 4, PAD = DK4 + 4, ROW = 4 * PAD;
     const int n = n_, dv = dv_, heads = a.heads;
     const int h = blockIdx.x, tid = threadIdx.x, T = 4 * dv, c = tid & 3; /* the launch's size */
@@ -164,6 +165,7 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
     if (z_on) *(float4 *)(sz + 4 * tid) = zq;
     if (w_on) *(float4 *)(sw + 4 * tid) = wq;
     if (tid < 32) sx2[tid] = x2v;
+    if (gy == 0) sgh[0] = gA, sgh[1] = gdt;
     __syncthreads();
 
     /* ---- conv + SiLU of the head's channels: q (dk), k (dk), v (dv), one per thread ---- */
@@ -209,22 +211,27 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
         }
     }
     /* meanwhile the last wave computes the gates, beta = sigmoid(b) and
-     * decay = exp(A softplus(a + dt_bias)) with A = -exp(A_log) */
+     * decay = exp(A softplus(a + dt_bias)) with A = -exp(A_log): each lane's first item from
+     * the values requested at entry (the head's A and dt_bias through LDS, since a value
+     * the compiler requests again here would be waited for behind the wave's recurrence
+     * state), items past the wave (2 n > 64) in a loop of their own, whose loads would
+     * otherwise make the first item's waits wait for every request in flight */
+    auto gate = [&](int x, float g, float Ai, float dt) {
+        if (x < n) {
+            const float A = a.A ? Ai : -nmx_gate_expf_t(Ai, sx2);
+            float sp_ = g + dt;
+            sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf_t(sp_, sx2));
+            sdec[x] = nmx_gate_expf_t(A * sp_, sx2);
+        } else {
+            sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf_t(-g, sx2));
+        }
+    };
+    if (gy >= 0 && gy < 2 * n) gate(gy, ga, sgh[0], sgh[1]);
     if (gy >= 0) {
-        for (int x = gy; x < 2 * n; x += 64) {
-            const bool first = x == gy;
-            if (x < n) {
-                const float av = first ? ga : a_in[(size_t)x * g_stride + h];
-                const float Ai = first ? gA : a.A ? a.A[h] : a.A_log[h];
-                const float dt = first ? gdt : a.dt_bias[h];
-                const float A = a.A ? Ai : -nmx_gate_expf_t(Ai, sx2);
-                float sp_ = av + dt;
-                sp_ = sp_ > 20.0f ? sp_ : nmx_gate_log1pf(nmx_gate_expf_t(sp_, sx2));
-                sdec[x] = nmx_gate_expf_t(A * sp_, sx2);
-            } else {
-                const float b = first ? ga : b_in[(size_t)(x - n) * g_stride + h];
-                sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf_t(-b, sx2));
-            }
+        for (int x = gy + 64; x < 2 * n; x += 64) {
+            const float g =
+                x < n ? a_in[(size_t)x * g_stride + h] : b_in[(size_t)(x - n) * g_stride + h];
+            gate(x, g, sgh[0], sgh[1]);
         }
     }
     __syncthreads();
