@@ -997,12 +997,26 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
         bs[u] = p < np ? srow[p] : 0.0f;
     }
     const int rows0 = np < PV_PT ? np : PV_PT;
-    float4 vb[PV_PER];
+    /* the first tile in two halves of PV_HA rows: the first half's values in every thread
+     * (element f = u 256 + tid), the second half's in waves 1-3 only (f = u 192 + tid - 64),
+     * which store its products while wave 0 runs the first half's chains */
+    constexpr int PV_UA = PV_PER / 2, PV_HA = PV_UA * 256 / F4, PV_UB = PV_UA * 256 / 192;
+    static_assert(PV_PER % 2 == 0 && PV_UA * 256 % 192 == 0 && PV_HA % 4 == 0,
+                  "halves of whole rows, the second 16-byte aligned in LDS");
+    float4 va[PV_UA], vbh[PV_UB];
 #pragma unroll
-    for (int u = 0; u < PV_PER; u++) {
+    for (int u = 0; u < PV_UA; u++) {
         const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
-        vb[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < rows0) vb[u] = kv_load4<KVT>(vc, R0 + r, hd, d0 + 4 * c4, vsc);
+        va[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < rows0) va[u] = kv_load4<KVT>(vc, R0 + r, hd, d0 + 4 * c4, vsc);
+    }
+    if (tid >= 64) {
+#pragma unroll
+        for (int u = 0; u < PV_UB; u++) {
+            const int f = u * 192 + tid - 64, r = PV_HA + f / F4, c4 = f % F4;
+            vbh[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (r < rows0) vbh[u] = kv_load4<KVT>(vc, R0 + r, hd, d0 + 4 * c4, vsc);
+        }
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -1045,13 +1059,27 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
         q[3 * PV_RS] = w * v.w;
     };
     float o = 0.0f;
+    /* every thread stores the first half's products; then wave 0's chain lanes add them while
+     * waves 1-3 store the second half's (whose values may still be arriving); the chains go on
+     * over the second half and the later tiles, each adding the positions in order */
+    const int hA = rows0 < PV_HA ? rows0 : PV_HA;
 #pragma unroll
-    for (int u = 0; u < PV_PER; u++) {
+    for (int u = 0; u < PV_UA; u++) {
         const int f = u * 256 + tid, r = f / F4, c4 = f - r * F4;
-        if (r < rows0) put(r, c4, ecm[pv_cm(r, m4, s4)] * inv, vb[u]);
+        if (r < rows0) put(r, c4, ecm[pv_cm(r, m4, s4)] * inv, va[u]);
     }
     __syncthreads();
-    for (int base = 0, rows = rows0; base < np;) {
+    if (tid < PV_DS) {
+        o = pv_chain4(o, vt + tid * PV_RS, hA);
+    } else if (tid >= 64) {
+#pragma unroll
+        for (int u = 0; u < PV_UB; u++) {
+            const int f = u * 192 + tid - 64, r = PV_HA + f / F4, c4 = f % F4;
+            if (r < rows0) put(r, c4, ecm[pv_cm(r, m4, s4)] * inv, vbh[u]);
+        }
+    }
+    __syncthreads();
+    for (int base = hA, rows = rows0 - hA, voff = hA; base < np;) {
         const int next = base + rows, rows2 = np - next < PV_PT2 ? np - next : PV_PT2;
         float4 nb[PV_PER2];
         if (tid >= 64 && next < np) { /* waves 1-3: the next tile, during wave 0's chains */
@@ -1063,7 +1091,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
                 if (r < rows2) nb[u] = kv_load4<KVT>(vc, R0 + next + r, hd, d0 + 4 * c4, vsc);
             }
         }
-        if (tid < PV_DS) o = pv_chain4(o, vt + tid * PV_RS, rows);
+        if (tid < PV_DS) o = pv_chain4(o, vt + tid * PV_RS + voff, rows);
         __syncthreads(); /* the chains of this tile are done */
         if (next >= np) break;
         if (tid >= 64) {
@@ -1075,7 +1103,7 @@ __global__ __launch_bounds__(256) void attn_pv_k(const float *__restrict__ sc,
             }
         }
         __syncthreads();
-        base = next, rows = rows2;
+        base = next, rows = rows2, voff = 0;
     }
     if (tid < PV_DS) {
         o = o * nmx_sigmoid(gate);
