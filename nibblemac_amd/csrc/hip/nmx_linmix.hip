@@ -374,10 +374,34 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
             nmx_a8_store(yv, a.aq + u * 32, a.ad + u, a.afs + u);
         }
     };
+    /* items x and x + T together where both exist (the boundary n0 dv is a multiple of 32,
+     * so each half-wave takes one branch): their chains interleave, where the threads with
+     * two items ran them one after the other and ended the launch last */
+    auto out2 = [&](int x1, float z1, int x2, float z2) {
+        const int t1 = x1 / dv, j1 = x1 - t1 * dv, t2 = x2 / dv, j2 = x2 - t2 * dv;
+        const float g1 = nmx_silu(z1), g2 = nmx_silu(z2);
+        float y1 = (so[t1 * dv + j1] * srn[2 * n + t1]) * sw[j1];
+        float y2 = (so[t2 * dv + j2] * srn[2 * n + t2]) * sw[j2];
+        y1 = y1 * g1;
+        y2 = y2 * g2;
+        const int c1 = h * dv + j1, c2 = h * dv + j2;
+        if (a.y) {
+            a.y[(size_t)t1 * a.y_stride + c1] = y1;
+            a.y[(size_t)t2 * a.y_stride + c2] = y2;
+        }
+        if (a.aq) {
+            const size_t u1 = (size_t)(c1 >> 5) * n + t1, u2 = (size_t)(c2 >> 5) * n + t2;
+            nmx_a8_store2(y1, a.aq + u1 * 32, a.ad + u1, a.afs + u1, y2, a.aq + u2 * 32,
+                          a.ad + u2, a.afs + u2);
+        }
+    };
     /* z of the first n0 tokens from LDS, of later ones from memory, in two loops: one load
      * through a pointer that may be either is a generic load, and a wait for it waits for every
      * memory operation in flight, the state and log stores included */
-    for (int x = tid; x < n0 * dv; x += T) out(x, sz[x]);
+    for (int x = tid; x < n0 * dv; x += 2 * T) {
+        if (x + T < n0 * dv) out2(x, sz[x], x + T, sz[x + T]);
+        else out(x, sz[x]);
+    }
     for (int x = n0 * dv + tid; x < n * dv; x += T) {
         const int t = x / dv, jj = x - t * dv;
         out(x, z_in[(size_t)t * z_stride + h * dv + jj]);
