@@ -226,7 +226,26 @@ __global__ __launch_bounds__(MIX_MAX_THREADS) void lin_mix_k(
             sbet[x - n] = 1.0f / (1.0f + nmx_gate_expf_t(-g, sx2));
         }
     };
-    if (gy >= 0 && gy < 2 * n) gate(gy, ga, sgh[0], sgh[1]);
+    if (gy >= 0 && 2 * n <= 63) {
+        /* (the whole gate wave) each lane's first exponential in one call: exp(a + dt) in the
+         * decay lanes, exp(-b) in the beta lanes and exp(A_log) in lane 63, which has no item;
+         * then the betas' divide and the decays' log1p and last exponential. The decay chain
+         * is two exponentials long instead of three, and the betas' exponential no longer runs
+         * after it */
+        const bool dl = gy < n, bl = gy >= n && gy < 2 * n;
+        const float spv = ga + sgh[1];
+        const float e1 = nmx_gate_expf_t(gy == 63 ? sgh[0] : dl ? spv : -ga, sx2);
+        const float A =
+            a.A ? sgh[0] : -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e1), 63));
+        if (dl) {
+            const float sp_ = spv > 20.0f ? spv : nmx_gate_log1pf(e1);
+            sdec[gy] = nmx_gate_expf_t(A * sp_, sx2);
+        } else if (bl) {
+            sbet[gy - n] = 1.0f / (1.0f + e1);
+        }
+    } else if (gy >= 0 && gy < 2 * n) {
+        gate(gy, ga, sgh[0], sgh[1]);
+    }
     if (gy >= 0) {
         for (int x = gy + 64; x < 2 * n; x += 64) {
             const float g =
